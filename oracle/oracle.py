@@ -1,0 +1,339 @@
+"""Python face of the CPU parity oracle (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg
+may import this module, and only to check (or time, as the CPU baseline) the
+HIP path -- never as the product path.
+
+Contents:
+  * ctypes bindings to ``liboracle.so`` (the C restatement in
+    ``attn_oracle.c`` of vantablack's ``forward.cpuAttention``
+    (src/runtime/forward.zig:187-228), ``prefill.attentionCausal``
+    (src/runtime/prefill.zig:237-287), ``math.softmax`` (src/kernels/math.zig:
+    136-150), the KvCache layout (src/runtime/kv_cache.zig) and the pool
+    (src/runtime/pool.zig));
+  * the portable seeded input generator (SplitMix64 -> f64 Box-Muller -> f32
+    -> KV dtype) used for every parity input;
+  * exact dtype helpers (f32 -> f16/bf16 round-to-nearest-even, and the exact
+    upcasts of src/kernels/simd.zig:123-126 and forward.zig:661-666).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+NO_WINDOW = (1 << 64) - 1  # maxInt(usize): sliding window disabled (model.zig:59-62)
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with oracle/Makefile (gcc only)."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-B" if force else "-s", "-C", _HERE, "liboracle.so"],
+                       check=True, stdout=subprocess.DEVNULL)
+    return _LIB_PATH
+
+
+class KvCacheC(ctypes.Structure):
+    _fields_ = [("n_layers", ctypes.c_size_t), ("n_kv_heads", ctypes.c_size_t),
+                ("head_dim", ctypes.c_size_t), ("max_seq", ctypes.c_size_t),
+                ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("pos", ctypes.c_size_t)]
+
+
+class ConfigC(ctypes.Structure):
+    _fields_ = [("n_heads", ctypes.c_size_t), ("n_kv_heads", ctypes.c_size_t),
+                ("head_dim", ctypes.c_size_t), ("max_seq", ctypes.c_size_t),
+                ("sliding_window", ctypes.c_size_t)]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P, S, F = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float
+        L.vtb_oracle_softmax.argtypes = [P, S]
+        L.vtb_oracle_argmax.argtypes = [P, S]
+        L.vtb_oracle_argmax.restype = S
+        L.vtb_oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.vtb_oracle_f16_to_f32.restype = F
+        L.vtb_oracle_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        L.vtb_oracle_bf16_to_f32.restype = F
+        L.vtb_oracle_upcast_f16.argtypes = [P, P, S]
+        L.vtb_oracle_upcast_bf16.argtypes = [P, P, S]
+        L.vtb_oracle_kv_slot_offset.argtypes = [P, S]
+        L.vtb_oracle_kv_slot_offset.restype = S
+        L.vtb_oracle_kv_layer_offset.argtypes = [P, S]
+        L.vtb_oracle_kv_layer_offset.restype = S
+        L.vtb_oracle_kv_advance.argtypes = [P]
+        L.vtb_oracle_kv_shrink_to_fit.argtypes = [P, S]
+        L.vtb_oracle_window_start.argtypes = [S, S]
+        L.vtb_oracle_window_start.restype = S
+        L.vtb_oracle_cpu_attention.argtypes = [P, P, P, S, P, P]
+        L.vtb_oracle_attention_causal.argtypes = [P, P, P, S, S, P, P]
+        L.vtb_oracle_attention_f64.argtypes = [P, P, P, S, S, P]
+        L.vtb_oracle_pool_init.argtypes = [S, S]
+        L.vtb_oracle_pool_init.restype = P
+        L.vtb_oracle_pool_deinit.argtypes = [P]
+        L.vtb_oracle_pool_workers.argtypes = [P]
+        L.vtb_oracle_pool_workers.restype = S
+        L.vtb_oracle_pool_set_active.argtypes = [P, S]
+        L.vtb_oracle_pool_sum.argtypes = [P, P, S]
+        L.vtb_oracle_pool_sum.restype = ctypes.c_uint64
+        L.vtb_oracle_cpu_attention_pooled.argtypes = [P, P, P, P, S, S, P, P]
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+# ---------------------------------------------------------------------------
+# Portable seeded RNG: SplitMix64 (counter-based) -> f64 Box-Muller -> f32.
+# ---------------------------------------------------------------------------
+_GAMMA = np.uint64(0x9E3779B97F4A7C15)
+_M1 = np.uint64(0xBF58476D1CE4E5B9)
+_M2 = np.uint64(0x94D049BB133111EB)
+
+
+def splitmix64(seed: int, idx: np.ndarray) -> np.ndarray:
+    """Value number ``idx`` of the SplitMix64 stream started at ``seed``."""
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed & 0xFFFFFFFFFFFFFFFF) + (idx.astype(np.uint64) + np.uint64(1)) * _GAMMA
+        z = (z ^ (z >> np.uint64(30))) * _M1
+        z = (z ^ (z >> np.uint64(27))) * _M2
+        return z ^ (z >> np.uint64(31))
+
+
+def normal(seed: int, n: int, offset: int = 0) -> np.ndarray:
+    """n standard normals (f64 Box-Muller, one normal per pair of draws),
+    returned as f32.  Element i depends only on (seed, offset + i)."""
+    i = np.arange(offset, offset + n, dtype=np.uint64)
+    a = splitmix64(seed, np.uint64(2) * i)
+    b = splitmix64(seed, np.uint64(2) * i + np.uint64(1))
+    u1 = ((a >> np.uint64(11)).astype(np.float64) + 1.0) * (1.0 / 9007199254740992.0)
+    u2 = (b >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+    z = np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
+    return z.astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# dtype helpers
+# ---------------------------------------------------------------------------
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round f32 to bf16 (round-to-nearest-even; NaN stays a quiet NaN)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+    r = np.where(nan, ((u >> np.uint32(16)) | np.uint32(0x40)).astype(np.uint16), r)
+    return r.astype(np.uint16)
+
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    """Round f32 to IEEE binary16 (numpy's cast is round-to-nearest-even)."""
+    return np.ascontiguousarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    """simd.zig:123-126, via the C restatement."""
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, np.float32)
+    lib().vtb_oracle_upcast_bf16(_ptr(bits), _ptr(out), bits.size)
+    return out
+
+
+def f16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    """forward.zig:661-666 (@floatCast f16 -> f32), via the C restatement."""
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, np.float32)
+    lib().vtb_oracle_upcast_f16(_ptr(bits), _ptr(out), bits.size)
+    return out
+
+
+def to_dtype(x: np.ndarray, dtype: str):
+    """Round f32 values to the storage dtype.  Returns (storage, exact_f32):
+    storage is what the GPU holds (float32 or uint16 bit patterns) and
+    exact_f32 is its exact upcast, the oracle's input."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if dtype == "f32":
+        return x, x
+    if dtype == "f16":
+        b = f32_to_f16_bits(x)
+        return b, f16_bits_to_f32(b)
+    if dtype == "bf16":
+        b = f32_to_bf16_bits(x)
+        return b, bf16_bits_to_f32(b)
+    raise ValueError(dtype)
+
+
+# ---------------------------------------------------------------------------
+# Oracle calls
+# ---------------------------------------------------------------------------
+def softmax(x: np.ndarray) -> np.ndarray:
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    lib().vtb_oracle_softmax(_ptr(y), y.size)
+    return y
+
+
+def argmax(x: np.ndarray) -> int:
+    y = np.ascontiguousarray(x, dtype=np.float32)
+    return int(lib().vtb_oracle_argmax(_ptr(y), y.size))
+
+
+def window_start(pos: int, sliding_window: int = NO_WINDOW) -> int:
+    return int(lib().vtb_oracle_window_start(pos, sliding_window))
+
+
+class OracleKvCache:
+    """kv_cache.zig:20-196 over numpy f32 storage (the oracle's view)."""
+
+    def __init__(self, n_layers, n_kv_heads, head_dim, max_seq):
+        total = n_layers * max_seq * n_kv_heads * head_dim
+        self.k = np.zeros(total, np.float32)
+        self.v = np.zeros(total, np.float32)
+        self.c = KvCacheC(n_layers, n_kv_heads, head_dim, max_seq, _ptr(self.k), _ptr(self.v), 0)
+
+    @property
+    def pos(self):
+        return self.c.pos
+
+    @pos.setter
+    def pos(self, p):
+        self.c.pos = p
+
+    @property
+    def max_seq(self):
+        return self.c.max_seq
+
+    @property
+    def row(self):
+        return self.c.n_kv_heads * self.c.head_dim
+
+    def key_slot(self, layer):
+        off = lib().vtb_oracle_kv_slot_offset(ctypes.byref(self.c), layer)
+        if off == NO_WINDOW:
+            raise IndexError("slot out of range")
+        return self.k[off:off + self.row]
+
+    def value_slot(self, layer):
+        off = lib().vtb_oracle_kv_slot_offset(ctypes.byref(self.c), layer)
+        if off == NO_WINDOW:
+            raise IndexError("slot out of range")
+        return self.v[off:off + self.row]
+
+    def keys_for(self, layer, n_tokens):
+        off = lib().vtb_oracle_kv_layer_offset(ctypes.byref(self.c), layer)
+        return self.k[off:off + n_tokens * self.row]
+
+    def values_for(self, layer, n_tokens):
+        off = lib().vtb_oracle_kv_layer_offset(ctypes.byref(self.c), layer)
+        return self.v[off:off + n_tokens * self.row]
+
+    def layer_rows(self, which, layer):
+        """[max_seq, n_kv, head_dim] view of one layer of K or V."""
+        arr = self.k if which == "k" else self.v
+        n = self.c.max_seq * self.row
+        off = layer * n
+        return arr[off:off + n].reshape(self.c.max_seq, self.c.n_kv_heads, self.c.head_dim)
+
+    def advance(self):
+        if lib().vtb_oracle_kv_advance(ctypes.byref(self.c)) != 0:
+            raise IndexError("KvCacheFull")
+
+    def shrink_to_fit(self, new_max_seq):
+        rc = lib().vtb_oracle_kv_shrink_to_fit(ctypes.byref(self.c), new_max_seq)
+        if rc == 4:
+            raise ValueError("NewMaxSeqBelowPos")
+
+
+def config(n_heads, n_kv_heads, head_dim, max_seq, sliding_window=NO_WINDOW) -> ConfigC:
+    return ConfigC(n_heads, n_kv_heads, head_dim, max_seq, sliding_window)
+
+
+def cpu_attention(q: np.ndarray, cache: OracleKvCache, c: ConfigC, layer: int) -> np.ndarray:
+    """forward.zig:187-228 for the query at cache.pos."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    scores = np.zeros(c.n_heads * c.max_seq, np.float32)
+    out = np.zeros(c.n_heads * c.head_dim, np.float32)
+    rc = lib().vtb_oracle_cpu_attention(_ptr(q), ctypes.byref(cache.c), ctypes.byref(c),
+                                        layer, _ptr(scores), _ptr(out))
+    if rc != 0:
+        raise IndexError("cpu_attention: layer or pos out of range")
+    return out
+
+
+def attention_causal(q_all: np.ndarray, cache: OracleKvCache, c: ConfigC, layer: int,
+                     rows) -> np.ndarray:
+    """prefill.zig:237-287 for the listed batch positions b (query at
+    cache.pos + b).  Returns [len(rows), n_heads*head_dim]."""
+    q_all = np.ascontiguousarray(q_all, dtype=np.float32)
+    qd = c.n_heads * c.head_dim
+    B = q_all.size // qd
+    scores = np.zeros(c.n_heads * c.max_seq, np.float32)
+    full = np.zeros(B * qd, np.float32)
+    for b in rows:
+        rc = lib().vtb_oracle_attention_causal(_ptr(q_all), ctypes.byref(cache.c), ctypes.byref(c),
+                                               layer, int(b), _ptr(scores), _ptr(full))
+        if rc != 0:
+            raise IndexError("attention_causal: out of range")
+    return full.reshape(B, qd)[np.asarray(list(rows), dtype=np.int64)]
+
+
+def attention_f64(q: np.ndarray, cache: OracleKvCache, c: ConfigC, layer: int, cur_pos: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    out = np.zeros(c.n_heads * c.head_dim, np.float64)
+    rc = lib().vtb_oracle_attention_f64(_ptr(q), ctypes.byref(cache.c), ctypes.byref(c),
+                                        layer, cur_pos, _ptr(out))
+    if rc != 0:
+        raise IndexError("attention_f64: out of range")
+    return out
+
+
+class Pool:
+    """pool.zig ThreadPool restatement (CPU baseline only)."""
+
+    def __init__(self, requested: int = 0):
+        self.h = lib().vtb_oracle_pool_init(requested, os.cpu_count() or 1)
+
+    @property
+    def workers(self):
+        return int(lib().vtb_oracle_pool_workers(self.h))
+
+    def set_active(self, n):
+        lib().vtb_oracle_pool_set_active(self.h, n)
+
+    def sum(self, a: np.ndarray) -> int:
+        a = np.ascontiguousarray(a, dtype=np.uint32)
+        return int(lib().vtb_oracle_pool_sum(self.h, _ptr(a), a.size))
+
+    def attention(self, q, cache: OracleKvCache, c: ConfigC, layer: int, cur_pos: int, scores=None, out=None):
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        if scores is None:
+            scores = np.zeros(c.n_heads * c.max_seq, np.float32)
+        if out is None:
+            out = np.zeros(c.n_heads * c.head_dim, np.float32)
+        rc = lib().vtb_oracle_cpu_attention_pooled(self.h, _ptr(q), ctypes.byref(cache.c), ctypes.byref(c),
+                                                   layer, cur_pos, _ptr(scores), _ptr(out))
+        if rc != 0:
+            raise IndexError("pooled attention: out of range")
+        return out
+
+    def close(self):
+        if self.h:
+            lib().vtb_oracle_pool_deinit(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
