@@ -1,0 +1,246 @@
+"""Benchmark of the KV-cache attention path on one MI355X.
+
+Headline (BASELINE.json metric "decode attn HBM GB/s (% of peak) @ctx 8K"):
+Llama-2-7B-shaped full-stack decode (config C2 shapes) at context 8K -- 32
+layers x 32 q heads x 32 KV heads x head_dim 128, f16 KV cache already
+holding 8192 rows.  One step = one decoded token: for each of the 32 layers,
+append the token's K/V row (f32 -> f16) and run decode attention over all
+rows so far; the cache grows by one row per step.
+
+  value    = algorithmic bytes of all attention launches in the timed steps
+             / wall time of those steps (appends and launch gaps included);
+  roofline = the decode kernel alone: algorithmic bytes per launch / its
+             average launch duration from HIP events on the kernel's stream.
+Algorithmic bytes per (layer, step) = 2*L*n_kv*d*sizeof(kv) + n_heads*d*(4+4).
+
+Secondary (metric "prefill attn TFLOP/s (% MFMA peak)"): Llama-3-8B causal
+prefill (config C4) at 8192 tokens, bf16, FLOPs = 4*n_heads*d*L(L+1)/2.
+
+cpu_baseline: the CPU oracle (a C restatement of vantablack's cpuAttention,
+oracle/attn_oracle.c) on a bounded sample of the same decode workload, on
+the host's cores, once faithfully single-threaded (as vantablack runs
+attention) and once split over heads on a pool.zig-style pool.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ctx 8192]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode attn HBM GB/s (% of peak) @ctx 8K; prefill attn TFLOP/s (% MFMA peak)"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def decode_bytes(L, n_heads, n_kv, d, kv_bytes):
+    return 2 * L * n_kv * d * kv_bytes + n_heads * d * 8
+
+
+def bench_decode(ctx, torch, args):
+    import numpy as np
+    import vantablack_amd as vb
+
+    n_layers, n_heads, n_kv, d = 32, 32, 32, 128
+    L0 = args.ctx
+    total_steps = args.warmup + args.steps
+    max_seq = L0 + total_steps
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.ExternalStream(ctx.stream)
+    # Layer-major cache [n_layers][max_seq][n_kv][d], f16, rows [0, L0) filled.
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    log(f"bench: allocating f16 KV cache {2 * n_layers * max_seq * n_kv * d * 2 / 2**30:.2f} GiB")
+    kc = torch.empty((n_layers, max_seq, n_kv, d), dtype=torch.float16, device=dev)
+    vc = torch.empty_like(kc)
+    kc.normal_(generator=g)
+    vc.normal_(generator=g)
+    q = (torch.randn((n_layers, n_heads * d), generator=g, device=dev) / np.sqrt(d)).contiguous()
+    kcur = torch.randn((n_layers, total_steps, n_kv * d), generator=g, device=dev)
+    vcur = torch.randn((n_layers, total_steps, n_kv * d), generator=g, device=dev)
+    out = torch.empty((n_layers, n_heads * d), device=dev)
+    torch.cuda.synchronize()
+
+    kb, vbuf = ctx.wrap_tensor(kc), ctx.wrap_tensor(vc)
+    kcb, vcb = ctx.wrap_tensor(kcur), ctx.wrap_tensor(vcur)
+    row_bytes = n_kv * d * 2
+    layer_bytes = max_seq * row_bytes
+    inv = 1.0 / np.sqrt(d)
+    kvrow_f32 = n_kv * d * 4
+
+    # Each layer reads its own q row and writes its own output row.
+    qbs = [ctx.wrap_tensor(q[l]) for l in range(n_layers)]
+    obs = [ctx.wrap_tensor(out[l]) for l in range(n_layers)]
+
+    def step_layers(seg, s, events=None):
+        pos = L0 + s
+        for l in range(n_layers):
+            slot = l * layer_bytes + pos * row_bytes
+            src_off = (l * total_steps + s) * kvrow_f32
+            seg.kv_append(kb, slot, vb.F16, kcb, src_off, n_kv * d)
+            seg.kv_append(vbuf, slot, vb.F16, vcb, src_off, n_kv * d)
+            if events is not None:
+                events[s][l][0].record(stream)
+            seg.attn_decode(obs[l], qbs[l], kb, l * layer_bytes, vbuf, l * layer_bytes, n_heads, n_kv, d,
+                            pos + 1, inv, vb.F16)
+            if events is not None:
+                events[s][l][1].record(stream)
+
+    with ctx.segment() as seg:
+        for s in range(args.warmup):
+            step_layers(seg, s)
+    ctx.wait_idle()
+    torch.cuda.synchronize()
+
+    t0 = time.perf_counter()
+    with ctx.segment() as seg:
+        for s in range(args.warmup, total_steps):
+            step_layers(seg, s)
+    ctx.wait_idle()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    alg = sum(n_layers * decode_bytes(L0 + s + 1, n_heads, n_kv, d, 2) for s in range(args.warmup, total_steps))
+    value_gbs = alg / wall / 1e9
+
+    # Kernel-only timing: the same launches bracketed by HIP events on the
+    # context stream (the stream the kernel runs on).
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n_layers)] for _ in range(args.steps)]
+    # Attention only, at the same lengths as the timed steps.
+    with ctx.segment() as seg:
+        for s in range(args.steps):
+            pos = L0 + args.warmup + s
+            for l in range(n_layers):
+                ev[s][l][0].record(stream)
+                seg.attn_decode(obs[l], qbs[l], kb, l * layer_bytes, vbuf, l * layer_bytes, n_heads, n_kv, d,
+                                pos + 1, inv, vb.F16)
+                ev[s][l][1].record(stream)
+    ctx.wait_idle()
+    torch.cuda.synchronize()
+    durs = [ev[s][l][0].elapsed_time(ev[s][l][1]) * 1e-3 for s in range(args.steps) for l in range(n_layers)]
+    avg_launch = sum(durs) / len(durs)
+    L_mid = L0 + args.warmup + (args.steps + 1) // 2
+    per_launch = sum(decode_bytes(L0 + args.warmup + s + 1, n_heads, n_kv, d, 2)
+                     for s in range(args.steps)) / args.steps
+    achieved = per_launch / avg_launch / 1e9
+    log(f"decode: wall {wall * 1e3:.2f} ms for {args.steps} steps, {value_gbs:.1f} GB/s whole-step; "
+        f"kernel avg {avg_launch * 1e6:.2f} us/launch -> {achieved:.1f} GB/s")
+    for b in qbs + obs + [kb, vbuf, kcb, vcb]:
+        b.release()
+    del kc, vc
+    torch.cuda.empty_cache()
+    return {
+        "value": value_gbs, "ms_per_step": wall * 1e3 / args.steps, "avg_launch_s": avg_launch,
+        "bytes_per_launch": per_launch, "achieved_gbs": achieved, "L_mid": L_mid,
+    }
+
+
+def cpu_baseline(seconds_budget=12.0):
+    """Time the CPU oracle on a bounded sample of the decode workload: one
+    C2 layer at L=8192 (f32 values of the f16 cache, as vantablack's f32
+    cache would hold them), repeated until ~seconds_budget is spent."""
+    import numpy as np
+    from oracle import oracle as orc
+    n_heads, n_kv, d, L = 32, 32, 128, 8192
+    rng = np.random.default_rng(0)
+    cache = orc.OracleKvCache(1, n_kv, d, L)
+    cache.k[:] = rng.standard_normal(cache.k.size, dtype=np.float32).astype(np.float16).astype(np.float32)
+    cache.v[:] = rng.standard_normal(cache.v.size, dtype=np.float32).astype(np.float16).astype(np.float32)
+    cache.pos = L - 1
+    c = orc.config(n_heads, n_kv, d, L)
+    q = (rng.standard_normal(n_heads * d, dtype=np.float32) / np.float32(np.sqrt(d)))
+    per = decode_bytes(L, n_heads, n_kv, d, 2)
+    res = {}
+    workers = int(os.environ.get("VTB_CPU_WORKERS", "16"))
+    for label, nw in (("faithful_1t", 1), ("pool", workers)):
+        pool = orc.Pool(nw)
+        try:
+            n, t0 = 0, time.perf_counter()
+            while True:
+                pool.attention(q, cache, c, 0, L - 1)
+                n += 1
+                el = time.perf_counter() - t0
+                if el > seconds_budget / 2:
+                    break
+        finally:
+            pool.close()
+        res[label] = {"gbs": n * per / el / 1e9, "ms_per_layer": el / n * 1e3, "layers": n, "workers": nw}
+        log(f"cpu {label}: {res[label]['ms_per_layer']:.2f} ms per layer-step ({n} runs)")
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=32)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--ctx", type=int, default=8192)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; the path's multi-GPU sharding is "
+                                   "design-only (DESIGN.md). Run with --gpus 1."}))
+        sys.exit(2)
+
+    import torch
+    import vantablack_amd as vb
+    ctx = vb.Context()
+    dec = bench_decode(ctx, torch, args)
+    cpu = None if args.no_cpu else cpu_baseline()
+    ctx.close()
+
+    line = {
+        "metric": METRIC,
+        "value": round(dec["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (torch.randn on device; random f16 KV cache)",
+        "config": {
+            "workload": f"C2 Llama-2-7B full-stack decode attention @ctx {args.ctx // 1024}K: 32 layers x "
+                        f"32q/32kv heads x d128, f16 KV, L {args.ctx + args.warmup + 1}->"
+                        f"{args.ctx + args.warmup + args.steps}, 1 token/step (KV append + attention per layer)",
+            "n_layers": 32, "n_heads": 32, "n_kv_heads": 32, "head_dim": 128, "kv_dtype": "f16",
+            "ctx": args.ctx,
+        },
+        "pct_of_hbm_peak": round(100.0 * dec["value"] / HBM_PEAK_GBS, 2),
+        "roofline": {
+            "bound": "hbm", "achieved": round(dec["achieved_gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(dec["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "vtb_decode_f16_d128_g1", "avg_launch_us": round(dec["avg_launch_s"] * 1e6, 3),
+            "bytes_per_launch": int(dec["bytes_per_launch"]),
+        },
+    }
+    if cpu:
+        line["cpu_baseline"] = {
+            "value": round(cpu["pool"]["gbs"], 3), "unit": "GB/s", "cores": cpu["pool"]["workers"],
+            "kind": "port",
+            "sample": "one C2 layer at L=8192 (32 heads, d128, f32 values), repeated ~6 s per line; "
+                      "pool = heads split over pool.zig-style workers (vantablack itself runs attention "
+                      "single-threaded)",
+            "faithful_1t": {"value": round(cpu["faithful_1t"]["gbs"], 3), "cores": 1,
+                            "ms_per_layer": round(cpu["faithful_1t"]["ms_per_layer"], 3)},
+            "pool_ms_per_layer": round(cpu["pool"]["ms_per_layer"], 3),
+        }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,190 @@
+/*
+ * vtb_hip.h -- C ABI of the MI355X (gfx950) KV-cache attention path for
+ * vantablack.  Plain pointers, sizes and opaque handles only.
+ *
+ * The shape follows vantablack's Metal bridge (src/metal/bridge.h): a
+ * process-long context, explicitly released buffers, "segments" that enqueue
+ * asynchronously, and a wait_idle drain before the host reads results.
+ *   - constructors return NULL on failure (bridge.h:23-35);
+ *   - calls returning int use 0 = ok, 1 = bad arguments, 2 = device error
+ *     (bridge.m:774, 799-802), plus 3 = KvCacheFull (forward.zig:27-31,161),
+ *     4 = NewMaxSeqBelowPos (kv_cache.zig:149), 5 = unsupported shape;
+ *   - segment encoders return void; the first error they hit is reported by
+ *     vtb_hip_segment_commit (bridge.h:80-89 semantics).
+ *
+ * Memory is discrete HBM: buffers have no host mapping (unlike the shared
+ * MTLBuffers behind KvCache at kv_cache.zig:44-57).  Host data moves only
+ * through vtb_hip_upload / vtb_hip_download.
+ *
+ * One context owns one HIP stream; every call on a context is ordered on it.
+ * A context is driven by one host thread (server.zig:463-467 serialises
+ * inference the same way).
+ */
+#ifndef VTB_HIP_H
+#define VTB_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct VtbHipCtx VtbHipCtx;
+typedef struct VtbHipBuf VtbHipBuf;
+typedef struct VtbHipSeg VtbHipSeg;
+typedef struct VtbHipKvCache VtbHipKvCache;
+
+enum {
+    VTB_HIP_OK = 0,
+    VTB_HIP_EINVAL = 1,
+    VTB_HIP_EDEVICE = 2,
+    VTB_HIP_EFULL = 3,
+    VTB_HIP_ESHRINK = 4,
+    VTB_HIP_EUNSUPPORTED = 5
+};
+
+/* KV cache element type.  vantablack's cache is f32 only
+ * (kv_cache.zig:25-27); f16 and bf16 are added here. */
+enum { VTB_HIP_F32 = 0, VTB_HIP_F16 = 1, VTB_HIP_BF16 = 2 };
+
+/* LlamaConfig.sliding_window == maxInt(usize): no window (model.zig:59-62). */
+#define VTB_HIP_NO_WINDOW ((size_t)-1)
+
+/* The attention fields of LlamaConfig (model.zig:40-70). */
+typedef struct {
+    size_t n_heads;
+    size_t n_kv_heads;
+    size_t head_dim;
+    size_t max_seq;
+    size_t sliding_window; /* VTB_HIP_NO_WINDOW to disable */
+} VtbHipAttnConfig;
+
+/* ---- lifecycle: replaces vtb_metal_init / vtb_metal_destroy (bridge.h:23-25).
+ * Binds the current HIP device, creates a default-priority stream and loads
+ * the gfx950 code objects (hipModuleLoadData).  NULL if no gfx950 device. */
+VtbHipCtx *vtb_hip_init(void);
+void vtb_hip_destroy(VtbHipCtx *ctx);
+/* The hipStream_t every call on ctx is enqueued on. */
+void *vtb_hip_stream(VtbHipCtx *ctx);
+/* Text of the most recent error on ctx ("" if none). */
+const char *vtb_hip_last_error(VtbHipCtx *ctx);
+/* Number of compute units of the bound device (0 on error). */
+int vtb_hip_cu_count(VtbHipCtx *ctx);
+
+/* ---- buffers: replaces vtb_metal_alloc / vtb_metal_wrap / vtb_metal_release
+ * (bridge.h:27-39).  Device memory, no host pointer. */
+VtbHipBuf *vtb_hip_alloc(VtbHipCtx *ctx, size_t bytes);
+/* Wrap existing device memory (no copy, not freed on release). */
+VtbHipBuf *vtb_hip_wrap(VtbHipCtx *ctx, void *device_ptr, size_t bytes);
+void vtb_hip_release(VtbHipBuf *buf);
+void *vtb_hip_buf_device_ptr(VtbHipBuf *buf);
+size_t vtb_hip_buf_size(VtbHipBuf *buf);
+/* Stream-ordered host<->device copies; download blocks until the bytes are
+ * on the host.  These replace the host slices of the unified-memory design
+ * (forward.zig:56-73). */
+int vtb_hip_upload(VtbHipCtx *ctx, VtbHipBuf *dst, size_t dst_offset, const void *src, size_t bytes);
+int vtb_hip_download(VtbHipCtx *ctx, void *dst, VtbHipBuf *src, size_t src_offset, size_t bytes);
+
+/* ---- segments: replaces vtb_metal_segment_begin / _commit / vtb_metal_wait_idle
+ * (bridge.h:73-89).  Work is enqueued on the context stream as it is encoded;
+ * commit reports the first encoding error and does not wait. */
+VtbHipSeg *vtb_hip_segment_begin(VtbHipCtx *ctx);
+int vtb_hip_segment_commit(VtbHipSeg *seg);
+/* Blocks until all work enqueued on ctx has finished (bridge.h:84-87). */
+int vtb_hip_wait_idle(VtbHipCtx *ctx);
+
+/* f32 copy, dst[dst_off + i] = src[src_off + i] for i < n_floats.
+ * Replaces vtb_metal_segment_copy (bridge.h:148-155). */
+void vtb_hip_segment_copy(VtbHipSeg *seg, VtbHipBuf *dst_buf, size_t dst_offset_bytes,
+                          VtbHipBuf *src_buf, size_t src_offset_bytes, size_t n_floats);
+
+/* KV-slot append: kv[slot_off + i] = round(src[src_off + i]) for i < n,
+ * rounding f32 to the cache dtype (nearest even).  Replaces the two
+ * seg.copy splices into kv_k / kv_v (forward.zig:466-468) and the CPU
+ * @memcpy into keySlot/valueSlot (forward.zig:267-269).  n may span several
+ * consecutive slots (a prefill's B rows, prefill.zig:175-191). */
+void vtb_hip_segment_kv_append(VtbHipSeg *seg, VtbHipBuf *kv_buf, size_t slot_offset_bytes,
+                               int kv_dtype, VtbHipBuf *src_buf, size_t src_offset_bytes,
+                               size_t n);
+
+/* Decode attention for one token, one layer:
+ *   out[h,:] = sum_t softmax_t((q[h] . K[t,kv_h]) * inv_sqrt_hd) V[t,kv_h,:]
+ * for t in [0, seq_len), kv_h = (h*n_kv_heads)/n_heads.  q and out are f32
+ * [n_heads*head_dim]; K/V rows are [n_kv_heads*head_dim] of kv_dtype starting
+ * at the given byte offsets (the caller applies the sliding window by moving
+ * the offset forward window_start rows and passing attended_len as seq_len,
+ * exactly as forward.zig:470-483 does).  Replaces vtb_metal_segment_attn_scores,
+ * _softmax_rows and _attn_weighted_sum (bridge.h:157-183) with one split-K
+ * launch; no score buffer exists.  head_dim in {64,128,256}; offsets 16-byte
+ * aligned. */
+void vtb_hip_segment_attn_decode(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *q_buf,
+                                 VtbHipBuf *k_cache_buf, size_t k_cache_offset_bytes,
+                                 VtbHipBuf *v_cache_buf, size_t v_cache_offset_bytes,
+                                 size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                 size_t seq_len, float inv_sqrt_hd, int kv_dtype);
+
+/* Causal prefill attention for n_tokens queries of one layer.  Query b sits
+ * at absolute position pos0 + b and attends rows [window_start(pos0+b),
+ * pos0+b] of the layer whose row 0 is at layer_offset_bytes in k/v, where
+ * window_start follows forward.zig:195-203.  Replaces the per-position loop
+ * `for b: attentionCausal` (prefill.zig:193-197, 237-287), which has no Metal
+ * counterpart.  q: [n_tokens][n_heads*head_dim]; out: f32, same shape.
+ * For f16/bf16 caches q holds that dtype and the kernel runs on MFMA
+ * (P is rounded to f16 for the PV product); for f32 caches q is f32 and the
+ * exact f32 decode kernel runs per query. */
+void vtb_hip_segment_attn_prefill(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *q_buf,
+                                  VtbHipBuf *k_cache_buf, VtbHipBuf *v_cache_buf,
+                                  size_t layer_offset_bytes, size_t n_tokens, size_t pos0,
+                                  size_t sliding_window, size_t n_heads, size_t n_kv_heads,
+                                  size_t head_dim, float inv_sqrt_hd, int dtype);
+
+/* ---- KvCache, device-handle mode (kv_cache.zig:20-196).  Layer-major
+ * [n_layers][max_seq][n_kv_heads][head_dim] of dtype in HBM; no host slices. */
+VtbHipKvCache *vtb_hip_kv_cache_init(VtbHipCtx *ctx, size_t n_layers, size_t n_kv_heads,
+                                     size_t head_dim, size_t max_seq, int dtype); /* :33-73 */
+void vtb_hip_kv_cache_deinit(VtbHipKvCache *cache);                              /* :75-81 */
+void vtb_hip_kv_cache_reset(VtbHipKvCache *cache);                               /* :83-85 */
+size_t vtb_hip_kv_cache_pos(const VtbHipKvCache *cache);
+/* Set pos directly (tests and prefill's `cache.pos += B`, prefill.zig:141). */
+int vtb_hip_kv_cache_set_pos(VtbHipKvCache *cache, size_t pos);
+size_t vtb_hip_kv_cache_max_seq(const VtbHipKvCache *cache);
+int vtb_hip_kv_cache_dtype(const VtbHipKvCache *cache);
+int vtb_hip_kv_cache_advance(VtbHipKvCache *cache);                              /* :130-133 */
+/* Byte offset of the slot at pos in layer (keySlot/valueSlot, :97-111);
+ * (size_t)-1 where the reference asserts. */
+size_t vtb_hip_kv_cache_slot_offset(const VtbHipKvCache *cache, size_t layer);
+/* Byte offset of row 0 of layer (keysFor/valuesFor, :116-128). */
+size_t vtb_hip_kv_cache_layer_offset(const VtbHipKvCache *cache, size_t layer);
+VtbHipBuf *vtb_hip_kv_cache_k(VtbHipKvCache *cache);
+VtbHipBuf *vtb_hip_kv_cache_v(VtbHipKvCache *cache);
+/* :147-195.  Compacts every layer's live prefix into a new allocation of
+ * new_max_seq rows per layer and frees the old one (the HBM tail is returned,
+ * unlike the Metal path).  0, or 4 if new_max_seq < pos. */
+int vtb_hip_kv_cache_shrink_to_fit(VtbHipKvCache *cache, size_t new_max_seq);
+
+/* ---- Layer-level entries mirroring the reference call sites.
+ *
+ * Decode, one layer (forward.zig:267-270 then cpuAttention :187-228): write
+ * k_cur/v_cur (f32 [n_kv_heads*head_dim]) into the slot at cache->pos, then
+ * attend [window_start(pos), pos] with q (f32 [n_heads*head_dim]) into
+ * attn_out (f32).  Does not advance pos (stepWithBackend advances once after
+ * all layers, forward.zig:168).  3 if pos >= max_seq. */
+int vtb_hip_layer_attention(VtbHipSeg *seg, VtbHipKvCache *cache, const VtbHipAttnConfig *c,
+                            size_t layer, VtbHipBuf *q, VtbHipBuf *k_cur, VtbHipBuf *v_cur,
+                            VtbHipBuf *attn_out);
+
+/* Prefill, one layer (prefill.zig:174-197): write the n_tokens rows of
+ * k_cur/v_cur (f32 [n_tokens][kv_dim]) into slots pos..pos+n_tokens-1, then
+ * causal attention for every query (q f32 [n_tokens][n_heads*head_dim]) into
+ * attn_out.  For f16/bf16 caches q is rounded to the cache dtype before the
+ * MFMA kernel.  Does not advance pos.  3 if pos + n_tokens > max_seq. */
+int vtb_hip_prefill_attention(VtbHipSeg *seg, VtbHipKvCache *cache, const VtbHipAttnConfig *c,
+                              size_t layer, size_t n_tokens, VtbHipBuf *q, VtbHipBuf *k_cur,
+                              VtbHipBuf *v_cur, VtbHipBuf *attn_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VTB_HIP_H */

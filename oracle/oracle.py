@@ -140,7 +140,8 @@ def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
 
 def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
     """Round f32 to IEEE binary16 (numpy's cast is round-to-nearest-even)."""
-    return np.ascontiguousarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+    with np.errstate(over="ignore"):  # out-of-range values round to +-inf, as IEEE requires
+        return np.ascontiguousarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
 
 
 def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:

@@ -17,3 +17,15 @@ def orc():
     from oracle import oracle
     oracle.build()
     return oracle
+
+
+@pytest.fixture(scope="session")
+def ctx():
+    """A vtb_hip context on cuda:0.  Skips only where no GPU device node
+    exists at all; on a GPU box a failing init is an error, never a skip."""
+    if not os.path.exists("/dev/kfd"):
+        pytest.skip("no GPU (/dev/kfd absent)")
+    import vantablack_amd as vb
+    c = vb.Context()
+    yield c
+    c.close()

@@ -1,0 +1,90 @@
+"""GPU parity harness: runs a case through the C ABI and through the oracle on
+the same seeded inputs, and measures the agreement.
+
+Tolerances (from the task's north star, written here once):
+  * f32 KV:      max relative error <= 1e-5;
+  * f16/bf16 KV: max relative error <= 2e-3 and identical argmax of the
+                 downstream logits.
+The relative error is tests.util.rel_err (per head: max|diff| / max|ref|).
+Downstream logits are a fixed seeded projection W (VOCAB x n_heads*head_dim)
+of the attention output, evaluated in f64 for both sides.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from tests.util import rel_err
+
+TOL = {"f32": 1e-5, "f16": 2e-3, "bf16": 2e-3}
+VOCAB = 2048
+
+
+def downstream_argmax(orc, out: np.ndarray, n_rows: int, seed: int = 777) -> np.ndarray:
+    """argmax of W @ out_row for every row (query), W ~ N(0,1) seeded."""
+    o = np.asarray(out, np.float64).reshape(n_rows, -1)
+    W = orc.normal(seed, VOCAB * o.shape[1]).astype(np.float64).reshape(VOCAB, o.shape[1])
+    return np.argmax(o @ W.T, axis=1)
+
+
+def check(orc, got, ref, n_heads, dtype, n_queries=1, what=""):
+    err = rel_err(got, ref, n_heads * n_queries)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    assert err <= TOL[dtype], f"{what}: rel err {err:.3e} > {TOL[dtype]:.0e}"
+    if dtype != "f32":
+        a = downstream_argmax(orc, got, n_queries)
+        b = downstream_argmax(orc, ref, n_queries)
+        assert np.array_equal(a, b), f"{what}: downstream argmax differs"
+    return err
+
+
+def make_kv(orc, n_rows, n_kv, d, dtype, seed, outlier_frac=0.0, outlier_scale=20.0):
+    """Seeded K/V rows [n_rows, n_kv, d]; returns (k_store, k_exact, v_store, v_exact)."""
+    k = orc.normal(seed * 2 + 1, n_rows * n_kv * d).reshape(n_rows, n_kv, d)
+    v = orc.normal(seed * 2 + 2, n_rows * n_kv * d).reshape(n_rows, n_kv, d)
+    if outlier_frac > 0:
+        n_ch = max(1, int(round(outlier_frac * n_kv * d)))
+        ch = np.random.default_rng(seed).choice(n_kv * d, n_ch, replace=False)
+        for arr in (k, v):
+            flat = arr.reshape(n_rows, n_kv * d)
+            flat[:, ch] *= np.float32(outlier_scale)
+    ks, kx = orc.to_dtype(k, dtype)
+    vs, vx = orc.to_dtype(v, dtype)
+    return ks.reshape(k.shape), kx.reshape(k.shape), vs.reshape(v.shape), vx.reshape(v.shape)
+
+
+def decode_case(ctx, orc, n_heads, n_kv, d, pos, dtype, window=None, seed=0, q_scale=None,
+                n_layers=1, layer=0, max_seq=None, outlier_frac=0.0):
+    """One decode step at `pos` through vtb_hip_layer_attention (KV-slot write
+    + attention) against forward.cpuAttention restated.  Returns the error."""
+    import vantablack_amd as vb
+    max_seq = max_seq or pos + 1
+    W = orc.NO_WINDOW if window is None else window
+    ks, kx, vs, vx = make_kv(orc, pos + 1, n_kv, d, dtype, seed, outlier_frac)
+    q = orc.normal(seed + 1000, n_heads * d)
+    q = q * np.float32(q_scale) if q_scale is not None else q
+
+    cache = vb.KvCache(ctx, n_layers, n_kv, d, max_seq, dtype)
+    try:
+        if pos > 0:
+            cache.write_rows("k", layer, 0, ks[:pos])
+            cache.write_rows("v", layer, 0, vs[:pos])
+        cache.pos = pos
+        c = vb.LlamaConfig(n_heads, n_kv, d, max_seq, W)
+        qb, kb, vb_, ob = (ctx.to_device(q), ctx.to_device(kx[pos].reshape(-1)),
+                           ctx.to_device(vx[pos].reshape(-1)), ctx.alloc(n_heads * d * 4))
+        with ctx.segment() as seg:
+            vb.layer_attention(seg, cache, c, layer, qb, kb, vb_, ob)
+        ctx.wait_idle()
+        got = ctx.download(ob, np.float32, n_heads * d)
+        # the slot write must land bit-exactly
+        row = cache.read_rows("k", layer, pos + 1)[pos]
+        assert np.array_equal(row.reshape(-1), ks[pos].reshape(-1)), "KV slot write mismatch"
+    finally:
+        cache.close()
+
+    ocache = orc.OracleKvCache(n_layers, n_kv, d, max_seq)
+    ocache.layer_rows("k", layer)[:pos + 1] = kx
+    ocache.layer_rows("v", layer)[:pos + 1] = vx
+    ocache.pos = pos
+    ref = orc.cpu_attention(q, ocache, orc.config(n_heads, n_kv, d, max_seq, W), layer)
+    return check(orc, got, ref, n_heads, dtype, what=f"decode h{n_heads}/{n_kv} d{d} pos{pos} {dtype} w{window}")

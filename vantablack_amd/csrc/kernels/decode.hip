@@ -1,0 +1,334 @@
+// Split-K decode attention over the layer-major KV cache (gfx950).
+//
+// Replaces vantablack's three Metal kernels attn_scores / softmax_rows /
+// attn_weighted_sum (src/metal/bridge.m:490-603) and computes exactly what
+// forward.cpuAttention does (src/runtime/forward.zig:187-228):
+//   out[h] = sum_t softmax_t(q[h].K[t,kv_h] / sqrt(D)) V[t,kv_h],
+//   kv_h = (h*n_kv)/n_heads, t over [window_start, pos].
+//
+// Work decomposition (one launch per layer):
+//   grid  = (n_splits, n_kv, n_q); block = NW waves.
+//   A workgroup owns one (query b, KV head, row split) and each of its waves
+//   a contiguous run of the split's rows.  Every K/V row is read from HBM once
+//   and used for all q heads of the GQA group, so GQA reuse costs no extra
+//   HBM traffic.
+//   Inside a wave, a K (or V) row of D elements is spread over LPR = D*bytes/16
+//   lanes, one 16-byte load per lane; RPW = 64/LPR rows are read per load
+//   instruction, NIT instructions per tile.  Tiles are double-buffered in
+//   registers: the next tile's loads are issued before this tile's math.
+//   Scores are reduced across the LPR lanes with DPP adds; the softmax is
+//   online (running max m, sum l, accumulator acc) per wave, in registers.
+//   The waves combine into one (m, l, o) partial per workgroup with LDS
+//   float atomics after agreeing on the workgroup max.  The last-arriving
+//   workgroup of each (query, KV head) merges the partials (log-sum-exp),
+//   loading them in independent batches, and writes out[h] = o/l.  It resets
+//   the arrival counter to zero, so no memset is needed between launches.
+//   Partials travel through agent-coherent stores/loads and a relaxed
+//   counter; no device-wide fence (L2 writeback/invalidate) is executed.
+//
+// Numerics: all arithmetic is f32 on exactly-upcast K/V.  The 1/sqrt(D)
+// scale is folded with log2(e) into q once, and exp is evaluated as exp2.
+//
+// Multi-query form (n_q > 1): query b sits at absolute position pos0 + b and
+// attends [window_start(pos0+b), pos0+b] -- the row loop of
+// prefill.attentionCausal (src/runtime/prefill.zig:237-287).  The f32-cache
+// prefill path uses it; decode is n_q = 1.
+#include "common.h"
+#include "../tiles.h"
+
+namespace vtb {
+
+struct DecodeArgs {
+  const float* q;       // [n_q][n_heads][D] f32
+  const void* k;        // layer base: row t at k + t*n_kv*D elements
+  const void* v;
+  float* out;           // [n_q][n_heads][D] f32
+  float* ws_o;          // [n_q][n_kv][n_splits][G][D]
+  float* ws_ml;         // [n_q][n_kv][n_splits][G][2]
+  unsigned* counters;   // [n_q][n_kv], zero between launches
+  int n_heads;
+  int n_kv;
+  int n_splits;
+  int rows_per_split;   // multiple of NW * RPW
+  long long pos0;       // absolute position of query 0
+  long long window;     // sliding window in rows; <= 0 disables it
+  float scale_log2;     // (1/sqrt(D)) * log2(e)
+  int pad;
+};
+
+template <typename KV, int D, int G, int NIT, int NW>
+__device__ __forceinline__ void decode_body(const DecodeArgs& a) {
+  constexpr int EPL = Unpack<KV>::N;           // elements per lane per load
+  constexpr int LPR = D / EPL;                 // lanes per row
+  constexpr int RPW = 64 / LPR;                // rows per load instruction
+  constexpr int TR = RPW * NIT;                // rows per wave tile
+  constexpr int NT = NW * 64;                  // threads per workgroup
+  static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "bad row split");
+
+  __shared__ float s_m[NW][G];
+  __shared__ float s_l[G];
+  __shared__ float s_o[G][D];
+  __shared__ int s_last;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int split = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+
+  const long long qpos = a.pos0 + b;
+  const long long wstart = (a.window <= 0 || qpos < a.window) ? 0 : qpos - a.window + 1;
+  const long long L = qpos + 1 - wstart;
+  const long long r0 = wstart + (long long)split * a.rows_per_split;
+  const long long r1 = (r0 + a.rows_per_split < qpos + 1) ? r0 + a.rows_per_split : qpos + 1;
+  if (r0 >= r1) return;  // this query needs fewer splits; not counted below
+  const int n_act = (int)((L + a.rows_per_split - 1) / a.rows_per_split);
+
+  // GQA group of this KV head: h with (h*n_kv)/n_heads == kvh.
+  const int h_lo = (kvh * a.n_heads + a.n_kv - 1) / a.n_kv;
+  const int h_hi = ((kvh + 1) * a.n_heads + a.n_kv - 1) / a.n_kv;
+  const int gs = h_hi - h_lo;
+  if (gs <= 0) return;
+
+  for (int i = threadIdx.x; i < G * D; i += NT) (&s_o[0][0])[i] = 0.0f;
+  if (threadIdx.x < G) s_l[threadIdx.x] = 0.0f;
+
+  const int col = lane % LPR;
+  const int rsub = lane / LPR;
+  const long long row_stride = (long long)a.n_kv * D;  // elements
+  const char* kbase = (const char*)a.k + ((long long)kvh * D + col * EPL) * KV::bytes;
+  const char* vbase = (const char*)a.v + ((long long)kvh * D + col * EPL) * KV::bytes;
+
+  float qv[G][EPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float* qp = a.q + ((long long)b * a.n_heads + h_lo + (g < gs ? g : 0)) * D + col * EPL;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) qv[g][e] = (g < gs) ? qp[e] * a.scale_log2 : 0.0f;
+  }
+
+  float m[G], l[G], acc[G][EPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
+  }
+
+  // This wave's contiguous rows [w0, w1): an equal share, rounded to RPW.
+  const long long per_wave = ((r1 - r0 + NW - 1) / NW + RPW - 1) / RPW * RPW;
+  const long long w0 = r0 + (long long)wave * per_wave;
+  const long long w1 = (w0 + per_wave < r1) ? w0 + per_wave : r1;
+
+  auto issue = [&](long long t0, u32x4 (&kr)[NIT], u32x4 (&vr)[NIT]) {
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) {
+      long long row = t0 + i * RPW + rsub;
+      long long rc = row < w1 ? row : w1 - 1;  // clamp: never read past the range
+      kr[i] = load16(kbase + rc * row_stride * KV::bytes);
+    }
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) {
+      long long row = t0 + i * RPW + rsub;
+      long long rc = row < w1 ? row : w1 - 1;
+      vr[i] = load16(vbase + rc * row_stride * KV::bytes);
+    }
+  };
+  auto compute = [&](long long t0, const u32x4 (&kr)[NIT], const u32x4 (&vr)[NIT]) {
+    float s[G][NIT];
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) {
+      float kf[EPL];
+      Unpack<KV>::run(kr[i], kf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) d = fmaf(qv[g][e], kf[e], d);
+        s[g][i] = d;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mt = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < NIT; ++i) {
+        float v = group_sum<LPR>(s[g][i]);
+        v = (t0 + i * RPW + rsub < w1) ? v : -INFINITY;
+        s[g][i] = v;
+        mt = fmaxf(mt, v);
+      }
+      mt = stride_max<LPR>(mt);
+      const float mn = fmaxf(m[g], mt);  // finite: row t0 is always in range
+      const float corr = exp2_fast(m[g] - mn);
+      m[g] = mn;
+      float ls = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NIT; ++i) {
+        s[g][i] = exp2_fast(s[g][i] - mn);
+        ls += s[g][i];
+      }
+      l[g] = l[g] * corr + ls;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[g][e] *= corr;
+    }
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) {
+      float vf[EPL];
+      Unpack<KV>::run(vr[i], vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(s[g][i], vf[e], acc[g][e]);
+    }
+  };
+
+  u32x4 ka[NIT], va[NIT], kb[NIT], vb[NIT];
+  long long t0 = w0;
+  if (t0 < w1) issue(t0, ka, va);
+  while (t0 < w1) {
+    if (t0 + TR < w1) issue(t0 + TR, kb, vb);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(t0, ka, va);
+    t0 += TR;
+    if (t0 >= w1) break;
+    if (t0 + TR < w1) issue(t0 + TR, ka, va);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(t0, kb, vb);
+    t0 += TR;
+  }
+
+  // Combine the row groups of the wave (lanes sharing `col`).
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    l[g] = stride_sum<LPR>(l[g]);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[g][e] = stride_sum<LPR>(acc[g][e]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) s_m[wave][g] = m[g];
+  }
+  __syncthreads();
+
+  // Workgroup combine: rescale each wave to the workgroup max and add into
+  // LDS.  A wave with no rows has m = -inf and contributes nothing.
+  float M[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mm = fmaxf(mm, s_m[w][g]);
+    M[g] = mm;
+  }
+  if (w0 < w1 && rsub == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float f = exp2_fast(m[g] - M[g]);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) atomicAdd(&s_o[g][col * EPL + e], acc[g][e] * f);
+      if (col == 0) atomicAdd(&s_l[g], l[g] * f);
+    }
+  }
+  __syncthreads();
+
+  const bool single = (n_act == 1);
+  const long long part = ((long long)b * a.n_kv + kvh) * a.n_splits + split;
+  for (int idx = threadIdx.x; idx < G * D; idx += NT) {
+    const int g = idx / D, d = idx % D;
+    if (g >= gs) continue;
+    if (single) {
+      a.out[((long long)b * a.n_heads + h_lo + g) * D + d] = s_o[g][d] / s_l[g];
+    } else {
+      // Agent-scope atomic stores are coherent across the XCDs' L2s, so the
+      // partials need no cache-wide writeback (a __threadfence() here costs
+      // a full L2 writeback + invalidate per workgroup on this chip).
+      store_coherent(&a.ws_o[(part * G + g) * D + d], s_o[g][d]);
+      if (d == 0) {
+        store_coherent(&a.ws_ml[(part * G + g) * 2 + 0], M[g]);
+        store_coherent(&a.ws_ml[(part * G + g) * 2 + 1], s_l[g]);
+      }
+    }
+  }
+  if (single) return;
+
+  // Publish: every thread's coherent stores complete before the workgroup
+  // counts itself in; the last of the n_act workgroups merges.
+  wait_stores();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned* ctr = a.counters + (long long)b * a.n_kv + kvh;
+    unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = (prev == (unsigned)(n_act - 1));
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  // Merge n_act partials.  Each thread owns outputs (g, d); partials are
+  // consumed in batches of MB whose loads are all independent, with an
+  // online rescale between batches.
+  constexpr int MB = 8;
+  const long long part0 = ((long long)b * a.n_kv + kvh) * a.n_splits;
+  for (int idx = threadIdx.x; idx < G * D; idx += NT) {
+    const int g = idx / D, d = idx % D;
+    if (g >= gs) continue;
+    float Mx = -INFINITY, Ls = 0.0f, O = 0.0f;
+    for (int sp0 = 0; sp0 < n_act; sp0 += MB) {
+      float mv[MB], lv[MB], ov[MB];
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        const int sp = sp0 + j < n_act ? sp0 + j : n_act - 1;
+        const long long pj = (part0 + sp) * G + g;
+        mv[j] = load_coherent(&a.ws_ml[pj * 2]);
+        lv[j] = load_coherent(&a.ws_ml[pj * 2 + 1]);
+        ov[j] = load_coherent(&a.ws_o[pj * D + d]);
+      }
+      float mb = Mx;
+#pragma unroll
+      for (int j = 0; j < MB; ++j)
+        if (sp0 + j < n_act) mb = fmaxf(mb, mv[j]);
+      const float c = exp2_fast(Mx - mb);
+      Ls *= c;
+      O *= c;
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        if (sp0 + j < n_act) {
+          const float f = exp2_fast(mv[j] - mb);
+          Ls += lv[j] * f;
+          O += ov[j] * f;
+        }
+      }
+      Mx = mb;
+    }
+    a.out[((long long)b * a.n_heads + h_lo + g) * D + d] = O / Ls;
+  }
+}
+
+}  // namespace vtb
+
+// Kernel entry points, one per (KV dtype, head_dim, max GQA group).  Looked
+// up by name with hipModuleGetFunction: vtb_decode_<kv>_d<D>_g<G>.
+#define VTB_DECODE(KVN, KVT, D, G)                                                     \
+  extern "C" __global__ __launch_bounds__(vtb::decode_waves(G) * 64) void             \
+      vtb_decode_##KVN##_d##D##_g##G(vtb::DecodeArgs a) {                             \
+    vtb::decode_body<vtb::KVT, D, G, vtb::decode_nit(G), vtb::decode_waves(G)>(a);    \
+  }
+
+#define VTB_DECODE_G(KVN, KVT, D) \
+  VTB_DECODE(KVN, KVT, D, 1)      \
+  VTB_DECODE(KVN, KVT, D, 2)      \
+  VTB_DECODE(KVN, KVT, D, 4)      \
+  VTB_DECODE(KVN, KVT, D, 8)      \
+  VTB_DECODE(KVN, KVT, D, 16)
+
+#define VTB_DECODE_D(KVN, KVT) \
+  VTB_DECODE_G(KVN, KVT, 64)   \
+  VTB_DECODE_G(KVN, KVT, 128)  \
+  VTB_DECODE_G(KVN, KVT, 256)
+
+VTB_DECODE_D(f32, kv_f32)
+VTB_DECODE_D(f16, kv_f16)
+VTB_DECODE_D(bf16, kv_bf16)

@@ -1,0 +1,25 @@
+// Tile constants shared by the gfx950 kernels and the host launcher, so the
+// host's split planning always matches what each compiled kernel assumes.
+#pragma once
+
+namespace vtb {
+
+// Decode: 16-byte loads per lane per wave tile (NIT), by GQA group width.
+// Tiles are double-buffered, so a wave keeps 2 x 2 x NIT loads in flight;
+// NIT shrinks as the group widens to keep the q/acc registers resident.
+constexpr int decode_nit(int g) { return g <= 4 ? 4 : (g == 8 ? 2 : 1); }
+
+// Waves per decode workgroup: as many as the register budget allows
+// (16 waves = 4 per SIMD needs <= 128 registers per lane).
+constexpr int decode_waves(int g) { return g == 1 ? 16 : (g <= 8 ? 8 : 4); }
+
+// Rows read by one wave load instruction (the split granularity).
+constexpr int decode_rows_per_load(int head_dim, int kv_bytes) {
+  return 64 / (head_dim * kv_bytes / 16);
+}
+
+// Prefill (MFMA): queries per workgroup and keys per LDS tile, by head_dim.
+constexpr int prefill_block_m(int head_dim) { return head_dim <= 128 ? 128 : 64; }
+constexpr int prefill_block_n(int head_dim) { return head_dim <= 128 ? 64 : 32; }
+
+}  // namespace vtb

@@ -1,0 +1,730 @@
+// Host shim of the gfx950 KV-cache attention path: the C ABI in
+// include/vtb_hip.h.  Built with g++ against the HIP runtime only; the
+// kernels are gfx950 code objects (hipcc --genco) embedded in this library
+// and loaded with hipModuleLoadData, launched with hipModuleLaunchKernel.
+//
+// Mirrors the conventions of vantablack's Metal bridge (src/metal/bridge.m):
+// opaque handles, NULL on failed construction, int return codes, segments
+// that enqueue asynchronously and a wait_idle drain.
+#include "vtb_hip.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "tiles.h"
+
+extern "C" {
+// Code objects embedded by blobs.S (.incbin of the hipcc --genco outputs).
+extern const unsigned char vtb_blob_decode[];
+extern const unsigned char vtb_blob_prefill[];
+extern const unsigned char vtb_blob_kvcopy[];
+}
+
+namespace {
+
+constexpr int kNumKv = 3;     // f32, f16, bf16
+constexpr int kNumD = 3;      // 64, 128, 256
+constexpr int kNumG = 5;      // 1, 2, 4, 8, 16
+const int kGs[kNumG] = {1, 2, 4, 8, 16};
+const char* kKvNames[kNumKv] = {"f32", "f16", "bf16"};
+const int kKvBytes[kNumKv] = {4, 2, 2};
+
+int d_index(size_t d) { return d == 64 ? 0 : d == 128 ? 1 : d == 256 ? 2 : -1; }
+
+// Arguments of vtb_decode_* (layout must match DecodeArgs in decode.hip).
+struct DecodeArgs {
+  const float* q;
+  const void* k;
+  const void* v;
+  float* out;
+  float* ws_o;
+  float* ws_ml;
+  unsigned* counters;
+  int n_heads;
+  int n_kv;
+  int n_splits;
+  int rows_per_split;
+  long long pos0;
+  long long window;
+  float scale_log2;
+  int pad;
+};
+
+// Arguments of vtb_prefill_* (layout must match PrefillArgs in prefill.hip).
+struct PrefillArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  float* out;
+  int n_q;
+  int n_heads;
+  int n_kv;
+  int pad0;
+  long long pos0;
+  long long window;
+  float scale_log2;
+  int pad1;
+};
+
+struct AppendArgs {
+  void* dst;
+  const float* src;
+  long long n;
+  int vec;
+  int pad;
+};
+
+struct CopyArgs {
+  float* dst;
+  const float* src;
+  long long n;
+};
+
+}  // namespace
+
+struct VtbHipCtx {
+  int device = 0;
+  int cu_count = 0;
+  hipStream_t stream = nullptr;
+  hipModule_t mod_decode = nullptr, mod_prefill = nullptr, mod_kvcopy = nullptr;
+  hipFunction_t f_decode[kNumKv][kNumD][kNumG] = {};
+  hipFunction_t f_prefill[kNumKv][kNumD] = {};
+  hipFunction_t f_append[kNumKv] = {};
+  hipFunction_t f_copy = nullptr;
+  // Split-K workspace and arrival counters (counters are zero between launches).
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  unsigned* counters = nullptr;
+  size_t n_counters = 0;
+  // Prefill query-conversion scratch (f32 -> cache dtype).
+  void* qconv = nullptr;
+  size_t qconv_bytes = 0;
+  std::string err;
+};
+
+struct VtbHipBuf {
+  VtbHipCtx* ctx;
+  void* ptr;
+  size_t bytes;
+  bool owned;
+};
+
+struct VtbHipSeg {
+  VtbHipCtx* ctx;
+  int rc;
+};
+
+struct VtbHipKvCache {
+  VtbHipCtx* ctx;
+  size_t n_layers, n_kv_heads, head_dim, max_seq;
+  int dtype;
+  size_t pos;
+  VtbHipBuf* k;
+  VtbHipBuf* v;
+};
+
+namespace {
+
+int set_err(VtbHipCtx* ctx, int rc, const char* what, hipError_t e = hipSuccess) {
+  // The error is handled here: clear HIP's last-error slot so it does not
+  // surface later in an unrelated caller (e.g. torch's next allocation).
+  if (e != hipSuccess) (void)hipGetLastError();
+  if (ctx) {
+    char buf[512];
+    if (e != hipSuccess)
+      snprintf(buf, sizeof buf, "%s: %s", what, hipGetErrorString(e));
+    else
+      snprintf(buf, sizeof buf, "%s", what);
+    ctx->err = buf;
+  }
+  return rc;
+}
+
+#define HIP_TRY(ctx, call, what)                                  \
+  do {                                                            \
+    hipError_t e_ = (call);                                       \
+    if (e_ != hipSuccess) return set_err((ctx), VTB_HIP_EDEVICE, (what), e_); \
+  } while (0)
+
+int kv_bytes(int dtype) { return (dtype >= 0 && dtype < kNumKv) ? kKvBytes[dtype] : 0; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int launch(VtbHipCtx* ctx, hipFunction_t f, unsigned gx, unsigned gy, unsigned gz, unsigned bx,
+           void* args) {
+  void* params[] = {args};
+  HIP_TRY(ctx, hipModuleLaunchKernel(f, gx, gy, gz, bx, 1, 1, 0, ctx->stream, params, nullptr),
+          "hipModuleLaunchKernel");
+  return VTB_HIP_OK;
+}
+
+// Grow the split-K workspace / counter array.  Growth waits for in-flight
+// work first, so a buffer is never freed under a running kernel.
+int ensure_workspace(VtbHipCtx* ctx, size_t ws_bytes, size_t n_counters) {
+  if (ws_bytes > ctx->ws_bytes) {
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (ctx->ws) HIP_TRY(ctx, hipFree(ctx->ws), "hipFree");
+    ctx->ws = nullptr;
+    ctx->ws_bytes = 0;
+    size_t sz = std::max(ws_bytes, (size_t)1 << 20);
+    HIP_TRY(ctx, hipMalloc(&ctx->ws, sz), "hipMalloc(workspace)");
+    ctx->ws_bytes = sz;
+  }
+  if (n_counters > ctx->n_counters) {
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (ctx->counters) HIP_TRY(ctx, hipFree(ctx->counters), "hipFree");
+    ctx->counters = nullptr;
+    ctx->n_counters = 0;
+    size_t n = std::max(n_counters, (size_t)4096);
+    HIP_TRY(ctx, hipMalloc((void**)&ctx->counters, n * sizeof(unsigned)), "hipMalloc(counters)");
+    HIP_TRY(ctx, hipMemsetAsync(ctx->counters, 0, n * sizeof(unsigned), ctx->stream),
+            "hipMemsetAsync(counters)");
+    ctx->n_counters = n;
+  }
+  return VTB_HIP_OK;
+}
+
+int env_int(const char* name, int dflt) {
+  const char* s = getenv(name);
+  if (!s || !*s) return dflt;
+  int v = atoi(s);
+  return v > 0 ? v : dflt;
+}
+
+// Split-K decode / f32 prefill launcher.  Queries b in [0, n_q) sit at
+// pos0 + b and attend [window_start, pos0 + b] of the layer rows at k/v.
+int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, const void* v,
+                  size_t n_q, size_t n_heads, size_t n_kv, size_t head_dim, long long pos0,
+                  long long window, float inv_sqrt_hd, int dtype) {
+  const int di = d_index(head_dim);
+  if (di < 0) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "head_dim must be 64, 128 or 256");
+  if (dtype < 0 || dtype >= kNumKv) return set_err(ctx, VTB_HIP_EINVAL, "bad kv dtype");
+  if (n_heads == 0 || n_kv == 0 || n_q == 0 || pos0 < 0)
+    return set_err(ctx, VTB_HIP_EINVAL, "empty shape");
+  if (!aligned16(k) || !aligned16(v)) return set_err(ctx, VTB_HIP_EINVAL, "K/V not 16-byte aligned");
+  const size_t gmax = (n_heads + n_kv - 1) / n_kv;
+  int gi = 0;
+  while (gi < kNumG && (size_t)kGs[gi] < gmax) ++gi;
+  if (gi == kNumG) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "GQA group wider than 16");
+  const int G = kGs[gi];
+  if (n_q > 65535 || n_kv > 65535) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "grid too large");
+
+  // Longest attended range over the queries.
+  long long Lmax = 0;
+  for (long long b : {0LL, (long long)n_q - 1}) {
+    long long qp = pos0 + b;
+    long long ws = (window <= 0 || qp < window) ? 0 : qp - window + 1;
+    Lmax = std::max(Lmax, qp + 1 - ws);
+  }
+  // One workgroup per CU: the workgroup's waves fill the CU, and few splits
+  // keep the final merge short.  Rows per split are a multiple of the rows
+  // one wave load instruction covers.
+  const long long quantum = vtb::decode_rows_per_load((int)head_dim, kKvBytes[dtype]);
+  const long long target = env_int("VTB_DECODE_TARGET_WGS", std::max(ctx->cu_count, 1));
+  long long want = std::max(1LL, (target + (long long)(n_kv * n_q) - 1) / (long long)(n_kv * n_q));
+  long long rps = (Lmax + want - 1) / want;
+  rps = std::max(quantum, (rps + quantum - 1) / quantum * quantum);
+  long long n_splits = (Lmax + rps - 1) / rps;
+  if (n_splits > 65535) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "too many splits");
+
+  const size_t n_part = n_q * n_kv * (size_t)n_splits * G;
+  const size_t ws_need = n_splits > 1 ? n_part * (head_dim + 2) * sizeof(float) : 0;
+  int rc = ensure_workspace(ctx, ws_need, n_q * n_kv);
+  if (rc) return rc;
+
+  DecodeArgs a;
+  memset(&a, 0, sizeof a);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.ws_o = (float*)ctx->ws;
+  a.ws_ml = (float*)ctx->ws + n_part * head_dim;
+  a.counters = ctx->counters;
+  a.n_heads = (int)n_heads;
+  a.n_kv = (int)n_kv;
+  a.n_splits = (int)n_splits;
+  a.rows_per_split = (int)rps;
+  a.pos0 = pos0;
+  a.window = window;
+  a.scale_log2 = inv_sqrt_hd * 1.4426950408889634f;
+  return launch(ctx, ctx->f_decode[dtype][di][gi], (unsigned)n_splits, (unsigned)n_kv,
+                (unsigned)n_q, 64 * vtb::decode_waves(G), &a);
+}
+
+int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const void* q, const void* k, const void* v,
+                        size_t n_q, size_t n_heads, size_t n_kv, size_t head_dim, long long pos0,
+                        long long window, float inv_sqrt_hd, int dtype) {
+  const int di = d_index(head_dim);
+  if (di < 0) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "head_dim must be 64, 128 or 256");
+  if (dtype != VTB_HIP_F16 && dtype != VTB_HIP_BF16)
+    return set_err(ctx, VTB_HIP_EINVAL, "MFMA prefill needs an f16 or bf16 cache");
+  if (!ctx->f_prefill[dtype][di])
+    return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prefill kernel not built for this shape");
+  if (!aligned16(k) || !aligned16(v) || !aligned16(q))
+    return set_err(ctx, VTB_HIP_EINVAL, "q/K/V not 16-byte aligned");
+  const size_t bm = (size_t)vtb::prefill_block_m((int)head_dim);
+  const size_t nblk = (n_q + bm - 1) / bm;
+  if (nblk > 0x7fffffff || n_heads > 65535) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "grid too large");
+  PrefillArgs a;
+  memset(&a, 0, sizeof a);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.n_q = (int)n_q;
+  a.n_heads = (int)n_heads;
+  a.n_kv = (int)n_kv;
+  a.pos0 = pos0;
+  a.window = window;
+  a.scale_log2 = inv_sqrt_hd * 1.4426950408889634f;
+  return launch(ctx, ctx->f_prefill[dtype][di], (unsigned)nblk, (unsigned)n_heads, 1, 256, &a);
+}
+
+int launch_append(VtbHipCtx* ctx, void* dst, const float* src, size_t n, int dtype) {
+  if (n == 0) return VTB_HIP_OK;
+  if (dtype < 0 || dtype >= kNumKv) return set_err(ctx, VTB_HIP_EINVAL, "bad kv dtype");
+  AppendArgs a;
+  memset(&a, 0, sizeof a);
+  a.dst = dst;
+  a.src = src;
+  a.n = (long long)n;
+  const uintptr_t dmask = kKvBytes[dtype] == 4 ? 15u : 7u;
+  a.vec = ((reinterpret_cast<uintptr_t>(dst) & dmask) == 0 && aligned16(src)) ? 1 : 0;
+  const size_t threads = (n + 3) / 4;
+  const size_t blocks = (threads + 255) / 256;
+  if (blocks > 0x7fffffff) return set_err(ctx, VTB_HIP_EINVAL, "append too large");
+  return launch(ctx, ctx->f_append[dtype], (unsigned)blocks, 1, 1, 256, &a);
+}
+
+long long window_arg(size_t sliding_window) {
+  if (sliding_window == VTB_HIP_NO_WINDOW || sliding_window > (size_t)(1LL << 62)) return 0;
+  return (long long)sliding_window;
+}
+
+bool buf_ok(const VtbHipBuf* b, size_t off, size_t bytes) {
+  return b && b->ptr && off <= b->bytes && bytes <= b->bytes - off;
+}
+
+char* bptr(VtbHipBuf* b, size_t off = 0) { return static_cast<char*>(b->ptr) + off; }
+
+}  // namespace
+
+// ============================================================== lifecycle
+
+extern "C" VtbHipCtx* vtb_hip_init(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return nullptr;
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return nullptr;
+  VtbHipCtx* ctx = new VtbHipCtx();
+  ctx->device = dev;
+  ctx->cu_count = prop.multiProcessorCount;
+  bool ok = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) == hipSuccess;
+  ok = ok && hipModuleLoadData(&ctx->mod_decode, vtb_blob_decode) == hipSuccess;
+  ok = ok && hipModuleLoadData(&ctx->mod_prefill, vtb_blob_prefill) == hipSuccess;
+  ok = ok && hipModuleLoadData(&ctx->mod_kvcopy, vtb_blob_kvcopy) == hipSuccess;
+  char name[96];
+  for (int kv = 0; ok && kv < kNumKv; ++kv) {
+    for (int di = 0; ok && di < kNumD; ++di) {
+      const int D = 64 << di;
+      for (int gi = 0; ok && gi < kNumG; ++gi) {
+        snprintf(name, sizeof name, "vtb_decode_%s_d%d_g%d", kKvNames[kv], D, kGs[gi]);
+        ok = hipModuleGetFunction(&ctx->f_decode[kv][di][gi], ctx->mod_decode, name) == hipSuccess;
+      }
+      if (kv != VTB_HIP_F32) {
+        snprintf(name, sizeof name, "vtb_prefill_%s_d%d", kKvNames[kv], D);
+        if (hipModuleGetFunction(&ctx->f_prefill[kv][di], ctx->mod_prefill, name) != hipSuccess)
+          ctx->f_prefill[kv][di] = nullptr;  // shape not built: reported at launch
+      }
+    }
+    if (ok) {
+      snprintf(name, sizeof name, "vtb_kv_append_%s", kKvNames[kv]);
+      ok = hipModuleGetFunction(&ctx->f_append[kv], ctx->mod_kvcopy, name) == hipSuccess;
+    }
+  }
+  ok = ok && hipModuleGetFunction(&ctx->f_copy, ctx->mod_kvcopy, "vtb_copy_f32") == hipSuccess;
+  (void)hipGetLastError();  // absent optional kernels are not an error for the caller
+  if (!ok) {
+    vtb_hip_destroy(ctx);
+    return nullptr;
+  }
+  return ctx;
+}
+
+extern "C" void vtb_hip_destroy(VtbHipCtx* ctx) {
+  if (!ctx) return;
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  if (ctx->counters) (void)hipFree(ctx->counters);
+  if (ctx->qconv) (void)hipFree(ctx->qconv);
+  if (ctx->mod_decode) (void)hipModuleUnload(ctx->mod_decode);
+  if (ctx->mod_prefill) (void)hipModuleUnload(ctx->mod_prefill);
+  if (ctx->mod_kvcopy) (void)hipModuleUnload(ctx->mod_kvcopy);
+  if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+extern "C" void* vtb_hip_stream(VtbHipCtx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+extern "C" const char* vtb_hip_last_error(VtbHipCtx* ctx) { return ctx ? ctx->err.c_str() : ""; }
+
+extern "C" int vtb_hip_cu_count(VtbHipCtx* ctx) { return ctx ? ctx->cu_count : 0; }
+
+// ============================================================== buffers
+
+extern "C" VtbHipBuf* vtb_hip_alloc(VtbHipCtx* ctx, size_t bytes) {
+  if (!ctx || bytes == 0) return nullptr;
+  void* p = nullptr;
+  const hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) {
+    set_err(ctx, VTB_HIP_EDEVICE, "hipMalloc failed", e);
+    return nullptr;
+  }
+  return new VtbHipBuf{ctx, p, bytes, true};
+}
+
+extern "C" VtbHipBuf* vtb_hip_wrap(VtbHipCtx* ctx, void* device_ptr, size_t bytes) {
+  if (!ctx || !device_ptr || bytes == 0) return nullptr;
+  return new VtbHipBuf{ctx, device_ptr, bytes, false};
+}
+
+extern "C" void vtb_hip_release(VtbHipBuf* buf) {
+  if (!buf) return;
+  // hipFree waits for the device itself, so release never touches buf->ctx
+  // and stays safe after the context is destroyed.
+  if (buf->owned && buf->ptr) (void)hipFree(buf->ptr);
+  delete buf;
+}
+
+extern "C" void* vtb_hip_buf_device_ptr(VtbHipBuf* buf) { return buf ? buf->ptr : nullptr; }
+
+extern "C" size_t vtb_hip_buf_size(VtbHipBuf* buf) { return buf ? buf->bytes : 0; }
+
+extern "C" int vtb_hip_upload(VtbHipCtx* ctx, VtbHipBuf* dst, size_t dst_offset, const void* src,
+                              size_t bytes) {
+  if (!ctx || !src || !buf_ok(dst, dst_offset, bytes)) return set_err(ctx, VTB_HIP_EINVAL, "upload: bad range");
+  if (bytes == 0) return VTB_HIP_OK;
+  HIP_TRY(ctx, hipMemcpyAsync(bptr(dst, dst_offset), src, bytes, hipMemcpyHostToDevice, ctx->stream),
+          "hipMemcpyAsync(H2D)");
+  // The source is caller memory that may be reused at once: complete the copy.
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  return VTB_HIP_OK;
+}
+
+extern "C" int vtb_hip_download(VtbHipCtx* ctx, void* dst, VtbHipBuf* src, size_t src_offset,
+                                size_t bytes) {
+  if (!ctx || !dst || !buf_ok(src, src_offset, bytes)) return set_err(ctx, VTB_HIP_EINVAL, "download: bad range");
+  if (bytes == 0) return VTB_HIP_OK;
+  HIP_TRY(ctx, hipMemcpyAsync(dst, bptr(src, src_offset), bytes, hipMemcpyDeviceToHost, ctx->stream),
+          "hipMemcpyAsync(D2H)");
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  return VTB_HIP_OK;
+}
+
+// ============================================================== segments
+
+extern "C" VtbHipSeg* vtb_hip_segment_begin(VtbHipCtx* ctx) {
+  if (!ctx) return nullptr;
+  return new VtbHipSeg{ctx, VTB_HIP_OK};
+}
+
+extern "C" int vtb_hip_segment_commit(VtbHipSeg* seg) {
+  if (!seg) return VTB_HIP_EINVAL;
+  int rc = seg->rc;
+  delete seg;
+  return rc;
+}
+
+extern "C" int vtb_hip_wait_idle(VtbHipCtx* ctx) {
+  if (!ctx) return VTB_HIP_EINVAL;
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  return VTB_HIP_OK;
+}
+
+static void seg_note(VtbHipSeg* seg, int rc) {
+  if (seg && seg->rc == VTB_HIP_OK) seg->rc = rc;
+}
+
+extern "C" void vtb_hip_segment_copy(VtbHipSeg* seg, VtbHipBuf* dst_buf, size_t dst_offset_bytes,
+                                     VtbHipBuf* src_buf, size_t src_offset_bytes, size_t n_floats) {
+  if (!seg) return;
+  VtbHipCtx* ctx = seg->ctx;
+  if (n_floats == 0) return;
+  if ((dst_offset_bytes | src_offset_bytes) & 3u || n_floats > ((size_t)1 << 40) ||
+      !buf_ok(dst_buf, dst_offset_bytes, n_floats * 4) || !buf_ok(src_buf, src_offset_bytes, n_floats * 4))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "copy: bad range"));
+  CopyArgs a{(float*)bptr(dst_buf, dst_offset_bytes), (const float*)bptr(src_buf, src_offset_bytes),
+             (long long)n_floats};
+  seg_note(seg, launch(ctx, ctx->f_copy, (unsigned)((n_floats + 255) / 256), 1, 1, 256, &a));
+}
+
+extern "C" void vtb_hip_segment_kv_append(VtbHipSeg* seg, VtbHipBuf* kv_buf, size_t slot_offset_bytes,
+                                          int kv_dtype, VtbHipBuf* src_buf, size_t src_offset_bytes,
+                                          size_t n) {
+  if (!seg) return;
+  VtbHipCtx* ctx = seg->ctx;
+  const int eb = kv_bytes(kv_dtype);
+  if (!eb) return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "kv_append: bad dtype"));
+  if (n == 0) return;
+  if (slot_offset_bytes % eb || src_offset_bytes % 4 || n > ((size_t)1 << 40) ||
+      !buf_ok(kv_buf, slot_offset_bytes, n * eb) || !buf_ok(src_buf, src_offset_bytes, n * 4))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "kv_append: bad range"));
+  seg_note(seg, launch_append(ctx, bptr(kv_buf, slot_offset_bytes),
+                              (const float*)bptr(src_buf, src_offset_bytes), n, kv_dtype));
+}
+
+extern "C" void vtb_hip_segment_attn_decode(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* q_buf,
+                                            VtbHipBuf* k_cache_buf, size_t k_cache_offset_bytes,
+                                            VtbHipBuf* v_cache_buf, size_t v_cache_offset_bytes,
+                                            size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                            size_t seq_len, float inv_sqrt_hd, int kv_dtype) {
+  if (!seg) return;
+  VtbHipCtx* ctx = seg->ctx;
+  const int eb = kv_bytes(kv_dtype);
+  if (!eb || n_heads == 0 || n_kv_heads == 0 || head_dim == 0 || n_heads > 65535 ||
+      n_kv_heads > 65535 || head_dim > 4096)
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_decode: bad shape"));
+  const size_t qbytes = n_heads * head_dim * 4;
+  if (!buf_ok(out_buf, 0, qbytes) || !buf_ok(q_buf, 0, qbytes))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_decode: q/out too small"));
+  if (seq_len == 0) {
+    // Empty softmax: the reference leaves attn_out zeroed (forward.zig:205).
+    if (hipMemsetAsync(out_buf->ptr, 0, qbytes, ctx->stream) != hipSuccess)
+      seg_note(seg, set_err(ctx, VTB_HIP_EDEVICE, "hipMemsetAsync"));
+    return;
+  }
+  const size_t kv_rows_bytes = seq_len * n_kv_heads * head_dim * eb;
+  if (!buf_ok(k_cache_buf, k_cache_offset_bytes, kv_rows_bytes) ||
+      !buf_ok(v_cache_buf, v_cache_offset_bytes, kv_rows_bytes))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_decode: K/V range outside buffer"));
+  seg_note(seg, launch_decode(ctx, (float*)out_buf->ptr, (const float*)q_buf->ptr,
+                              bptr(k_cache_buf, k_cache_offset_bytes),
+                              bptr(v_cache_buf, v_cache_offset_bytes), 1, n_heads, n_kv_heads,
+                              head_dim, (long long)seq_len - 1, 0, inv_sqrt_hd, kv_dtype));
+}
+
+extern "C" void vtb_hip_segment_attn_prefill(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* q_buf,
+                                             VtbHipBuf* k_cache_buf, VtbHipBuf* v_cache_buf,
+                                             size_t layer_offset_bytes, size_t n_tokens, size_t pos0,
+                                             size_t sliding_window, size_t n_heads, size_t n_kv_heads,
+                                             size_t head_dim, float inv_sqrt_hd, int dtype) {
+  if (!seg) return;
+  VtbHipCtx* ctx = seg->ctx;
+  const int eb = kv_bytes(dtype);
+  if (!eb || n_heads == 0 || n_kv_heads == 0 || head_dim == 0 || n_heads > 65535 ||
+      n_kv_heads > 65535 || head_dim > 4096 || pos0 > ((size_t)1 << 40) || n_tokens > ((size_t)1 << 31))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_prefill: bad shape"));
+  if (n_tokens == 0) return;  // prefillCpu returns early for B == 0 (prefill.zig:120)
+  const size_t qelems = n_tokens * n_heads * head_dim;
+  const size_t qb = dtype == VTB_HIP_F32 ? 4 : 2;
+  if (!buf_ok(out_buf, 0, qelems * 4) || !buf_ok(q_buf, 0, qelems * qb))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_prefill: q/out too small"));
+  const size_t rows = pos0 + n_tokens;
+  const size_t kv_rows_bytes = rows * n_kv_heads * head_dim * eb;
+  if (!buf_ok(k_cache_buf, layer_offset_bytes, kv_rows_bytes) ||
+      !buf_ok(v_cache_buf, layer_offset_bytes, kv_rows_bytes))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_prefill: K/V range outside buffer"));
+  const long long w = window_arg(sliding_window);
+  int rc;
+  if (dtype == VTB_HIP_F32)
+    rc = launch_decode(ctx, (float*)out_buf->ptr, (const float*)q_buf->ptr,
+                       bptr(k_cache_buf, layer_offset_bytes), bptr(v_cache_buf, layer_offset_bytes),
+                       n_tokens, n_heads, n_kv_heads, head_dim, (long long)pos0, w, inv_sqrt_hd, dtype);
+  else
+    rc = launch_prefill_mfma(ctx, (float*)out_buf->ptr, q_buf->ptr, bptr(k_cache_buf, layer_offset_bytes),
+                             bptr(v_cache_buf, layer_offset_bytes), n_tokens, n_heads, n_kv_heads,
+                             head_dim, (long long)pos0, w, inv_sqrt_hd, dtype);
+  seg_note(seg, rc);
+}
+
+// ============================================================== KvCache
+
+extern "C" VtbHipKvCache* vtb_hip_kv_cache_init(VtbHipCtx* ctx, size_t n_layers, size_t n_kv_heads,
+                                                size_t head_dim, size_t max_seq, int dtype) {
+  const int eb = kv_bytes(dtype);
+  if (!ctx || !eb || n_layers == 0 || n_kv_heads == 0 || head_dim == 0 || max_seq == 0) return nullptr;
+  const double total = (double)n_layers * max_seq * n_kv_heads * head_dim * eb;
+  if (total > 1e15) return nullptr;
+  const size_t bytes = n_layers * max_seq * n_kv_heads * head_dim * eb;
+  VtbHipBuf* k = vtb_hip_alloc(ctx, bytes);
+  if (!k) return nullptr;
+  VtbHipBuf* v = vtb_hip_alloc(ctx, bytes);
+  if (!v) {
+    vtb_hip_release(k);
+    return nullptr;
+  }
+  // Unwritten rows are never read (attention stops at pos), but a defined
+  // initial state keeps debugging reads deterministic.
+  (void)hipMemsetAsync(k->ptr, 0, bytes, ctx->stream);
+  (void)hipMemsetAsync(v->ptr, 0, bytes, ctx->stream);
+  return new VtbHipKvCache{ctx, n_layers, n_kv_heads, head_dim, max_seq, dtype, 0, k, v};
+}
+
+extern "C" void vtb_hip_kv_cache_deinit(VtbHipKvCache* c) {
+  if (!c) return;
+  vtb_hip_release(c->k);
+  vtb_hip_release(c->v);
+  delete c;
+}
+
+extern "C" void vtb_hip_kv_cache_reset(VtbHipKvCache* c) {
+  if (c) c->pos = 0;
+}
+
+extern "C" size_t vtb_hip_kv_cache_pos(const VtbHipKvCache* c) { return c ? c->pos : 0; }
+
+extern "C" int vtb_hip_kv_cache_set_pos(VtbHipKvCache* c, size_t pos) {
+  if (!c || pos > c->max_seq) return VTB_HIP_EINVAL;
+  c->pos = pos;
+  return VTB_HIP_OK;
+}
+
+extern "C" size_t vtb_hip_kv_cache_max_seq(const VtbHipKvCache* c) { return c ? c->max_seq : 0; }
+
+extern "C" int vtb_hip_kv_cache_dtype(const VtbHipKvCache* c) { return c ? c->dtype : -1; }
+
+extern "C" int vtb_hip_kv_cache_advance(VtbHipKvCache* c) {
+  if (!c) return VTB_HIP_EINVAL;
+  if (c->pos >= c->max_seq) return VTB_HIP_EFULL;
+  c->pos += 1;
+  return VTB_HIP_OK;
+}
+
+static size_t row_bytes(const VtbHipKvCache* c) { return c->n_kv_heads * c->head_dim * kv_bytes(c->dtype); }
+
+extern "C" size_t vtb_hip_kv_cache_slot_offset(const VtbHipKvCache* c, size_t layer) {
+  if (!c || layer >= c->n_layers || c->pos >= c->max_seq) return (size_t)-1;
+  return (layer * c->max_seq + c->pos) * row_bytes(c);
+}
+
+extern "C" size_t vtb_hip_kv_cache_layer_offset(const VtbHipKvCache* c, size_t layer) {
+  if (!c || layer >= c->n_layers) return (size_t)-1;
+  return layer * c->max_seq * row_bytes(c);
+}
+
+extern "C" VtbHipBuf* vtb_hip_kv_cache_k(VtbHipKvCache* c) { return c ? c->k : nullptr; }
+extern "C" VtbHipBuf* vtb_hip_kv_cache_v(VtbHipKvCache* c) { return c ? c->v : nullptr; }
+
+extern "C" int vtb_hip_kv_cache_shrink_to_fit(VtbHipKvCache* c, size_t new_max_seq) {
+  if (!c) return VTB_HIP_EINVAL;
+  if (new_max_seq >= c->max_seq) return VTB_HIP_OK;
+  if (new_max_seq < c->pos) return VTB_HIP_ESHRINK;
+  if (new_max_seq == 0) return VTB_HIP_EINVAL;
+  VtbHipCtx* ctx = c->ctx;
+  const size_t rb = row_bytes(c);
+  const size_t new_bytes = c->n_layers * new_max_seq * rb;
+  VtbHipBuf* nk = vtb_hip_alloc(ctx, new_bytes);
+  if (!nk) return VTB_HIP_EDEVICE;
+  VtbHipBuf* nv = vtb_hip_alloc(ctx, new_bytes);
+  if (!nv) {
+    vtb_hip_release(nk);
+    return VTB_HIP_EDEVICE;
+  }
+  const size_t live = c->pos * rb;
+  for (size_t l = 0; l < c->n_layers && live > 0; ++l) {
+    const size_t src = l * c->max_seq * rb, dst = l * new_max_seq * rb;
+    if (hipMemcpyAsync(bptr(nk, dst), bptr(c->k, src), live, hipMemcpyDeviceToDevice, ctx->stream) != hipSuccess ||
+        hipMemcpyAsync(bptr(nv, dst), bptr(c->v, src), live, hipMemcpyDeviceToDevice, ctx->stream) != hipSuccess) {
+      vtb_hip_release(nk);
+      vtb_hip_release(nv);
+      return set_err(ctx, VTB_HIP_EDEVICE, "shrink_to_fit: copy failed");
+    }
+  }
+  vtb_hip_release(c->k);  // hipFree waits for the copies above
+  vtb_hip_release(c->v);
+  c->k = nk;
+  c->v = nv;
+  c->max_seq = new_max_seq;
+  return VTB_HIP_OK;
+}
+
+// ============================================================== layer-level entries
+
+static int check_cfg(const VtbHipKvCache* c, const VtbHipAttnConfig* cfg) {
+  if (!c || !cfg) return VTB_HIP_EINVAL;
+  if (cfg->n_kv_heads != c->n_kv_heads || cfg->head_dim != c->head_dim || cfg->n_heads == 0)
+    return VTB_HIP_EINVAL;
+  return VTB_HIP_OK;
+}
+
+extern "C" int vtb_hip_layer_attention(VtbHipSeg* seg, VtbHipKvCache* c, const VtbHipAttnConfig* cfg,
+                                       size_t layer, VtbHipBuf* q, VtbHipBuf* k_cur, VtbHipBuf* v_cur,
+                                       VtbHipBuf* attn_out) {
+  if (!seg) return VTB_HIP_EINVAL;
+  VtbHipCtx* ctx = seg->ctx;
+  int rc = check_cfg(c, cfg);
+  if (rc) return set_err(ctx, rc, "layer_attention: config does not match cache");
+  if (layer >= c->n_layers) return set_err(ctx, VTB_HIP_EINVAL, "layer_attention: layer out of range");
+  if (c->pos >= c->max_seq) return set_err(ctx, VTB_HIP_EFULL, "KvCacheFull");
+  const size_t kv_dim = c->n_kv_heads * c->head_dim;
+  const size_t qn = cfg->n_heads * cfg->head_dim;
+  if (!buf_ok(q, 0, qn * 4) || !buf_ok(attn_out, 0, qn * 4) || !buf_ok(k_cur, 0, kv_dim * 4) ||
+      !buf_ok(v_cur, 0, kv_dim * 4))
+    return set_err(ctx, VTB_HIP_EINVAL, "layer_attention: buffer too small");
+  const size_t slot = vtb_hip_kv_cache_slot_offset(c, layer);
+  rc = launch_append(ctx, bptr(c->k, slot), (const float*)k_cur->ptr, kv_dim, c->dtype);
+  if (!rc) rc = launch_append(ctx, bptr(c->v, slot), (const float*)v_cur->ptr, kv_dim, c->dtype);
+  if (!rc) {
+    const size_t lo = vtb_hip_kv_cache_layer_offset(c, layer);
+    const float inv_sqrt_hd = 1.0f / sqrtf((float)cfg->head_dim);
+    rc = launch_decode(ctx, (float*)attn_out->ptr, (const float*)q->ptr, bptr(c->k, lo), bptr(c->v, lo), 1,
+                       cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, (long long)c->pos,
+                       window_arg(cfg->sliding_window), inv_sqrt_hd, c->dtype);
+  }
+  seg_note(seg, rc);
+  return rc;
+}
+
+extern "C" int vtb_hip_prefill_attention(VtbHipSeg* seg, VtbHipKvCache* c, const VtbHipAttnConfig* cfg,
+                                         size_t layer, size_t n_tokens, VtbHipBuf* q, VtbHipBuf* k_cur,
+                                         VtbHipBuf* v_cur, VtbHipBuf* attn_out) {
+  if (!seg) return VTB_HIP_EINVAL;
+  VtbHipCtx* ctx = seg->ctx;
+  int rc = check_cfg(c, cfg);
+  if (rc) return set_err(ctx, rc, "prefill_attention: config does not match cache");
+  if (layer >= c->n_layers) return set_err(ctx, VTB_HIP_EINVAL, "prefill_attention: layer out of range");
+  if (n_tokens == 0) return VTB_HIP_OK;
+  if (n_tokens > c->max_seq || c->pos + n_tokens > c->max_seq) return set_err(ctx, VTB_HIP_EFULL, "KvCacheFull");
+  const size_t kv_dim = c->n_kv_heads * c->head_dim;
+  const size_t qn = n_tokens * cfg->n_heads * cfg->head_dim;
+  if (!buf_ok(q, 0, qn * 4) || !buf_ok(attn_out, 0, qn * 4) || !buf_ok(k_cur, 0, n_tokens * kv_dim * 4) ||
+      !buf_ok(v_cur, 0, n_tokens * kv_dim * 4))
+    return set_err(ctx, VTB_HIP_EINVAL, "prefill_attention: buffer too small");
+  const size_t slot = vtb_hip_kv_cache_slot_offset(c, layer);
+  rc = launch_append(ctx, bptr(c->k, slot), (const float*)k_cur->ptr, n_tokens * kv_dim, c->dtype);
+  if (!rc) rc = launch_append(ctx, bptr(c->v, slot), (const float*)v_cur->ptr, n_tokens * kv_dim, c->dtype);
+  const size_t lo = vtb_hip_kv_cache_layer_offset(c, layer);
+  const float inv_sqrt_hd = 1.0f / sqrtf((float)cfg->head_dim);
+  const long long w = window_arg(cfg->sliding_window);
+  if (!rc && c->dtype == VTB_HIP_F32) {
+    rc = launch_decode(ctx, (float*)attn_out->ptr, (const float*)q->ptr, bptr(c->k, lo), bptr(c->v, lo),
+                       n_tokens, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, (long long)c->pos, w,
+                       inv_sqrt_hd, c->dtype);
+  } else if (!rc) {
+    // Round q to the cache dtype into the context's scratch, then MFMA.
+    const size_t need = qn * 2;
+    if (need > ctx->qconv_bytes) {
+      if (hipStreamSynchronize(ctx->stream) != hipSuccess) return set_err(ctx, VTB_HIP_EDEVICE, "sync");
+      if (ctx->qconv) (void)hipFree(ctx->qconv);
+      ctx->qconv = nullptr;
+      ctx->qconv_bytes = 0;
+      if (hipMalloc(&ctx->qconv, need) != hipSuccess) return set_err(ctx, VTB_HIP_EDEVICE, "hipMalloc(qconv)");
+      ctx->qconv_bytes = need;
+    }
+    rc = launch_append(ctx, ctx->qconv, (const float*)q->ptr, qn, c->dtype);
+    if (!rc)
+      rc = launch_prefill_mfma(ctx, (float*)attn_out->ptr, ctx->qconv, bptr(c->k, lo), bptr(c->v, lo), n_tokens,
+                               cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, (long long)c->pos, w,
+                               inv_sqrt_hd, c->dtype);
+  }
+  seg_note(seg, rc);
+  return rc;
+}
