@@ -146,6 +146,46 @@ def bench_decode(ctx, torch, args):
     }
 
 
+def prefill_flops(L, n_heads, d):
+    return 4 * n_heads * d * L * (L + 1) // 2
+
+
+def bench_prefill(ctx, torch, n_heads, n_kv, d, L, reps=5, warmup=2):
+    """Causal prefill of L tokens (pos0 = 0), bf16 Q/K/V resident in HBM.
+    Returns the average launch time from HIP events on the context stream."""
+    import numpy as np
+    import vantablack_amd as vb
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(4321)
+    q = torch.randn((L, n_heads * d), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((L, n_kv * d), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((L, n_kv * d), generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty((L, n_heads * d), device=dev)
+    torch.cuda.synchronize()
+    qb, kb, vbuf, ob = ctx.wrap_tensor(q), ctx.wrap_tensor(k), ctx.wrap_tensor(v), ctx.wrap_tensor(out)
+    stream = torch.cuda.ExternalStream(ctx.stream)
+    inv = 1.0 / np.sqrt(d)
+    with ctx.segment() as seg:
+        for _ in range(warmup):
+            seg.attn_prefill(ob, qb, kb, vbuf, 0, L, 0, vb.NO_WINDOW, n_heads, n_kv, d, inv, vb.BF16)
+    ctx.wait_idle()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    with ctx.segment() as seg:
+        for e0, e1 in ev:
+            e0.record(stream)
+            seg.attn_prefill(ob, qb, kb, vbuf, 0, L, 0, vb.NO_WINDOW, n_heads, n_kv, d, inv, vb.BF16)
+            e1.record(stream)
+    ctx.wait_idle()
+    torch.cuda.synchronize()
+    t = sum(e0.elapsed_time(e1) for e0, e1 in ev) / reps * 1e-3
+    fl = prefill_flops(L, n_heads, d)
+    for b in (qb, kb, vbuf, ob):
+        b.release()
+    log(f"prefill h{n_heads}/{n_kv} d{d} L{L}: {t * 1e6:.1f} us/launch -> {fl / t / 1e12:.1f} TFLOP/s")
+    return {"avg_launch_s": t, "flops": fl, "tflops": fl / t / 1e12}
+
+
 def cpu_baseline(seconds_budget=12.0):
     """Time the CPU oracle on a bounded sample of the decode workload: one
     C2 layer at L=8192 (f32 values of the f16 cache, as vantablack's f32
@@ -187,6 +227,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--ctx", type=int, default=8192)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; the path's multi-GPU sharding is "
@@ -197,6 +238,12 @@ def main():
     import vantablack_amd as vb
     ctx = vb.Context()
     dec = bench_decode(ctx, torch, args)
+    pre = {} if args.no_prefill else {
+        "C4_L512": bench_prefill(ctx, torch, 32, 8, 128, 512),
+        "C4_L2048": bench_prefill(ctx, torch, 32, 8, 128, 2048),
+        "C4_L8192": bench_prefill(ctx, torch, 32, 8, 128, 8192),
+        "C5_L4096": bench_prefill(ctx, torch, 8, 1, 256, 4096),
+    }
     cpu = None if args.no_cpu else cpu_baseline()
     ctx.close()
 
@@ -228,6 +275,20 @@ def main():
             "bytes_per_launch": int(dec["bytes_per_launch"]),
         },
     }
+    if pre:
+        p8 = pre["C4_L8192"]
+        line["prefill"] = {
+            "metric": "prefill attn TFLOP/s (% MFMA peak)",
+            "workload": "C4 Llama-3-8B causal prefill: 32q/8kv heads x d128, bf16, 8192 tokens, pos0 0",
+            "value": round(p8["tflops"], 2), "unit": "TFLOP/s",
+            "pct_of_bf16_peak": round(100.0 * p8["tflops"] / BF16_PEAK_TFLOPS, 2),
+            "roofline": {"bound": "mfma", "achieved": round(p8["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(p8["tflops"] / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                         "kernel": "vtb_prefill_bf16_d128", "avg_launch_us": round(p8["avg_launch_s"] * 1e6, 2),
+                         "flops_per_launch": p8["flops"]},
+            "all": {k: {"tflops": round(v["tflops"], 2), "us": round(v["avg_launch_s"] * 1e6, 2)}
+                    for k, v in pre.items()},
+        }
     if cpu:
         line["cpu_baseline"] = {
             "value": round(cpu["pool"]["gbs"], 3), "unit": "GB/s", "cores": cpu["pool"]["workers"],

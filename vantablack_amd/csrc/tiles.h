@@ -18,8 +18,9 @@ constexpr int decode_rows_per_load(int head_dim, int kv_bytes) {
   return 64 / (head_dim * kv_bytes / 16);
 }
 
-// Prefill (MFMA): queries per workgroup and keys per LDS tile, by head_dim.
-constexpr int prefill_block_m(int head_dim) { return head_dim <= 128 ? 128 : 64; }
+// Prefill (MFMA): 4 waves x 32 queries per workgroup; keys per LDS tile by
+// head_dim (the K and V^T tiles stay near 36 KiB of LDS).
+constexpr int prefill_block_m(int) { return 128; }
 constexpr int prefill_block_n(int head_dim) { return head_dim <= 128 ? 64 : 32; }
 
 }  // namespace vtb

@@ -271,7 +271,7 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const void* q, const void* k
     return set_err(ctx, VTB_HIP_EINVAL, "q/K/V not 16-byte aligned");
   const size_t bm = (size_t)vtb::prefill_block_m((int)head_dim);
   const size_t nblk = (n_q + bm - 1) / bm;
-  if (nblk > 0x7fffffff || n_heads > 65535) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "grid too large");
+  if (nblk > 65535 || n_heads > 0x7fffffff) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "grid too large");
   PrefillArgs a;
   memset(&a, 0, sizeof a);
   a.q = q;
@@ -284,7 +284,9 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const void* q, const void* k
   a.pos0 = pos0;
   a.window = window;
   a.scale_log2 = inv_sqrt_hd * 1.4426950408889634f;
-  return launch(ctx, ctx->f_prefill[dtype][di], (unsigned)nblk, (unsigned)n_heads, 1, 256, &a);
+  // x = head (fastest), y = query block: the longest (causal) blocks of every
+  // head are dispatched first.
+  return launch(ctx, ctx->f_prefill[dtype][di], (unsigned)n_heads, (unsigned)nblk, 1, 256, &a);
 }
 
 int launch_append(VtbHipCtx* ctx, void* dst, const float* src, size_t n, int dtype) {
