@@ -4,13 +4,14 @@ Headline (BASELINE.json metric "decode attn HBM GB/s (% of peak) @ctx 8K"):
 Llama-2-7B-shaped full-stack decode (config C2 shapes) at context 8K -- 32
 layers x 32 q heads x 32 KV heads x head_dim 128, f16 KV cache already
 holding 8192 rows.  One step = one decoded token: for each of the 32 layers,
-append the token's K/V row (f32 -> f16) and run decode attention over all
-rows so far; the cache grows by one row per step.
+one launch appends the token's K/V row (f32 -> f16) and runs decode
+attention over all rows so far; the cache grows by one row per step.
 
   value    = algorithmic bytes of all attention launches in the timed steps
              / wall time of those steps (appends and launch gaps included);
-  roofline = the decode kernel alone: algorithmic bytes per launch / its
-             average launch duration from HIP events on the kernel's stream.
+  roofline = the decode kernel: algorithmic bytes per launch / its average
+             launch duration from HIP events on the kernel's stream (a re-run
+             of the same launches bracketed by two events).
 Algorithmic bytes per (layer, step) = 2*L*n_kv*d*sizeof(kv) + n_heads*d*(4+4).
 
 Secondary (metric "prefill attn TFLOP/s (% MFMA peak)"): Llama-3-8B causal
@@ -72,29 +73,26 @@ def bench_decode(ctx, torch, args):
     torch.cuda.synchronize()
 
     kb, vbuf = ctx.wrap_tensor(kc), ctx.wrap_tensor(vc)
-    kcb, vcb = ctx.wrap_tensor(kcur), ctx.wrap_tensor(vcur)
     row_bytes = n_kv * d * 2
     layer_bytes = max_seq * row_bytes
     inv = 1.0 / np.sqrt(d)
-    kvrow_f32 = n_kv * d * 4
 
     # Each layer reads its own q row and writes its own output row.
     qbs = [ctx.wrap_tensor(q[l]) for l in range(n_layers)]
     obs = [ctx.wrap_tensor(out[l]) for l in range(n_layers)]
 
-    def step_layers(seg, s, events=None):
+    # The token's K/V rows per (layer, step), as the f32 k_cur/v_cur views the
+    # fused launch appends.
+    kcs = [[ctx.wrap_tensor(kcur[l, s]) for s in range(total_steps)] for l in range(n_layers)]
+    vcs = [[ctx.wrap_tensor(vcur[l, s]) for s in range(total_steps)] for l in range(n_layers)]
+
+    def step_layers(seg, s):
+        # One launch per layer: KV-slot append fused with decode attention
+        # (forward.zig:466-483 as one call), cache growing by one row per step.
         pos = L0 + s
         for l in range(n_layers):
-            slot = l * layer_bytes + pos * row_bytes
-            src_off = (l * total_steps + s) * kvrow_f32
-            seg.kv_append(kb, slot, vb.F16, kcb, src_off, n_kv * d)
-            seg.kv_append(vbuf, slot, vb.F16, vcb, src_off, n_kv * d)
-            if events is not None:
-                events[s][l][0].record(stream)
-            seg.attn_decode(obs[l], qbs[l], kb, l * layer_bytes, vbuf, l * layer_bytes, n_heads, n_kv, d,
-                            pos + 1, inv, vb.F16)
-            if events is not None:
-                events[s][l][1].record(stream)
+            seg.attn_decode_append(obs[l], qbs[l], kb, l * layer_bytes, vbuf, l * layer_bytes, kcs[l][s], vcs[l][s],
+                                   n_heads, n_kv, d, pos + 1, inv, vb.F16)
 
     with ctx.segment() as seg:
         for s in range(args.warmup):
@@ -113,30 +111,26 @@ def bench_decode(ctx, torch, args):
     alg = sum(n_layers * decode_bytes(L0 + s + 1, n_heads, n_kv, d, 2) for s in range(args.warmup, total_steps))
     value_gbs = alg / wall / 1e9
 
-    # Kernel-only timing: the same launches bracketed by HIP events on the
-    # context stream (the stream the kernel runs on).
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(n_layers)] for _ in range(args.steps)]
-    # Attention only, at the same lengths as the timed steps.
+    # Kernel timing: the same decode launches (same lengths, slot rewritten
+    # with the same rows) bracketed by two HIP events on the context stream,
+    # divided by the launch count -- the launches run back to back, so this
+    # is the kernel's average duration including the inter-kernel gap.
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
     with ctx.segment() as seg:
-        for s in range(args.steps):
-            pos = L0 + args.warmup + s
-            for l in range(n_layers):
-                ev[s][l][0].record(stream)
-                seg.attn_decode(obs[l], qbs[l], kb, l * layer_bytes, vbuf, l * layer_bytes, n_heads, n_kv, d,
-                                pos + 1, inv, vb.F16)
-                ev[s][l][1].record(stream)
+        for s in range(args.warmup, total_steps):
+            step_layers(seg, s)
+    e1.record(stream)
     ctx.wait_idle()
     torch.cuda.synchronize()
-    durs = [ev[s][l][0].elapsed_time(ev[s][l][1]) * 1e-3 for s in range(args.steps) for l in range(n_layers)]
-    avg_launch = sum(durs) / len(durs)
+    avg_launch = e0.elapsed_time(e1) * 1e-3 / (args.steps * n_layers)
     L_mid = L0 + args.warmup + (args.steps + 1) // 2
     per_launch = sum(decode_bytes(L0 + args.warmup + s + 1, n_heads, n_kv, d, 2)
                      for s in range(args.steps)) / args.steps
     achieved = per_launch / avg_launch / 1e9
     log(f"decode: wall {wall * 1e3:.2f} ms for {args.steps} steps, {value_gbs:.1f} GB/s whole-step; "
         f"kernel avg {avg_launch * 1e6:.2f} us/launch -> {achieved:.1f} GB/s")
-    for b in qbs + obs + [kb, vbuf, kcb, vcb]:
+    for b in qbs + obs + [kb, vbuf] + [x for row in kcs + vcs for x in row]:
         b.release()
     del kc, vc
     torch.cuda.empty_cache()
@@ -271,7 +265,8 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(dec["achieved_gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(dec["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "vtb_decode_f16_d128_g1", "avg_launch_us": round(dec["avg_launch_s"] * 1e6, 3),
+            "kernel": "vtb_decode_f16_d128_g1 (KV append fused)",
+            "avg_launch_us": round(dec["avg_launch_s"] * 1e6, 3),
             "bytes_per_launch": int(dec["bytes_per_launch"]),
         },
     }

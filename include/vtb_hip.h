@@ -124,6 +124,19 @@ void vtb_hip_segment_attn_decode(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *
                                  size_t n_heads, size_t n_kv_heads, size_t head_dim,
                                  size_t seq_len, float inv_sqrt_hd, int kv_dtype);
 
+/* Decode with the KV-slot append fused into the same launch: writes k_cur /
+ * v_cur (f32 [n_kv_heads*head_dim]), rounded to kv_dtype, into row
+ * seq_len-1 of the K/V views at the given offsets, then computes exactly
+ * what vtb_hip_segment_attn_decode computes over rows [0, seq_len).
+ * Replaces the Metal sequence seg.copy(kv_k slot), seg.copy(kv_v slot),
+ * attention trio (forward.zig:466-483) with one launch. */
+void vtb_hip_segment_attn_decode_append(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *q_buf,
+                                        VtbHipBuf *k_cache_buf, size_t k_cache_offset_bytes,
+                                        VtbHipBuf *v_cache_buf, size_t v_cache_offset_bytes,
+                                        VtbHipBuf *k_cur_buf, VtbHipBuf *v_cur_buf,
+                                        size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                        size_t seq_len, float inv_sqrt_hd, int kv_dtype);
+
 /* Causal prefill attention for n_tokens queries of one layer.  Query b sits
  * at absolute position pos0 + b and attends rows [window_start(pos0+b),
  * pos0+b] of the layer whose row 0 is at layer_offset_bytes in k/v, where
@@ -168,7 +181,8 @@ int vtb_hip_kv_cache_shrink_to_fit(VtbHipKvCache *cache, size_t new_max_seq);
  * Decode, one layer (forward.zig:267-270 then cpuAttention :187-228): write
  * k_cur/v_cur (f32 [n_kv_heads*head_dim]) into the slot at cache->pos, then
  * attend [window_start(pos), pos] with q (f32 [n_heads*head_dim]) into
- * attn_out (f32).  Does not advance pos (stepWithBackend advances once after
+ * attn_out (f32), in one launch (the slot write is fused into the decode
+ * kernel).  Does not advance pos (stepWithBackend advances once after
  * all layers, forward.zig:168).  3 if pos >= max_seq. */
 int vtb_hip_layer_attention(VtbHipSeg *seg, VtbHipKvCache *cache, const VtbHipAttnConfig *c,
                             size_t layer, VtbHipBuf *q, VtbHipBuf *k_cur, VtbHipBuf *v_cur,

@@ -59,10 +59,12 @@ def test_decode_shapes(ctx, orc, dtype, n_heads, n_kv, d):
     decode_case(ctx, orc, n_heads, n_kv, d, pos=777, dtype=dtype, seed=n_heads + d)
 
 
+@pytest.mark.parametrize("n_kv", [2, 8])
 @pytest.mark.parametrize("pos", [0, 1, 2, 31, 32, 33, 127, 128, 129, 1023, 4095, 9000])
-def test_decode_lengths(ctx, orc, pos):
-    # L = pos+1 runs through single-row, partial tiles, tile edges and many splits.
-    decode_case(ctx, orc, 8, 2, 128, pos=pos, dtype="f16", seed=pos)
+def test_decode_lengths(ctx, orc, pos, n_kv):
+    # L = pos+1 runs through single-row, partial tiles, tile edges and many
+    # splits, for GQA (n_kv 2) and MHA (n_kv 8: the row-major MHA kernel).
+    decode_case(ctx, orc, 8, n_kv, 128, pos=pos, dtype="f16", seed=pos)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -182,3 +184,42 @@ def test_bad_arguments_are_reported(ctx):
     with pytest.raises(vb.HipError) as e:
         seg.commit()
     assert e.value.rc == 1
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_fused_append_matches_separate_calls(ctx, orc, dtype):
+    """vtb_hip_segment_attn_decode_append == kv_append(K) + kv_append(V) +
+    attn_decode, bit for bit, for both the output and the cache contents."""
+    import vantablack_amd as vb
+    n_heads, n_kv, d, L = 16, 4, 128, 2500
+    ks, kx, vs, vx = make_kv(orc, L, n_kv, d, dtype, seed=12)
+    q = orc.normal(13, n_heads * d)
+    k_new, v_new = orc.normal(14, n_kv * d), orc.normal(15, n_kv * d)
+    dt = vb.hip.DTYPES[dtype]
+    row = n_kv * d * (4 if dtype == "f32" else 2)
+    outs, caches = [], []
+    for fused in (False, True):
+        kb, vbuf = ctx.to_device(ks), ctx.to_device(vs)
+        qb, kn, vn, ob = ctx.to_device(q), ctx.to_device(k_new), ctx.to_device(v_new), ctx.alloc(n_heads * d * 4)
+        with ctx.segment() as seg:
+            if fused:
+                seg.attn_decode_append(ob, qb, kb, 0, vbuf, 0, kn, vn, n_heads, n_kv, d, L, 1.0 / np.sqrt(d), dt)
+            else:
+                seg.kv_append(kb, (L - 1) * row, dt, kn, 0, n_kv * d)
+                seg.kv_append(vbuf, (L - 1) * row, dt, vn, 0, n_kv * d)
+                seg.attn_decode(ob, qb, kb, 0, vbuf, 0, n_heads, n_kv, d, L, 1.0 / np.sqrt(d), dt)
+        outs.append(ctx.download(ob, np.float32, n_heads * d))
+        npd = np.float32 if dtype == "f32" else np.uint16
+        caches.append((ctx.download(kb, npd, L * n_kv * d), ctx.download(vbuf, npd, L * n_kv * d)))
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(caches[0][0], caches[1][0]) and np.array_equal(caches[0][1], caches[1][1])
+    # and against the oracle with the appended row in place
+    kx2, vx2 = kx.copy(), vx.copy()
+    kx2[L - 1] = orc.to_dtype(k_new, dtype)[1].reshape(n_kv, d)
+    vx2[L - 1] = orc.to_dtype(v_new, dtype)[1].reshape(n_kv, d)
+    oc = orc.OracleKvCache(1, n_kv, d, L)
+    oc.layer_rows("k", 0)[:] = kx2
+    oc.layer_rows("v", 0)[:] = vx2
+    oc.pos = L - 1
+    check(orc, outs[1], orc.cpu_attention(q, oc, orc.config(n_heads, n_kv, d, L), 0), n_heads, dtype,
+          what="fused append")

@@ -18,8 +18,8 @@
 //   registers: the next tile's loads are issued before this tile's math.
 //   Scores are reduced across the LPR lanes with DPP adds; the softmax is
 //   online (running max m, sum l, accumulator acc) per wave, in registers.
-//   The waves combine into one (m, l, o) partial per workgroup with LDS
-//   float atomics after agreeing on the workgroup max.  The last-arriving
+//   The waves combine into one (m, l, o) partial per workgroup through
+//   per-wave LDS slots summed in a fixed order.  The last-arriving
 //   workgroup of each (query, KV head) merges the partials (log-sum-exp),
 //   loading them in independent batches, and writes out[h] = o/l.  It resets
 //   the arrival counter to zero, so no memset is needed between launches.
@@ -54,6 +54,8 @@ struct DecodeArgs {
   long long window;     // sliding window in rows; <= 0 disables it
   float scale_log2;     // (1/sqrt(D)) * log2(e)
   int pad;
+  const float* k_new;   // optional (decode only): f32 K/V row appended at
+  const float* v_new;   //   row pos0 before attention; null when not fused
 };
 
 template <typename KV, int D, int G, int NIT, int NW>
@@ -66,8 +68,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
   static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "bad row split");
 
   __shared__ float s_m[NW][G];
-  __shared__ float s_l[G];
-  __shared__ float s_o[G][D];
+  __shared__ float s_l[NW][G];
+  __shared__ float s_o[NW][G][D];
   __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
@@ -90,8 +92,21 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
   const int gs = h_hi - h_lo;
   if (gs <= 0) return;
 
-  for (int i = threadIdx.x; i < G * D; i += NT) (&s_o[0][0])[i] = 0.0f;
-  if (threadIdx.x < G) s_l[threadIdx.x] = 0.0f;
+
+  // Fused KV-slot append (forward.zig:267-270): the workgroup whose rows
+  // include the new row pos0 writes this KV head's K and V slice of it,
+  // rounded to the cache dtype, before any of its waves reads it.  Only this
+  // workgroup reads that slice, and the stores complete (vmcnt 0) before the
+  // barrier, so the later loads from the same CU see them.
+  if (a.k_new != nullptr && a.pos0 >= r0 && a.pos0 < r1) {
+    const long long off = a.pos0 * (long long)a.n_kv * D + (long long)kvh * D;
+    for (int i = threadIdx.x; i < D; i += NT) {
+      store_kv<KV>((void*)a.k, off + i, a.k_new[(long long)kvh * D + i]);
+      store_kv<KV>((void*)a.v, off + i, a.v_new[(long long)kvh * D + i]);
+    }
+    wait_stores();
+    __syncthreads();
+  }
 
   const int col = lane % LPR;
   const int rsub = lane / LPR;
@@ -206,29 +221,18 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
 #pragma unroll
     for (int e = 0; e < EPL; ++e) acc[g][e] = stride_sum<LPR>(acc[g][e]);
   }
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) s_m[wave][g] = m[g];
-  }
-  __syncthreads();
-
-  // Workgroup combine: rescale each wave to the workgroup max and add into
-  // LDS.  A wave with no rows has m = -inf and contributes nothing.
-  float M[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float mm = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) mm = fmaxf(mm, s_m[w][g]);
-    M[g] = mm;
-  }
-  if (w0 < w1 && rsub == 0) {
+  // Each wave parks (m, l, acc) in its own LDS slot; the workgroup combine
+  // then sums the waves in a fixed order, so results are bit-reproducible.
+  // A wave with no rows has m = -inf and contributes nothing.
+  if (rsub == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float f = exp2_fast(m[g] - M[g]);
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) atomicAdd(&s_o[g][col * EPL + e], acc[g][e] * f);
-      if (col == 0) atomicAdd(&s_l[g], l[g] * f);
+      for (int e = 0; e < EPL; ++e) s_o[wave][g][col * EPL + e] = acc[g][e];
+      if (col == 0) {
+        s_m[wave][g] = m[g];
+        s_l[wave][g] = l[g];
+      }
     }
   }
   __syncthreads();
@@ -238,16 +242,27 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
   for (int idx = threadIdx.x; idx < G * D; idx += NT) {
     const int g = idx / D, d = idx % D;
     if (g >= gs) continue;
+    float Mg = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) Mg = fmaxf(Mg, s_m[w][g]);
+    float Lg = 0.0f, Og = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      if (s_m[w][g] == -INFINITY) continue;
+      const float f = exp2_fast(s_m[w][g] - Mg);
+      Lg += s_l[w][g] * f;
+      Og += s_o[w][g][d] * f;
+    }
     if (single) {
-      a.out[((long long)b * a.n_heads + h_lo + g) * D + d] = s_o[g][d] / s_l[g];
+      a.out[((long long)b * a.n_heads + h_lo + g) * D + d] = Og / Lg;
     } else {
       // Agent-scope atomic stores are coherent across the XCDs' L2s, so the
       // partials need no cache-wide writeback (a __threadfence() here costs
       // a full L2 writeback + invalidate per workgroup on this chip).
-      store_coherent(&a.ws_o[(part * G + g) * D + d], s_o[g][d]);
+      store_coherent(&a.ws_o[(part * G + g) * D + d], Og);
       if (d == 0) {
-        store_coherent(&a.ws_ml[(part * G + g) * 2 + 0], M[g]);
-        store_coherent(&a.ws_ml[(part * G + g) * 2 + 1], s_l[g]);
+        store_coherent(&a.ws_ml[(part * G + g) * 2 + 0], Mg);
+        store_coherent(&a.ws_ml[(part * G + g) * 2 + 1], Lg);
       }
     }
   }

@@ -13,18 +13,6 @@
 
 namespace vtb {
 
-__device__ inline uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
-__device__ inline uint16_t f32_to_f16_rne(float f) {
-  _Float16 h = (_Float16)f;  // v_cvt_f16_f32: round to nearest even
-  return __builtin_bit_cast(uint16_t, h);
-}
-
 struct AppendArgs {
   void* dst;         // already offset to the first destination element
   const float* src;

@@ -7,11 +7,17 @@ namespace vtb {
 // Decode: 16-byte loads per lane per wave tile (NIT), by GQA group width.
 // Tiles are double-buffered, so a wave keeps 2 x 2 x NIT loads in flight;
 // NIT shrinks as the group widens to keep the q/acc registers resident.
-constexpr int decode_nit(int g) { return g <= 4 ? 4 : (g == 8 ? 2 : 1); }
+#ifndef VTB_DECODE_NIT1
+#define VTB_DECODE_NIT1 4
+#endif
+#ifndef VTB_DECODE_WAVES1
+#define VTB_DECODE_WAVES1 16
+#endif
+constexpr int decode_nit(int g) { return g == 1 ? VTB_DECODE_NIT1 : g <= 4 ? 4 : (g == 8 ? 2 : 1); }
 
 // Waves per decode workgroup: as many as the register budget allows
 // (16 waves = 4 per SIMD needs <= 128 registers per lane).
-constexpr int decode_waves(int g) { return g == 1 ? 16 : (g <= 8 ? 8 : 4); }
+constexpr int decode_waves(int g) { return g == 1 ? VTB_DECODE_WAVES1 : (g <= 8 ? 8 : 4); }
 
 // Rows read by one wave load instruction (the split granularity).
 constexpr int decode_rows_per_load(int head_dim, int kv_bytes) {

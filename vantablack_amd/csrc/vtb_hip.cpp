@@ -54,6 +54,8 @@ struct DecodeArgs {
   long long window;
   float scale_log2;
   int pad;
+  const float* k_new;
+  const float* v_new;
 };
 
 // Arguments of vtb_prefill_* (layout must match PrefillArgs in prefill.hip).
@@ -199,9 +201,12 @@ int env_int(const char* name, int dflt) {
 
 // Split-K decode / f32 prefill launcher.  Queries b in [0, n_q) sit at
 // pos0 + b and attend [window_start, pos0 + b] of the layer rows at k/v.
+// With k_new/v_new (decode, n_q == 1) the kernel first writes that f32 row,
+// rounded to the cache dtype, into row pos0 (the fused KV-slot append).
 int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, const void* v,
                   size_t n_q, size_t n_heads, size_t n_kv, size_t head_dim, long long pos0,
-                  long long window, float inv_sqrt_hd, int dtype) {
+                  long long window, float inv_sqrt_hd, int dtype, const float* k_new = nullptr,
+                  const float* v_new = nullptr) {
   const int di = d_index(head_dim);
   if (di < 0) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "head_dim must be 64, 128 or 256");
   if (dtype < 0 || dtype >= kNumKv) return set_err(ctx, VTB_HIP_EINVAL, "bad kv dtype");
@@ -227,7 +232,8 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
   // one wave load instruction covers.
   const long long quantum = vtb::decode_rows_per_load((int)head_dim, kKvBytes[dtype]);
   const long long target = env_int("VTB_DECODE_TARGET_WGS", std::max(ctx->cu_count, 1));
-  long long want = std::max(1LL, (target + (long long)(n_kv * n_q) - 1) / (long long)(n_kv * n_q));
+  const long long units = (long long)(n_kv * n_q);
+  long long want = std::max(1LL, (target + units - 1) / units);
   long long rps = (Lmax + want - 1) / want;
   rps = std::max(quantum, (rps + quantum - 1) / quantum * quantum);
   long long n_splits = (Lmax + rps - 1) / rps;
@@ -254,6 +260,9 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
   a.pos0 = pos0;
   a.window = window;
   a.scale_log2 = inv_sqrt_hd * 1.4426950408889634f;
+  if (k_new && (n_q != 1 || !v_new)) return set_err(ctx, VTB_HIP_EINVAL, "fused append needs one query");
+  a.k_new = k_new;
+  a.v_new = v_new;
   return launch(ctx, ctx->f_decode[dtype][di][gi], (unsigned)n_splits, (unsigned)n_kv,
                 (unsigned)n_q, 64 * vtb::decode_waves(G), &a);
 }
@@ -513,6 +522,31 @@ extern "C" void vtb_hip_segment_attn_decode(VtbHipSeg* seg, VtbHipBuf* out_buf, 
                               head_dim, (long long)seq_len - 1, 0, inv_sqrt_hd, kv_dtype));
 }
 
+extern "C" void vtb_hip_segment_attn_decode_append(
+    VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* q_buf, VtbHipBuf* k_cache_buf, size_t k_cache_offset_bytes,
+    VtbHipBuf* v_cache_buf, size_t v_cache_offset_bytes, VtbHipBuf* k_cur_buf, VtbHipBuf* v_cur_buf,
+    size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t seq_len, float inv_sqrt_hd, int kv_dtype) {
+  if (!seg) return;
+  VtbHipCtx* ctx = seg->ctx;
+  const int eb = kv_bytes(kv_dtype);
+  if (!eb || n_heads == 0 || n_kv_heads == 0 || head_dim == 0 || n_heads > 65535 ||
+      n_kv_heads > 65535 || head_dim > 4096 || seq_len == 0)
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_decode_append: bad shape"));
+  const size_t qbytes = n_heads * head_dim * 4;
+  const size_t kv_dim = n_kv_heads * head_dim;
+  if (!buf_ok(out_buf, 0, qbytes) || !buf_ok(q_buf, 0, qbytes) || !buf_ok(k_cur_buf, 0, kv_dim * 4) ||
+      !buf_ok(v_cur_buf, 0, kv_dim * 4))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_decode_append: q/out/k_cur/v_cur too small"));
+  const size_t kv_rows_bytes = seq_len * kv_dim * eb;
+  if (!buf_ok(k_cache_buf, k_cache_offset_bytes, kv_rows_bytes) ||
+      !buf_ok(v_cache_buf, v_cache_offset_bytes, kv_rows_bytes))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_decode_append: K/V range outside buffer"));
+  seg_note(seg, launch_decode(ctx, (float*)out_buf->ptr, (const float*)q_buf->ptr,
+                              bptr(k_cache_buf, k_cache_offset_bytes), bptr(v_cache_buf, v_cache_offset_bytes),
+                              1, n_heads, n_kv_heads, head_dim, (long long)seq_len - 1, 0, inv_sqrt_hd,
+                              kv_dtype, (const float*)k_cur_buf->ptr, (const float*)v_cur_buf->ptr));
+}
+
 extern "C" void vtb_hip_segment_attn_prefill(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* q_buf,
                                              VtbHipBuf* k_cache_buf, VtbHipBuf* v_cache_buf,
                                              size_t layer_offset_bytes, size_t n_tokens, size_t pos0,
@@ -671,16 +705,14 @@ extern "C" int vtb_hip_layer_attention(VtbHipSeg* seg, VtbHipKvCache* c, const V
   if (!buf_ok(q, 0, qn * 4) || !buf_ok(attn_out, 0, qn * 4) || !buf_ok(k_cur, 0, kv_dim * 4) ||
       !buf_ok(v_cur, 0, kv_dim * 4))
     return set_err(ctx, VTB_HIP_EINVAL, "layer_attention: buffer too small");
-  const size_t slot = vtb_hip_kv_cache_slot_offset(c, layer);
-  rc = launch_append(ctx, bptr(c->k, slot), (const float*)k_cur->ptr, kv_dim, c->dtype);
-  if (!rc) rc = launch_append(ctx, bptr(c->v, slot), (const float*)v_cur->ptr, kv_dim, c->dtype);
-  if (!rc) {
-    const size_t lo = vtb_hip_kv_cache_layer_offset(c, layer);
-    const float inv_sqrt_hd = 1.0f / sqrtf((float)cfg->head_dim);
-    rc = launch_decode(ctx, (float*)attn_out->ptr, (const float*)q->ptr, bptr(c->k, lo), bptr(c->v, lo), 1,
-                       cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, (long long)c->pos,
-                       window_arg(cfg->sliding_window), inv_sqrt_hd, c->dtype);
-  }
+  // One launch: the decode kernel writes the slot at pos (fused append),
+  // then attends [window_start(pos), pos].
+  const size_t lo = vtb_hip_kv_cache_layer_offset(c, layer);
+  const float inv_sqrt_hd = 1.0f / sqrtf((float)cfg->head_dim);
+  rc = launch_decode(ctx, (float*)attn_out->ptr, (const float*)q->ptr, bptr(c->k, lo), bptr(c->v, lo), 1,
+                     cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, (long long)c->pos,
+                     window_arg(cfg->sliding_window), inv_sqrt_hd, c->dtype, (const float*)k_cur->ptr,
+                     (const float*)v_cur->ptr);
   seg_note(seg, rc);
   return rc;
 }

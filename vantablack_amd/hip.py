@@ -29,7 +29,8 @@ import weakref
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libvtb_hip.so")
+# VTB_HIP_LIB selects another build of the same library (tuning variants).
+LIB_PATH = os.environ.get("VTB_HIP_LIB") or os.path.join(_HERE, "libvtb_hip.so")
 
 OK, EINVAL, EDEVICE, EFULL, ESHRINK, EUNSUPPORTED = 0, 1, 2, 3, 4, 5
 F32, F16, BF16 = 0, 1, 2
@@ -82,6 +83,7 @@ SIGNATURES = {
     "vtb_hip_segment_copy": ([_P, _P, _S, _P, _S, _S], None),
     "vtb_hip_segment_kv_append": ([_P, _P, _S, _I, _P, _S, _S], None),
     "vtb_hip_segment_attn_decode": ([_P, _P, _P, _P, _S, _P, _S, _S, _S, _S, _S, _F, _I], None),
+    "vtb_hip_segment_attn_decode_append": ([_P, _P, _P, _P, _S, _P, _S, _P, _P, _S, _S, _S, _S, _F, _I], None),
     "vtb_hip_segment_attn_prefill": ([_P, _P, _P, _P, _P, _S, _S, _S, _S, _S, _S, _S, _F, _I], None),
     "vtb_hip_kv_cache_init": ([_P, _S, _S, _S, _S, _I], _P),
     "vtb_hip_kv_cache_deinit": ([_P], None),
@@ -192,6 +194,12 @@ class Segment:
                     kv_dtype: int):
         lib().vtb_hip_segment_attn_decode(self.h, out.h, q.h, k.h, k_off, v.h, v_off, n_heads,
                                           n_kv_heads, head_dim, seq_len, inv_sqrt_hd, kv_dtype)
+
+    def attn_decode_append(self, out: Buffer, q: Buffer, k: Buffer, k_off: int, v: Buffer, v_off: int,
+                           k_cur: Buffer, v_cur: Buffer, n_heads: int, n_kv_heads: int, head_dim: int,
+                           seq_len: int, inv_sqrt_hd: float, kv_dtype: int):
+        lib().vtb_hip_segment_attn_decode_append(self.h, out.h, q.h, k.h, k_off, v.h, v_off, k_cur.h, v_cur.h,
+                                                 n_heads, n_kv_heads, head_dim, seq_len, inv_sqrt_hd, kv_dtype)
 
     def attn_prefill(self, out: Buffer, q: Buffer, k: Buffer, v: Buffer, layer_off: int, n_tokens: int,
                      pos0: int, sliding_window: int, n_heads: int, n_kv_heads: int, head_dim: int,
