@@ -27,8 +27,13 @@ def downstream_argmax(orc, out: np.ndarray, n_rows: int, seed: int = 777) -> np.
 
 
 def check(orc, got, ref, n_heads, dtype, n_queries=1, what=""):
+    fin = np.isfinite(np.asarray(got, np.float64).reshape(n_queries, n_heads, -1))
+    if not fin.all():
+        bad = np.argwhere(~fin)
+        raise AssertionError(f"{what}: {len(bad)} non-finite outputs; first (query, head, dim) "
+                             f"{bad[:6].tolist()}; queries {np.unique(bad[:, 0])[:10].tolist()} "
+                             f"heads {np.unique(bad[:, 1])[:10].tolist()}")
     err = rel_err(got, ref, n_heads * n_queries)
-    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
     assert err <= TOL[dtype], f"{what}: rel err {err:.3e} > {TOL[dtype]:.0e}"
     if dtype != "f32":
         a = downstream_argmax(orc, got, n_queries)

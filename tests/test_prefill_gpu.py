@@ -166,6 +166,46 @@ def test_prefill_attention_layer_entry(ctx, orc):
     check(orc, got, ref, n_heads, "bf16", n_queries=B, what="prefill layer entry")
 
 
+def test_prefill_scratch_survives_qconv_growth(ctx, orc):
+    """Regression: growing the q-conversion scratch (layer-level prefill with a
+    longer prompt) must leave the V^T scratch allocated.  Buffers allocated
+    afterwards must stay untouched by repeated prefills, and repeats agree."""
+    import vantablack_amd as vb
+    n_heads, n_kv, d = 8, 2, 128
+    own = vb.Context()  # a fresh context: its scratch buffers start unallocated
+    try:
+        assert prefill_case(own, orc, n_heads, n_kv, d, "bf16", 64, seed=71) <= 2e-3  # V^T scratch exists
+        for B in (16, 200):  # the second call grows the q scratch
+            cache = vb.KvCache(own, 1, n_kv, d, 256, "bf16")
+            try:
+                c = vb.LlamaConfig(n_heads, n_kv, d, 256, vb.NO_WINDOW)
+                kv = orc.normal(72, B * n_kv * d)
+                with own.segment() as seg:
+                    vb.prefill_attention(seg, cache, c, 0, B, own.to_device(orc.normal(73, B * n_heads * d)),
+                                         own.to_device(kv), own.to_device(kv), own.alloc(B * n_heads * d * 4))
+                own.wait_idle()
+            finally:
+                cache.close()
+        B = 256
+        vs = orc.to_dtype(orc.normal(74, B * n_kv * d), "bf16")[0]
+        ks = orc.to_dtype(orc.normal(75, B * n_kv * d), "bf16")[0]
+        qs = orc.to_dtype(orc.normal(76, B * n_heads * d), "bf16")[0]
+        vbuf, kb, qb = own.to_device(vs), own.to_device(ks), own.to_device(qs)
+        outs = []
+        for _ in range(3):
+            ob = own.alloc(B * n_heads * d * 4)
+            with own.segment() as seg:
+                seg.attn_prefill(ob, qb, kb, vbuf, 0, B, 0, vb.NO_WINDOW, n_heads, n_kv, d, 1 / np.sqrt(d),
+                                 vb.BF16)
+            outs.append(own.download(ob, np.float32, B * n_heads * d))
+        assert np.array_equal(own.download(vbuf, vs.dtype, vs.size), vs), "V input overwritten"
+        assert np.array_equal(own.download(kb, ks.dtype, ks.size), ks), "K input overwritten"
+        assert all(np.array_equal(outs[0], o) for o in outs[1:]), "repeated prefill differs"
+        assert np.isfinite(outs[0]).all()
+    finally:
+        own.close()
+
+
 def _sample_rows(B, bm=128):
     rows = {0, 1, B - 1, B - 2, B // 2}
     for blk in (1, 2, B // bm - 1):

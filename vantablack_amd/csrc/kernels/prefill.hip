@@ -6,23 +6,35 @@
 //   out[b,h] = sum_t softmax_t(q[b,h].K[t,kv_h] / sqrt(D)) V[t,kv_h]
 // over t in [window_start(pos0+b), pos0+b], kv_h = (h*n_kv)/n_heads.
 //
-// Flash-attention formulation, transposed so that every lane owns one query:
-//   S^T = K Q^T        v_mfma_f32_32x32x16_{bf16,f16}; A = K rows from LDS,
-//                      B = Q^T kept in registers for the whole key loop.
-//   online softmax     the 32x32 accumulator layout puts one query per lane
-//                      column (lane % 32) and 16 keys per lane, so row max /
-//                      row sum need one cross-lane step (lane ^ 32).
-//   O^T += V^T P^T     v_mfma_f32_32x32x16_f16; B = P^T straight from the S^T
-//                      accumulators (rounded to f16), A = V^T from LDS.  The
-//                      V^T tile is stored with its key columns permuted so the
-//                      8 keys a lane holds in P^T are 8 contiguous f16 in LDS.
-// P is rounded to f16 (not bf16: 11 vs 8 significant bits), and a bf16 V is
-// converted to f16 while it is transposed into LDS (exact for |v| in f16's
-// normal range; the cache dtype's values are carried over unchanged).
+// Two kernels per call:
+//   vtb_vt_<dt>_d<D>       V pre-pass: writes V^T as f16, [kv_h][d][key],
+//                          keys permuted inside each 16-key group (vt_col),
+//                          zero-padded to a whole number of key tiles.  A bf16
+//                          V is converted to f16 here (exact for |v| in f16's
+//                          normal range).  One pass over V: ~5 us at 8K keys.
+//   vtb_prefill_<dt>_d<D>  flash attention, transposed so that every lane
+//                          owns one query:
+//     S^T = K Q^T          v_mfma_f32_32x32x16_{bf16,f16}; A = K rows from LDS,
+//                          B = Q^T kept in registers for the whole key loop.
+//     online softmax       the 32x32 accumulator puts one query per lane
+//                          column (lane % 32) and 16 keys per lane, so the row
+//                          max / sum need one cross-lane step (lane ^ 32).
+//                          Rescaling of O is lazy: the running max is only
+//                          raised when a row's max grows by more than 2^8, so
+//                          P stays <= 256 (well inside f16) and most tiles skip
+//                          the O multiply.
+//     O^T += V^T P^T       v_mfma_f32_32x32x16_f16; B = P^T straight from the
+//                          S^T accumulators (rounded to f16), A = V^T from LDS.
+//                          The pre-pass permutation makes the 8 keys a lane
+//                          holds in P^T 8 contiguous f16 of a V^T row.
+// P is rounded to f16 (11 significant bits; bf16's 8 bits would give ~2e-3
+// relative error, at the parity bar).
 //
-// Workgroup = 4 waves x 32 queries = BM queries of one head; key tiles of BN
-// rows stream through LDS with the next tile prefetched into registers.
-// Tiles entirely above a wave's diagonal or before its window are skipped.
+// Workgroup = 4 waves x 32 queries = 128 queries of one head; key tiles of BN
+// rows stream through LDS (K row-major, V^T row-major, both padded so the
+// 16-byte MFMA operand reads and the tile stores are bank-conflict free),
+// with the next tile prefetched into registers.  Tiles entirely above a
+// wave's diagonal or before its window are skipped.
 #include "common.h"
 #include "../tiles.h"
 
@@ -31,16 +43,25 @@ namespace vtb {
 struct PrefillArgs {
   const void* q;       // [n_q][n_heads][D] of DT
   const void* k;       // layer base: row t at k + t*n_kv*D elements
-  const void* v;
+  const _Float16* vt;  // V^T from the pre-pass: [n_kv][D][vt_ld]
   float* out;          // [n_q][n_heads][D] f32
   int n_q;
   int n_heads;
   int n_kv;
-  int pad0;
+  int vt_ld;           // keys per V^T row (multiple of BN, >= pos0 + n_q)
   long long pos0;      // absolute position of query 0
   long long window;    // sliding window in rows; <= 0 disables it
   float scale_log2;    // (1/sqrt(D)) * log2(e)
   int pad1;
+};
+
+struct VtArgs {
+  const void* v;       // layer base: row t at v + t*n_kv*D elements
+  _Float16* vt;        // [n_kv][D][vt_ld]
+  int n_rows;          // rows of V to transpose; keys >= n_rows are zero
+  int n_kv;
+  int vt_ld;
+  int pad;
 };
 
 template <typename DT> struct Mfma;
@@ -66,25 +87,62 @@ __device__ inline f32x16 mfma_pv(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// Column of key x (0..15 within a 16-key step) in the V^T tile: swaps the
-// middle two 4-key groups, so lane half hi reads keys {4hi..4hi+3,
-// 8+4hi..8+4hi+3} -- the keys its P^T fragment holds -- as 8 contiguous f16.
+// Column of key x (0..15 within a 16-key group) in V^T: swaps the middle two
+// 4-key groups, so lane half hi reads keys {4hi..4hi+3, 8+4hi..8+4hi+3} --
+// exactly the keys its P^T fragment holds -- as 8 contiguous f16.  The map is
+// its own inverse.
 __device__ inline int vt_col(int x) { return 8 * ((x >> 2) & 1) + 4 * (x >> 3) + (x & 3); }
 
+// ---------------------------------------------------------------- pre-pass
+template <typename DT, int D>
+__device__ __forceinline__ void vt_body(const VtArgs& a) {
+  constexpr int TK = 64;            // keys per workgroup
+  constexpr int TP = D + 8;         // LDS pitch (f16)
+  __shared__ __attribute__((aligned(16))) _Float16 tile[TK * TP];
+  const int tid = threadIdx.x;
+  const int kvh = blockIdx.y;
+  const long long key0 = (long long)blockIdx.x * TK;
+  const long long row_stride = (long long)a.n_kv * D;
+  const uint16_t* vg = (const uint16_t*)a.v + (long long)kvh * D;
+  // Load 64 keys x D dims (16-byte chunks), convert to f16, stage row-major.
+  for (int c = tid; c < TK * D / 8; c += 256) {
+    const int key = c / (D / 8), dc = (c % (D / 8)) * 8;
+    u32x4 w = {0u, 0u, 0u, 0u};
+    if (key0 + key < a.n_rows) w = load16(vg + (key0 + key) * row_stride + dc);
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    f16x8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = Mfma<DT>::to_f16((uint16_t)(ww[e >> 1] >> (16 * (e & 1))));
+    *reinterpret_cast<f16x8*>(&tile[key * TP + dc]) = h;
+  }
+  __syncthreads();
+  // Write V^T rows: output column o of a 16-key group holds key vt_col(o).
+  for (int c = tid; c < D * TK / 8; c += 256) {
+    const int d = c / (TK / 8), o0 = (c % (TK / 8)) * 8;
+    f16x8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int o = o0 + e;
+      h[e] = tile[(16 * (o >> 4) + vt_col(o & 15)) * TP + d];
+    }
+    *reinterpret_cast<f16x8*>(a.vt + ((long long)kvh * D + d) * a.vt_ld + key0 + o0) = h;
+  }
+}
+
+// ---------------------------------------------------------------- attention
 template <typename DT, int D>
 __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   constexpr int BM = prefill_block_m(D);      // queries per workgroup (4 waves x 32)
   constexpr int BN = prefill_block_n(D);      // keys per tile
-  constexpr int KP = D + 8;                   // K tile row pitch (f16/bf16 elements)
-  constexpr int VP = BN + 8;                  // V^T tile row pitch
-  constexpr int KCH = BN * D / 8;             // 16-byte chunks per K (or V) tile
-  constexpr int KPT = (KCH + 255) / 256;      // K chunks per thread
-  constexpr int VBLK = (BN / 4) * (D / 8);    // 4-row x 8-col V blocks per tile
+  constexpr int KP = D + 8;                   // K tile row pitch (elements)
+  constexpr int VP = BN + 8;                  // V^T tile row pitch (f16)
+  constexpr int KCH = BN * D / 8;             // 16-byte chunks per K (and V^T) tile
+  constexpr int CPT = KCH / 256;              // chunks per thread
   constexpr int NS = BN / 32;                 // 32-key S^T tiles per key tile
   constexpr int ND = D / 32;                  // 32-dim O^T tiles
   constexpr int KS = D / 16;                  // k-steps of the QK product
   static_assert(BM == 128, "4 waves x 32 queries");
-  static_assert(VBLK <= 256 && KCH % 256 == 0, "tile does not match 256 threads");
+  static_assert(KCH % 256 == 0, "tile does not match 256 threads");
   typedef typename Mfma<DT>::frag frag;
 
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[BN * KP];
@@ -105,8 +163,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   const long long qpos = a.pos0 + mq;
   const long long q_lo = a.pos0 + m0;  // first query position of the workgroup
   const int m_last = (m0 + BM < a.n_q ? m0 + BM : a.n_q) - 1;
-  const long long q_hi = a.pos0 + m_last;
-  const long long kend = q_hi + 1;  // keys [.., kend) may be attended
+  const long long kend = a.pos0 + m_last + 1;  // keys [.., kend) may be attended
   long long kbeg = 0;
   if (a.window > 0 && q_lo >= a.window) kbeg = q_lo - a.window + 1;
   const long long kt_first = kbeg / BN * BN;
@@ -118,7 +175,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
 
   const long long row_stride = (long long)a.n_kv * D;  // elements
   const uint16_t* kg = (const uint16_t*)a.k + (long long)kvh * D;
-  const uint16_t* vg = (const uint16_t*)a.v + (long long)kvh * D;
+  const _Float16* vtg = a.vt + (long long)kvh * D * a.vt_ld;
 
   // Q^T fragments (B operand): lane holds Q[mq][16ks + 8hi .. +8].
   frag qf[KS];
@@ -132,58 +189,39 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   f32x16 o[ND];
 #pragma unroll
   for (int i = 0; i < ND; ++i) o[i] = f32x16{};
-  float m_run = -INFINITY, l_run = 0.0f;
+  float m_ref = -INFINITY;  // running reference max (log2 domain, scaled)
+  float l_run = 0.0f;
 
-  // Register prefetch of one tile: K as 16-byte chunks, V as one 4x8 block.
-  u32x4 kpre[KPT];
-  u32x4 vpre[4];
-  const int vblk = tid;                       // V block owned by this thread
-  const int vb_r = (vblk / (D / 8)) * 4;      // first of 4 key rows
-  const int vb_c = (vblk % (D / 8)) * 8;      // first of 8 dims
+  // Register prefetch of one tile: K and V^T as 16-byte chunks.
+  u32x4 kpre[CPT], vpre[CPT];
   auto prefetch = [&](long long kt0) {
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
+    for (int i = 0; i < CPT; ++i) {
       const int c = tid + 256 * i;
       const int r = c / (D / 8), cc = (c % (D / 8)) * 8;
       long long row = kt0 + r;
-      row = row < kend ? row : kend - 1;
+      row = row < kend ? row : kend - 1;  // never read past the prompt
       kpre[i] = load16(kg + row * row_stride + cc);
     }
-    if (vblk < VBLK) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        long long row = kt0 + vb_r + j;
-        row = row < kend ? row : kend - 1;
-        vpre[j] = load16(vg + row * row_stride + vb_c);
-      }
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i;
+      const int d = c / (BN / 8), cc = (c % (BN / 8)) * 8;
+      vpre[i] = load16(vtg + (long long)d * a.vt_ld + kt0 + cc);
     }
   };
   auto stage = [&]() {
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
+    for (int i = 0; i < CPT; ++i) {
       const int c = tid + 256 * i;
       const int r = c / (D / 8), cc = (c % (D / 8)) * 8;
       *reinterpret_cast<u32x4*>(&k_lds[r * KP + cc]) = kpre[i];
     }
-    if (vblk < VBLK) {
-      // Transpose the 4 (keys) x 8 (dims) block to 8 x 4 and store each dim's
-      // 4 keys as one 8-byte write at the permuted key column.
-      uint16_t e[4][8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const u32x4 w = vpre[j];
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int c = 0; c < 8; ++c) e[j][c] = (uint16_t)(ww[c >> 1] >> (16 * (c & 1)));
-      }
-      const int xcol = 16 * (vb_r / 16) + vt_col(vb_r % 16);
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        f16x4 t;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) t[j] = Mfma<DT>::to_f16(e[j][c]);
-        *reinterpret_cast<f16x4*>(&vt_lds[(vb_c + c) * VP + xcol]) = t;
-      }
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i;
+      const int d = c / (BN / 8), cc = (c % (BN / 8)) * 8;
+      *reinterpret_cast<u32x4*>(&vt_lds[d * VP + cc]) = vpre[i];
     }
   };
 
@@ -201,7 +239,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
     if (a.window > 0 && kt0 + BN - 1 < wq_lo - a.window + 1) live = false;
     if (!live) continue;
 
-    // S^T = K Q^T.
+    // S^T = K Q^T (raw dot products).
     f32x16 s[NS];
 #pragma unroll
     for (int nt = 0; nt < NS; ++nt) {
@@ -214,7 +252,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
       }
     }
 
-    // Scale to the log2 domain, mask, and the online softmax update.
+    // Mask (diagonal / window tiles only) and the row max of raw scores.
     const bool need_mask =
         (kt0 + BN - 1 > wq_lo) || (a.window > 0 && kt0 < wq_hi - a.window + 1);
     float mt = -INFINITY;
@@ -222,21 +260,31 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
     for (int nt = 0; nt < NS; ++nt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float v = s[nt][r] * sl;
+        float v = s[nt][r];
         if (need_mask) {
           const long long kp = kt0 + 32 * nt + 8 * (r >> 2) + 4 * hi + (r & 3);
           const bool ok = kp <= qpos && (a.window <= 0 || kp > qpos - a.window);
           v = ok ? v : -INFINITY;
+          s[nt][r] = v;
         }
-        s[nt][r] = v;
         mt = fmaxf(mt, v);
       }
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float m_new = fmaxf(m_run, mt);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // all masked so far
-    const float corr = exp2_fast(m_run - m_use);
-    m_run = m_new;
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * sl;
+
+    // Lazy rescale: raise the reference only if some row's max exceeds it by
+    // more than 8 (log2), keeping P <= 2^8.
+    const bool grow = mt > m_ref + 8.0f;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      // Rows that do not grow keep their reference (corr 1; also avoids
+      // -inf - -inf for rows still fully masked); m_ref = -inf -> corr 0.
+      const float corr = grow ? exp2_fast(m_ref - mt) : 1.0f;
+      m_ref = grow ? mt : m_ref;
+      l_run *= corr;
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) o[dt] *= corr;
+    }
+    const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;  // row masked so far
 
     f16x8 pf[NS * 2];
     float ls = 0.0f;
@@ -244,14 +292,12 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
     for (int nt = 0; nt < NS; ++nt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const _Float16 p = (_Float16)exp2_fast(s[nt][r] - m_use);
-        ls += (float)p;
-        pf[2 * nt + (r >> 3)][r & 7] = p;
+        const float p = exp2_fast(fmaf(s[nt][r], sl, -m_use));
+        ls += p;
+        pf[2 * nt + (r >> 3)][r & 7] = (_Float16)p;
       }
     }
-    l_run = l_run * corr + ls;
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt) o[dt] *= corr;
+    l_run += ls;
 
     // O^T += V^T P^T.
 #pragma unroll
@@ -286,9 +332,12 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
 
 }  // namespace vtb
 
-#define VTB_PREFILL(DTN, DTT, D)                                                          \
+#define VTB_PREFILL(DTN, DTT, D)                                                           \
   extern "C" __global__ __launch_bounds__(256) void vtb_prefill_##DTN##_d##D(vtb::PrefillArgs a) { \
-    vtb::prefill_body<vtb::DTT, D>(a);                                                    \
+    vtb::prefill_body<vtb::DTT, D>(a);                                                     \
+  }                                                                                        \
+  extern "C" __global__ __launch_bounds__(256) void vtb_vt_##DTN##_d##D(vtb::VtArgs a) {   \
+    vtb::vt_body<vtb::DTT, D>(a);                                                          \
   }
 
 VTB_PREFILL(bf16, kv_bf16, 64)

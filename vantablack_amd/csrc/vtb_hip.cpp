@@ -58,20 +58,29 @@ struct DecodeArgs {
   const float* v_new;
 };
 
-// Arguments of vtb_prefill_* (layout must match PrefillArgs in prefill.hip).
+// Arguments of vtb_prefill_* / vtb_vt_* (layouts must match prefill.hip).
 struct PrefillArgs {
   const void* q;
   const void* k;
-  const void* v;
+  const void* vt;
   float* out;
   int n_q;
   int n_heads;
   int n_kv;
-  int pad0;
+  int vt_ld;
   long long pos0;
   long long window;
   float scale_log2;
   int pad1;
+};
+
+struct VtArgs {
+  const void* v;
+  void* vt;
+  int n_rows;
+  int n_kv;
+  int vt_ld;
+  int pad;
 };
 
 struct AppendArgs {
@@ -97,6 +106,7 @@ struct VtbHipCtx {
   hipModule_t mod_decode = nullptr, mod_prefill = nullptr, mod_kvcopy = nullptr;
   hipFunction_t f_decode[kNumKv][kNumD][kNumG] = {};
   hipFunction_t f_prefill[kNumKv][kNumD] = {};
+  hipFunction_t f_vt[kNumKv][kNumD] = {};
   hipFunction_t f_append[kNumKv] = {};
   hipFunction_t f_copy = nullptr;
   // Split-K workspace and arrival counters (counters are zero between launches).
@@ -107,6 +117,9 @@ struct VtbHipCtx {
   // Prefill query-conversion scratch (f32 -> cache dtype).
   void* qconv = nullptr;
   size_t qconv_bytes = 0;
+  // Prefill V^T scratch (f16, written by the vtb_vt_* pre-pass).
+  void* vt = nullptr;
+  size_t vt_bytes = 0;
   std::string err;
 };
 
@@ -274,18 +287,43 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const void* q, const void* k
   if (di < 0) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "head_dim must be 64, 128 or 256");
   if (dtype != VTB_HIP_F16 && dtype != VTB_HIP_BF16)
     return set_err(ctx, VTB_HIP_EINVAL, "MFMA prefill needs an f16 or bf16 cache");
-  if (!ctx->f_prefill[dtype][di])
+  if (!ctx->f_prefill[dtype][di] || !ctx->f_vt[dtype][di])
     return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prefill kernel not built for this shape");
   if (!aligned16(k) || !aligned16(v) || !aligned16(q))
     return set_err(ctx, VTB_HIP_EINVAL, "q/K/V not 16-byte aligned");
   const size_t bm = (size_t)vtb::prefill_block_m((int)head_dim);
   const size_t nblk = (n_q + bm - 1) / bm;
   if (nblk > 65535 || n_heads > 0x7fffffff) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "grid too large");
+  // V pre-pass: V^T as f16 for keys [0, pos0 + n_q), padded to whole tiles.
+  const long long n_rows = pos0 + (long long)n_q;
+  const long long bn = vtb::prefill_block_n((int)head_dim);
+  const long long vt_ld = (n_rows + 63) / 64 * 64;  // multiple of the pre-pass tile and of bn
+  if (vt_ld % bn != 0 || vt_ld > 0x7fffffff) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prompt too long");
+  const size_t vt_need = (size_t)n_kv * head_dim * (size_t)vt_ld * 2;
+  if (vt_need > ctx->vt_bytes) {
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (ctx->vt) HIP_TRY(ctx, hipFree(ctx->vt), "hipFree");
+    ctx->vt = nullptr;
+    ctx->vt_bytes = 0;
+    HIP_TRY(ctx, hipMalloc(&ctx->vt, vt_need), "hipMalloc(V^T)");
+    ctx->vt_bytes = vt_need;
+  }
+  VtArgs va;
+  memset(&va, 0, sizeof va);
+  va.v = v;
+  va.vt = ctx->vt;
+  va.n_rows = (int)n_rows;
+  va.n_kv = (int)n_kv;
+  va.vt_ld = (int)vt_ld;
+  int rc = launch(ctx, ctx->f_vt[dtype][di], (unsigned)(vt_ld / 64), (unsigned)n_kv, 1, 256, &va);
+  if (rc) return rc;
+
   PrefillArgs a;
   memset(&a, 0, sizeof a);
   a.q = q;
   a.k = k;
-  a.v = v;
+  a.vt = ctx->vt;
+  a.vt_ld = (int)vt_ld;
   a.out = out;
   a.n_q = (int)n_q;
   a.n_heads = (int)n_heads;
@@ -354,6 +392,9 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
         snprintf(name, sizeof name, "vtb_prefill_%s_d%d", kKvNames[kv], D);
         if (hipModuleGetFunction(&ctx->f_prefill[kv][di], ctx->mod_prefill, name) != hipSuccess)
           ctx->f_prefill[kv][di] = nullptr;  // shape not built: reported at launch
+        snprintf(name, sizeof name, "vtb_vt_%s_d%d", kKvNames[kv], D);
+        if (hipModuleGetFunction(&ctx->f_vt[kv][di], ctx->mod_prefill, name) != hipSuccess)
+          ctx->f_vt[kv][di] = nullptr;
       }
     }
     if (ok) {
@@ -376,6 +417,7 @@ extern "C" void vtb_hip_destroy(VtbHipCtx* ctx) {
   if (ctx->ws) (void)hipFree(ctx->ws);
   if (ctx->counters) (void)hipFree(ctx->counters);
   if (ctx->qconv) (void)hipFree(ctx->qconv);
+  if (ctx->vt) (void)hipFree(ctx->vt);
   if (ctx->mod_decode) (void)hipModuleUnload(ctx->mod_decode);
   if (ctx->mod_prefill) (void)hipModuleUnload(ctx->mod_prefill);
   if (ctx->mod_kvcopy) (void)hipModuleUnload(ctx->mod_kvcopy);
