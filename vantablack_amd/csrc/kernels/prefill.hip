@@ -333,7 +333,8 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
 }  // namespace vtb
 
 #define VTB_PREFILL(DTN, DTT, D)                                                           \
-  extern "C" __global__ __launch_bounds__(256) void vtb_prefill_##DTN##_d##D(vtb::PrefillArgs a) { \
+  extern "C" __global__ __launch_bounds__(256, vtb::prefill_waves_per_simd(D))                  \
+  void vtb_prefill_##DTN##_d##D(vtb::PrefillArgs a) {                                         \
     vtb::prefill_body<vtb::DTT, D>(a);                                                     \
   }                                                                                        \
   extern "C" __global__ __launch_bounds__(256) void vtb_vt_##DTN##_d##D(vtb::VtArgs a) {   \

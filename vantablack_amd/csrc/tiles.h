@@ -28,5 +28,9 @@ constexpr int decode_rows_per_load(int head_dim, int kv_bytes) {
 // head_dim (the K and V^T tiles stay near 36 KiB of LDS).
 constexpr int prefill_block_m(int) { return 128; }
 constexpr int prefill_block_n(int head_dim) { return head_dim <= 128 ? 64 : 32; }
+// Minimum resident waves per SIMD the prefill kernel is compiled for: two
+// waves let one wave's softmax and LDS waits hide behind the other's MFMAs
+// (d <= 128 fits 256 registers without spilling; d256 needs more).
+constexpr int prefill_waves_per_simd(int head_dim) { return head_dim <= 128 ? 2 : 1; }
 
 }  // namespace vtb
