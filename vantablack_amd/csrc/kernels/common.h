@@ -63,6 +63,10 @@ __device__ inline u32x4 load16(const void* p) {
 #endif
 }
 
+// Data that other workgroups re-read soon (prefill K/V tiles): ordinary
+// cached load.
+__device__ inline u32x4 load16_cached(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
 // DPP lane moves within 16-lane rows (gfx9 encodings).
 template <int CTRL>
 __device__ inline float dpp(float v) {

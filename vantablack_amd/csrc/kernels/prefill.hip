@@ -150,12 +150,26 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int hi = lane >> 5;   // lane half
   const int lc = lane & 31;   // lane column: the query this lane owns
-  const int h = blockIdx.x;
   const int nblk = gridDim.y;
-  const int qb = nblk - 1 - (int)blockIdx.y;  // longest (last) query blocks first
+  int h, qb;
+  {
+    // Workgroups are dispatched round-robin over the 8 XCDs in linear order.
+    // When the heads split evenly, XCD x gets heads [x*hpx, (x+1)*hpx) --
+    // with GQA these share KV heads, so each XCD's L2 holds fewer K/V tiles
+    // -- and every XCD takes its longest (last) query blocks first.
+    const int i = blockIdx.y * gridDim.x + blockIdx.x;
+    if (a.n_heads % 8 == 0) {
+      const int hpx = a.n_heads / 8, j = i / 8;
+      h = (i % 8) * hpx + j % hpx;
+      qb = nblk - 1 - j / hpx;
+    } else {
+      h = blockIdx.x;
+      qb = nblk - 1 - (int)blockIdx.y;
+    }
+  }
   const int kvh = (int)(((long long)h * a.n_kv) / a.n_heads);
 
   const int m0 = qb * BM;
@@ -201,13 +215,13 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
       const int r = c / (D / 8), cc = (c % (D / 8)) * 8;
       long long row = kt0 + r;
       row = row < kend ? row : kend - 1;  // never read past the prompt
-      kpre[i] = load16(kg + row * row_stride + cc);
+      kpre[i] = load16_cached(kg + row * row_stride + cc);
     }
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + 256 * i;
       const int d = c / (BN / 8), cc = (c % (BN / 8)) * 8;
-      vpre[i] = load16(vtg + (long long)d * a.vt_ld + kt0 + cc);
+      vpre[i] = load16_cached(vtg + (long long)d * a.vt_ld + kt0 + cc);
     }
   };
   auto stage = [&]() {
@@ -226,6 +240,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   };
 
   const float sl = a.scale_log2;
+  // The window as a 32-bit bound (positions stay below 2^30; a larger or
+  // absent window keeps every causal key).
+  const int wcap = (a.window > 0 && a.window < (1 << 30)) ? (int)a.window : (1 << 30);
   long long kt0 = kt_first;
   if (kt0 < kend) prefetch(kt0);
   for (; kt0 < kend; kt0 += BN) {
@@ -252,23 +269,27 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
       }
     }
 
-    // Mask (diagonal / window tiles only) and the row max of raw scores.
-    const bool need_mask =
-        (kt0 + BN - 1 > wq_lo) || (a.window > 0 && kt0 < wq_hi - a.window + 1);
+    // Mask (diagonal / window tiles only: a wave-uniform branch).  Key
+    // 32nt + 8(r/4) + 4hi + r%4 of the tile is kept iff it lies in
+    // (qpos - window, qpos]; lim is qpos relative to this lane's first key.
+    const bool need_mask = (kt0 + BN - 1 > wq_lo) || (a.window > 0 && kt0 < wq_hi - a.window + 1);
+    if (need_mask) {
+      const int lim = (int)(qpos - kt0) - 4 * hi;
+#pragma unroll
+      for (int nt = 0; nt < NS; ++nt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int ko = 32 * nt + 8 * (r >> 2) + (r & 3);
+          const bool ok = ko <= lim && ko > lim - wcap;
+          s[nt][r] = ok ? s[nt][r] : -INFINITY;
+        }
+      }
+    }
     float mt = -INFINITY;
 #pragma unroll
     for (int nt = 0; nt < NS; ++nt) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float v = s[nt][r];
-        if (need_mask) {
-          const long long kp = kt0 + 32 * nt + 8 * (r >> 2) + 4 * hi + (r & 3);
-          const bool ok = kp <= qpos && (a.window <= 0 || kp > qpos - a.window);
-          v = ok ? v : -INFINITY;
-          s[nt][r] = v;
-        }
-        mt = fmaxf(mt, v);
-      }
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[nt][r]);
     }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * sl;
 

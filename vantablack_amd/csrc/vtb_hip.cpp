@@ -298,7 +298,8 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const void* q, const void* k
   const long long n_rows = pos0 + (long long)n_q;
   const long long bn = vtb::prefill_block_n((int)head_dim);
   const long long vt_ld = (n_rows + 63) / 64 * 64;  // multiple of the pre-pass tile and of bn
-  if (vt_ld % bn != 0 || vt_ld > 0x7fffffff) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prompt too long");
+  // The kernels compare positions in 32-bit arithmetic.
+  if (vt_ld % bn != 0 || vt_ld >= (1LL << 30)) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prompt too long");
   const size_t vt_need = (size_t)n_kv * head_dim * (size_t)vt_ld * 2;
   if (vt_need > ctx->vt_bytes) {
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
