@@ -139,5 +139,8 @@ __device__ inline float load_coherent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ inline void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Wait for all of this wave's vector-memory loads, including buffer->LDS
+// transfers (their LDS writes have landed when vmcnt reaches zero).
+__device__ inline void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 }  // namespace vtb

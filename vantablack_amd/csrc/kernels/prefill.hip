@@ -134,19 +134,34 @@ template <typename DT, int D>
 __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   constexpr int BM = prefill_block_m(D);      // queries per workgroup (4 waves x 32)
   constexpr int BN = prefill_block_n(D);      // keys per tile
-  constexpr int KP = D + 8;                   // K tile row pitch (elements)
-  constexpr int VP = BN + 8;                  // V^T tile row pitch (f16)
-  constexpr int KCH = BN * D / 8;             // 16-byte chunks per K (and V^T) tile
-  constexpr int CPT = KCH / 256;              // chunks per thread
+  constexpr int KCH = D / 8;                  // 16-byte chunks per K row
+  constexpr int VCH = BN / 8;                 // 16-byte chunks per V^T row
+  constexpr int KPB = (KCH + 1) * 16;         // LDS pitch of a K row: one pad chunk
+  constexpr int VPB = (VCH + 1) * 16;         // LDS pitch of a V^T row
+  constexpr int CPT = BN * KCH / 256;         // 16-byte chunks per thread per tile (K; V^T alike)
+  static_assert(BN * KCH % 256 == 0, "tile does not match 256 threads");
   constexpr int NS = BN / 32;                 // 32-key S^T tiles per key tile
   constexpr int ND = D / 32;                  // 32-dim O^T tiles
   constexpr int KS = D / 16;                  // k-steps of the QK product
+  constexpr int PS = BN / 16;                 // k-steps of the PV product
+#ifndef VTB_PF_KB
+#define VTB_PF_KB 1
+#endif
+#ifndef VTB_PF_VB
+#define VTB_PF_VB 2
+#endif
+  constexpr int KB = NS < VTB_PF_KB ? NS : VTB_PF_KB;  // S^T tiles per K-fragment batch
+  constexpr int VB = ND < VTB_PF_VB ? ND : VTB_PF_VB;  // O^T tiles per V-fragment batch
+  static_assert(NS % KB == 0 && ND % VB == 0, "batches must divide the tiles");
   static_assert(BM == 128, "4 waves x 32 queries");
-  static_assert(KCH % 256 == 0, "tile does not match 256 threads");
   typedef typename Mfma<DT>::frag frag;
 
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[BN * KP];
-  __shared__ __attribute__((aligned(16))) _Float16 vt_lds[D * VP];
+  // Two K and two V^T stages: tile j is read from stage j%2 while tile j+1
+  // is written into the other, so one barrier per tile suffices.
+  __shared__ __attribute__((aligned(16))) char k_lds0[BN * KPB];
+  __shared__ __attribute__((aligned(16))) char k_lds1[BN * KPB];
+  __shared__ __attribute__((aligned(16))) char v_lds0[D * VPB];
+  __shared__ __attribute__((aligned(16))) char v_lds1[D * VPB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -191,13 +206,45 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   const uint16_t* kg = (const uint16_t*)a.k + (long long)kvh * D;
   const _Float16* vtg = a.vt + (long long)kvh * D * a.vt_ld;
 
+  // Tile staging through registers: thread chunk i of a tile is K row
+  // (tid + 256i) / KCH, chunk (tid + 256i) % KCH, and V^T row (tid + 256i) /
+  // VCH, chunk (tid + 256i) % VCH.  K rows at or past kend are clamped to
+  // kend - 1 (those keys are masked for every query here).
+  u32x4 kpre[CPT], vpre[CPT];
+  auto fetch = [&](long long kt0) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i;
+      long long row = kt0 + c / KCH;
+      row = row < kend ? row : kend - 1;
+      kpre[i] = load16_cached(kg + row * row_stride + 8 * (c % KCH));
+    }
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i;
+      vpre[i] = load16_cached(vtg + (long long)(c / VCH) * a.vt_ld + kt0 + 8 * (c % VCH));
+    }
+  };
+  auto stage = [&](char* kl, char* vl) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<u32x4*>(kl + (c / KCH) * KPB + 16 * (c % KCH)) = kpre[i];
+    }
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<u32x4*>(vl + (c / VCH) * VPB + 16 * (c % VCH)) = vpre[i];
+    }
+  };
+
   // Q^T fragments (B operand): lane holds Q[mq][16ks + 8hi .. +8].
   frag qf[KS];
   {
     const int mr = mq < a.n_q ? mq : a.n_q - 1;
     const uint16_t* qp = (const uint16_t*)a.q + ((long long)mr * a.n_heads + h) * D + 8 * hi;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = __builtin_bit_cast(frag, load16(qp + 16 * ks));
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = __builtin_bit_cast(frag, load16_cached(qp + 16 * ks));
   }
 
   f32x16 o[ND];
@@ -205,69 +252,50 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   for (int i = 0; i < ND; ++i) o[i] = f32x16{};
   float m_ref = -INFINITY;  // running reference max (log2 domain, scaled)
   float l_run = 0.0f;
-
-  // Register prefetch of one tile: K and V^T as 16-byte chunks.
-  u32x4 kpre[CPT], vpre[CPT];
-  auto prefetch = [&](long long kt0) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + 256 * i;
-      const int r = c / (D / 8), cc = (c % (D / 8)) * 8;
-      long long row = kt0 + r;
-      row = row < kend ? row : kend - 1;  // never read past the prompt
-      kpre[i] = load16_cached(kg + row * row_stride + cc);
-    }
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + 256 * i;
-      const int d = c / (BN / 8), cc = (c % (BN / 8)) * 8;
-      vpre[i] = load16_cached(vtg + (long long)d * a.vt_ld + kt0 + cc);
-    }
-  };
-  auto stage = [&]() {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + 256 * i;
-      const int r = c / (D / 8), cc = (c % (D / 8)) * 8;
-      *reinterpret_cast<u32x4*>(&k_lds[r * KP + cc]) = kpre[i];
-    }
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + 256 * i;
-      const int d = c / (BN / 8), cc = (c % (BN / 8)) * 8;
-      *reinterpret_cast<u32x4*>(&vt_lds[d * VP + cc]) = vpre[i];
-    }
-  };
-
   const float sl = a.scale_log2;
   // The window as a 32-bit bound (positions stay below 2^30; a larger or
   // absent window keeps every causal key).
   const int wcap = (a.window > 0 && a.window < (1 << 30)) ? (int)a.window : (1 << 30);
-  long long kt0 = kt_first;
-  if (kt0 < kend) prefetch(kt0);
-  for (; kt0 < kend; kt0 += BN) {
-    __syncthreads();  // previous tile's LDS reads are done
-    stage();
-    __syncthreads();
-    if (kt0 + BN < kend) prefetch(kt0 + BN);
 
+  auto compute = [&](const char* kl, const char* vl, long long kt0) {
     // Skip tiles entirely above this wave's diagonal or before its windows.
     bool live = wave_live && kt0 <= wq_hi;
     if (a.window > 0 && kt0 + BN - 1 < wq_lo - a.window + 1) live = false;
-    if (!live) continue;
+    if (!live) return;
 
-    // S^T = K Q^T (raw dot products).
+    // S^T = K Q^T.  K fragments (row 32nt + lc, chunk 2ks + hi) are read in
+    // batches of KB S^T tiles so their LDS latency overlaps the MFMAs.
+    const char* kr = kl + lc * KPB + 16 * hi;
     f32x16 s[NS];
 #pragma unroll
-    for (int nt = 0; nt < NS; ++nt) {
-      s[nt] = f32x16{};
-      const uint16_t* kr = &k_lds[(32 * nt + lc) * KP + 8 * hi];
+    for (int nt = 0; nt < NS; ++nt) s[nt] = f32x16{};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const frag kf = __builtin_bit_cast(frag, *reinterpret_cast<const u32x4*>(kr + 16 * ks));
-        s[nt] = Mfma<DT>::qk(kf, qf[ks], s[nt]);
-      }
+    for (int n0 = 0; n0 < NS; n0 += KB) {
+      u32x4 kf[KS][KB];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int nb = 0; nb < KB; ++nb)
+          kf[ks][nb] = *reinterpret_cast<const u32x4*>(kr + 32 * (n0 + nb) * KPB + 32 * ks);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int nb = 0; nb < KB; ++nb)
+          s[n0 + nb] = Mfma<DT>::qk(__builtin_bit_cast(frag, kf[ks][nb]), qf[ks], s[n0 + nb]);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(0);
     }
+
+    // First V^T batch (dims 0 .. 32VB) for the PV product, in flight during
+    // the softmax.
+    const char* vr = vl + lc * VPB + 16 * hi;
+    u32x4 vf[PS][VB];
+#pragma unroll
+    for (int ks = 0; ks < PS; ++ks)
+#pragma unroll
+      for (int db = 0; db < VB; ++db) vf[ks][db] = *reinterpret_cast<const u32x4*>(vr + 32 * db * VPB + 32 * ks);
 
     // Mask (diagonal / window tiles only: a wave-uniform branch).  Key
     // 32nt + 8(r/4) + 4hi + r%4 of the tile is kept iff it lies in
@@ -307,7 +335,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
     }
     const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;  // row masked so far
 
-    f16x8 pf[NS * 2];
+    f16x8 pf[PS];
     float ls = 0.0f;
 #pragma unroll
     for (int nt = 0; nt < NS; ++nt) {
@@ -320,16 +348,50 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
     }
     l_run += ls;
 
-    // O^T += V^T P^T.
+    // O^T += V^T P^T, VB dim tiles per batch; the next batch's fragments are
+    // read while the current batch's MFMAs run.
 #pragma unroll
-    for (int dt = 0; dt < ND; ++dt) {
-      const _Float16* vr = &vt_lds[(32 * dt + lc) * VP + 8 * hi];
+    for (int d0 = 0; d0 < ND; d0 += VB) {
+      if (d0 > 0) {
 #pragma unroll
-      for (int ks = 0; ks < BN / 16; ++ks) {
-        const f16x8 vf = *reinterpret_cast<const f16x8*>(vr + 16 * ks);
-        o[dt] = mfma_pv(vf, pf[ks], o[dt]);
+        for (int ks = 0; ks < PS; ++ks)
+#pragma unroll
+          for (int db = 0; db < VB; ++db)
+            vf[ks][db] = *reinterpret_cast<const u32x4*>(vr + 32 * (d0 + db) * VPB + 32 * ks);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int ks = 0; ks < PS; ++ks)
+#pragma unroll
+        for (int db = 0; db < VB; ++db)
+          o[d0 + db] = mfma_pv(__builtin_bit_cast(f16x8, vf[ks][db]), pf[ks], o[d0 + db]);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(0);
     }
+  };
+
+  // Key loop, two tiles per trip so each stage is a fixed LDS object.  Per
+  // tile: barrier (the stage to read is complete; every wave is done with the
+  // other stage), fetch the next tile into registers, compute, then store the
+  // fetched tile into the other stage.
+  if (kt_first < kend) {
+    fetch(kt_first);
+    stage(k_lds0, v_lds0);
+  }
+  for (long long kt0 = kt_first; kt0 < kend; kt0 += 2 * BN) {
+    __syncthreads();
+    const bool more1 = kt0 + BN < kend;
+    if (more1) fetch(kt0 + BN);
+    compute(k_lds0, v_lds0, kt0);
+    if (!more1) break;
+    stage(k_lds1, v_lds1);
+    __syncthreads();
+    const bool more2 = kt0 + 2 * BN < kend;
+    if (more2) fetch(kt0 + 2 * BN);
+    compute(k_lds1, v_lds1, kt0 + BN);
+    if (!more2) break;
+    stage(k_lds0, v_lds0);
   }
 
   // out[mq][h][d] = O^T[d][mq] / l.  The lane holds d = 32dt + 8(r/4) +
