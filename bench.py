@@ -22,7 +22,15 @@ oracle/attn_oracle.c) on a bounded sample of the same decode workload, on
 the host's cores, once faithfully single-threaded (as vantablack runs
 attention) and once split over heads on a pool.zig-style pool.
 
+roofline.traffic: HBM-side bytes per launch of the same kernel shape, read
+from profiles/traffic.json.  That file comes from two rocprofv3 counter runs
+over `bench.py --pmc-workload` (FETCH_SIZE, then WRITE_SIZE), each scaled by
+what the counter reads for vtb_copy_f32 over a buffer of known size, and is
+written by `bench.py --pmc-summary FETCH_DIR WRITE_DIR`.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ctx 8192]
+       python bench.py --pmc-workload              (the counter-run workload)
+       python bench.py --pmc-summary FETCH_DIR WRITE_DIR
 """
 from __future__ import annotations
 
@@ -36,6 +44,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "decode attn HBM GB/s (% of peak) @ctx 8K; prefill attn TFLOP/s (% MFMA peak)"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+PMC_COPY_FLOATS = 64 << 20  # calibration copy: 256 MiB read + 256 MiB written
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 
@@ -214,7 +224,103 @@ def cpu_baseline(seconds_budget=12.0):
     return res
 
 
+def pmc_workload(ctx_rows=8192):
+    """One dispatch of each measured kernel shape, for rocprofv3 --pmc runs:
+    the calibration copy (vtb_copy_f32), one C2 decode launch at L = ctx+1
+    with the KV append fused (vtb_decode_f16_d128_g1), and one C4 prefill of
+    8192 tokens (vtb_vt_bf16_d128 + vtb_prefill_bf16_d128)."""
+    import numpy as np
+    import torch
+    import vantablack_amd as vb
+    ctx = vb.Context()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(99)
+    src = torch.randn(PMC_COPY_FLOATS, generator=g, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    with ctx.segment() as seg:
+        seg.copy(ctx.wrap_tensor(dst), 0, ctx.wrap_tensor(src), 0, PMC_COPY_FLOATS)
+    ctx.wait_idle()
+    log("pmc: copy done")
+    del src, dst
+    n_heads, n_kv, d, L = 32, 32, 128, ctx_rows + 1
+    kc = torch.randn((L, n_kv, d), generator=g, device=dev).to(torch.float16)
+    vc = torch.randn((L, n_kv, d), generator=g, device=dev).to(torch.float16)
+    q = torch.randn(n_heads * d, generator=g, device=dev) / np.sqrt(d)
+    kcur, vcur, out = torch.randn(n_kv * d, device=dev), torch.randn(n_kv * d, device=dev), torch.empty(n_heads * d, device=dev)
+    torch.cuda.synchronize()
+    with ctx.segment() as seg:
+        seg.attn_decode_append(ctx.wrap_tensor(out), ctx.wrap_tensor(q), ctx.wrap_tensor(kc), 0, ctx.wrap_tensor(vc), 0,
+                               ctx.wrap_tensor(kcur), ctx.wrap_tensor(vcur), n_heads, n_kv, d, L, 1.0 / np.sqrt(d), vb.F16)
+    ctx.wait_idle()
+    log("pmc: decode done")
+    del kc, vc
+    n_heads, n_kv, d, L = 32, 8, 128, 8192
+    qp = torch.randn((L, n_heads * d), generator=g, device=dev).to(torch.bfloat16)
+    kp = torch.randn((L, n_kv * d), generator=g, device=dev).to(torch.bfloat16)
+    vp = torch.randn((L, n_kv * d), generator=g, device=dev).to(torch.bfloat16)
+    op = torch.empty((L, n_heads * d), device=dev)
+    torch.cuda.synchronize()
+    with ctx.segment() as seg:
+        seg.attn_prefill(ctx.wrap_tensor(op), ctx.wrap_tensor(qp), ctx.wrap_tensor(kp), ctx.wrap_tensor(vp), 0, L, 0,
+                         vb.NO_WINDOW, n_heads, n_kv, d, 1.0 / np.sqrt(d), vb.BF16)
+    ctx.wait_idle()
+    log("pmc: prefill done")
+    ctx.close()
+
+
+def pmc_summary(fetch_dir, write_dir):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the vtb_* kernels from
+    two rocprofv3 --pmc csv outputs, scaled by the copy calibration, written
+    to profiles/traffic.json and printed as a markdown table."""
+    import csv
+    import glob
+
+    def read(dirname, counter):
+        vals = {}
+        for f in glob.glob(os.path.join(dirname, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] == counter and r["Kernel_Name"].startswith("vtb_"):
+                    name = r["Kernel_Name"].split("(")[0]
+                    vals.setdefault(name, []).append(float(r["Counter_Value"]))
+        return {k: sum(v) / len(v) for k, v in vals.items()}
+
+    fetch, write = read(fetch_dir, "FETCH_SIZE"), read(write_dir, "WRITE_SIZE")
+    copy_kib = PMC_COPY_FLOATS * 4 / 1024
+    f_fetch = copy_kib / fetch["vtb_copy_f32"]
+    f_write = copy_kib / write["vtb_copy_f32"]
+    kernels = {}
+    for name in sorted(set(fetch) & set(write)):
+        kernels[name] = {"fetch_kib": round(fetch[name], 1), "write_kib": round(write[name], 1),
+                         "traffic_bytes": int(round((fetch[name] * f_fetch + write[name] * f_write) * 1024))}
+    out = {"calibration": {"kernel": "vtb_copy_f32", "bytes_each_way": PMC_COPY_FLOATS * 4,
+                           "fetch_factor": round(f_fetch, 4), "write_factor": round(f_write, 4)},
+           "workload": "bench.py --pmc-workload: C2 decode at L=8193 (f16, KV append fused); C4 prefill 8192 tokens bf16",
+           "kernels": kernels}
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+    print(f"calibration (vtb_copy_f32, {PMC_COPY_FLOATS * 4 >> 20} MiB each way): "
+          f"FETCH x{f_fetch:.4f}, WRITE x{f_write:.4f}\n")
+    print("| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | calibrated traffic MB |")
+    print("|---|---|---|---|")
+    for k, v in kernels.items():
+        print(f"| {k} | {v['fetch_kib']:.1f} | {v['write_kib']:.1f} | {v['traffic_bytes'] / 1e6:.2f} |")
+
+
+def load_traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)["kernels"]
+    except (OSError, ValueError, KeyError):
+        return {}
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--pmc-workload":
+        return pmc_workload()
+    if len(sys.argv) > 1 and sys.argv[1] == "--pmc-summary":
+        return pmc_summary(sys.argv[2], sys.argv[3])
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=32)
@@ -240,6 +346,9 @@ def main():
     }
     cpu = None if args.no_cpu else cpu_baseline()
     ctx.close()
+    traffic = load_traffic()
+    dec_tr = traffic.get("vtb_decode_f16_d128_g1", {}).get("traffic_bytes")
+    pre_tr = traffic.get("vtb_prefill_bf16_d128", {}).get("traffic_bytes")
 
     line = {
         "metric": METRIC,
@@ -264,7 +373,9 @@ def main():
         "pct_of_hbm_peak": round(100.0 * dec["value"] / HBM_PEAK_GBS, 2),
         "roofline": {
             "bound": "hbm", "achieved": round(dec["achieved_gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(dec["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(dec["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": dec_tr,
+            "traffic_source": "profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated; L=8193)"
+            if dec_tr else None,
             "kernel": "vtb_decode_f16_d128_g1 (KV append fused)",
             "avg_launch_us": round(dec["avg_launch_s"] * 1e6, 3),
             "bytes_per_launch": int(dec["bytes_per_launch"]),
@@ -278,7 +389,7 @@ def main():
             "value": round(p8["tflops"], 2), "unit": "TFLOP/s",
             "pct_of_bf16_peak": round(100.0 * p8["tflops"] / BF16_PEAK_TFLOPS, 2),
             "roofline": {"bound": "mfma", "achieved": round(p8["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(p8["tflops"] / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                         "unit": "TFLOP/s", "frac": round(p8["tflops"] / BF16_PEAK_TFLOPS, 4), "traffic": pre_tr,
                          "kernel": "vtb_prefill_bf16_d128", "avg_launch_us": round(p8["avg_launch_s"] * 1e6, 2),
                          "flops_per_launch": p8["flops"]},
             "all": {k: {"tflops": round(v["tflops"], 2), "us": round(v["avg_launch_s"] * 1e6, 2)}
