@@ -45,7 +45,7 @@ struct DecodeArgs {
   float* out;           // [n_q][n_heads][D] f32
   float* ws_o;          // [n_q][n_kv][n_splits][G][D]
   float* ws_ml;         // [n_q][n_kv][n_splits][G][2]
-  unsigned* counters;   // [n_q][n_kv], zero between launches
+  unsigned* counters;   // [n_q][n_kv] x decode_counter_stride, zero between launches
   int n_heads;
   int n_kv;
   int n_splits;
@@ -273,7 +273,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
   wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
-    unsigned* ctr = a.counters + (long long)b * a.n_kv + kvh;
+    unsigned* ctr = a.counters + ((long long)b * a.n_kv + kvh) * decode_counter_stride;
     unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int last = (prev == (unsigned)(n_act - 1));
     if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

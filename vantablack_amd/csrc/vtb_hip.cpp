@@ -254,7 +254,7 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
 
   const size_t n_part = n_q * n_kv * (size_t)n_splits * G;
   const size_t ws_need = n_splits > 1 ? n_part * (head_dim + 2) * sizeof(float) : 0;
-  int rc = ensure_workspace(ctx, ws_need, n_q * n_kv);
+  int rc = ensure_workspace(ctx, ws_need, n_q * n_kv * vtb::decode_counter_stride);
   if (rc) return rc;
 
   DecodeArgs a;
