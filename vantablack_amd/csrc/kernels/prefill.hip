@@ -93,6 +93,19 @@ __device__ inline f32x16 mfma_pv(f16x8 a, f16x8 b, f32x16 c) {
 // its own inverse.
 __device__ inline int vt_col(int x) { return 8 * ((x >> 2) & 1) + 4 * (x >> 3) + (x & 3); }
 
+// v of lane l ^ 32 via v_permlane32_swap_b32, which swaps lanes 32..63 of
+// its first register with lanes 0..31 of its second: with both holding v,
+// the first ends up holding v of lane l % 32 and the second v of lane
+// l % 32 + 32, in every lane.  Inline asm because the compiler's builtin for
+// this instruction returns the first register for both results; the s_nop
+// gives the two wait states a VALU write needs before a permlane reads it.
+__device__ inline void lane_halves(float v, float& lo_half, float& hi_half) {
+  float x = v, y = v;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+  lo_half = x;
+  hi_half = y;
+}
+
 // ---------------------------------------------------------------- pre-pass
 template <typename DT, int D>
 __device__ __forceinline__ void vt_body(const VtArgs& a) {
@@ -319,7 +332,11 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[nt][r]);
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * sl;
+    {
+      float m0, m1;
+      lane_halves(mt, m0, m1);
+      mt = fmaxf(m0, m1) * sl;
+    }
 
     // Lazy rescale: raise the reference only if some row's max exceeds it by
     // more than 8 (log2), keeping P <= 2^8.
@@ -336,16 +353,24 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
     const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;  // row masked so far
 
     f16x8 pf[PS];
-    float ls = 0.0f;
 #pragma unroll
     for (int nt = 0; nt < NS; ++nt) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = exp2_fast(fmaf(s[nt][r], sl, -m_use));
-        ls += p;
-        pf[2 * nt + (r >> 3)][r & 7] = (_Float16)p;
-      }
+      for (int r = 0; r < 16; ++r)
+        pf[2 * nt + (r >> 3)][r & 7] = (_Float16)exp2_fast(fmaf(s[nt][r], sl, -m_use));
     }
+    // Row sum over the f16-rounded P, the values the PV MFMAs consume:
+    // v_dot2_f32_f16 against (1, 1) adds two of them per instruction.
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+    float ls = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PS; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const h2 pr = {pf[i][e], pf[i][e + 1]};
+        ls = __builtin_amdgcn_fdot2(pr, ones, ls, false);
+      }
     l_run += ls;
 
     // O^T += V^T P^T, VB dim tiles per batch; the next batch's fragments are
@@ -396,7 +421,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
 
   // out[mq][h][d] = O^T[d][mq] / l.  The lane holds d = 32dt + 8(r/4) +
   // 4hi + (r%4): four consecutive dims per r/4, written as one 16-byte store.
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  float l0, l1;
+  lane_halves(l_run, l0, l1);
+  const float l_tot = l0 + l1;
   if (mq < a.n_q) {
     const float inv = 1.0f / l_tot;
     float* op = a.out + ((long long)mq * a.n_heads + h) * D + 4 * hi;
