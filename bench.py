@@ -150,6 +150,67 @@ def bench_decode(ctx, torch, args):
     }
 
 
+def bench_decode_cfg(ctx, torch, name, n_layers, n_heads, n_kv, d, kv, L, steps=8, warmup=2, seed=7):
+    """Decode of one BASELINE config shape: every step runs the fused
+    append + attention launch for each of n_layers layers, the token at
+    attended length L (the cache holds the L attended rows; a sliding
+    window is the caller's offset shift of forward.zig:470-483, so only
+    the window's rows need to exist).  Returns per-launch time from HIP
+    events on the context stream and the algorithmic GB/s."""
+    import numpy as np
+    import vantablack_amd as vb
+    tdt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[kv]
+    vdt = {"f32": vb.F32, "f16": vb.F16, "bf16": vb.BF16}[kv]
+    eb = {"f32": 4, "f16": 2, "bf16": 2}[kv]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    rows = L + 1
+    kc = torch.randn((n_layers, rows, n_kv, d), generator=g, device=dev).to(tdt)
+    vc = torch.randn((n_layers, rows, n_kv, d), generator=g, device=dev).to(tdt)
+    q = (torch.randn((n_layers, n_heads * d), generator=g, device=dev) / np.sqrt(d)).contiguous()
+    kcur = torch.randn((n_layers, n_kv * d), generator=g, device=dev)
+    vcur = torch.randn((n_layers, n_kv * d), generator=g, device=dev)
+    out = torch.empty((n_layers, n_heads * d), device=dev)
+    torch.cuda.synchronize()
+    kb, vbuf = ctx.wrap_tensor(kc), ctx.wrap_tensor(vc)
+    qbs = [ctx.wrap_tensor(q[l]) for l in range(n_layers)]
+    obs = [ctx.wrap_tensor(out[l]) for l in range(n_layers)]
+    kcs = [ctx.wrap_tensor(kcur[l]) for l in range(n_layers)]
+    vcs = [ctx.wrap_tensor(vcur[l]) for l in range(n_layers)]
+    layer_bytes = rows * n_kv * d * eb
+    inv = 1.0 / np.sqrt(d)
+    stream = torch.cuda.ExternalStream(ctx.stream)
+
+    def one_step(seg):
+        for l in range(n_layers):
+            seg.attn_decode_append(obs[l], qbs[l], kb, l * layer_bytes, vbuf, l * layer_bytes, kcs[l], vcs[l],
+                                   n_heads, n_kv, d, L, inv, vdt)
+
+    with ctx.segment() as seg:
+        for _ in range(warmup):
+            one_step(seg)
+    ctx.wait_idle()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    with ctx.segment() as seg:
+        for _ in range(steps):
+            one_step(seg)
+    e1.record(stream)
+    ctx.wait_idle()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / (steps * n_layers)
+    per = decode_bytes(L, n_heads, n_kv, d, eb)
+    for b in qbs + obs + kcs + vcs + [kb, vbuf]:
+        b.release()
+    del kc, vc
+    torch.cuda.empty_cache()
+    log(f"decode {name}: h{n_heads}/{n_kv} d{d} {kv} L={L}: {t * 1e6:.2f} us/launch -> {per / t / 1e9:.1f} GB/s")
+    return {"us_per_launch": round(t * 1e6, 3), "gbs": round(per / t / 1e9, 1),
+            "pct_of_hbm_peak": round(100.0 * per / t / 1e9 / HBM_PEAK_GBS, 2), "bytes_per_launch": per,
+            "shape": f"{n_layers} layers, {n_heads}q/{n_kv}kv heads, d{d}, {kv} KV, attended L={L}"}
+
+
 def prefill_flops(L, n_heads, d):
     return 4 * n_heads * d * L * (L + 1) // 2
 
@@ -328,6 +389,7 @@ def main():
     ap.add_argument("--ctx", type=int, default=8192)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-more", action="store_true", help="skip the C1/C3/C5 decode lines")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; the path's multi-GPU sharding is "
@@ -338,6 +400,13 @@ def main():
     import vantablack_amd as vb
     ctx = vb.Context()
     dec = bench_decode(ctx, torch, args)
+    # The other decode configs (3, 5), reported
+    # beside the headline.  C3: window 4096 at position 16383 -> 4096 rows.
+    dec_more = {} if args.no_more else {
+        "C1": bench_decode_cfg(ctx, torch, "C1", 1, 32, 4, 64, "f32", 512, steps=64),
+        "C3": bench_decode_cfg(ctx, torch, "C3", 32, 32, 8, 128, "bf16", 4096),
+        "C5": bench_decode_cfg(ctx, torch, "C5", 26, 8, 1, 256, "bf16", 32768),
+    }
     pre = {} if args.no_prefill else {
         "C4_L512": bench_prefill(ctx, torch, 32, 8, 128, 512),
         "C4_L2048": bench_prefill(ctx, torch, 32, 8, 128, 2048),
@@ -381,6 +450,8 @@ def main():
             "bytes_per_launch": int(dec["bytes_per_launch"]),
         },
     }
+    if dec_more:
+        line["decode_other_configs"] = dec_more
     if pre:
         p8 = pre["C4_L8192"]
         line["prefill"] = {

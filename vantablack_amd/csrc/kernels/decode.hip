@@ -45,7 +45,9 @@ struct DecodeArgs {
   float* out;           // [n_q][n_heads][D] f32
   float* ws_o;          // [n_q][n_kv][n_splits][G][D]
   float* ws_ml;         // [n_q][n_kv][n_splits][G][2]
-  unsigned* counters;   // [n_q][n_kv] x decode_counter_stride, zero between launches
+  float* wg_o;          // [n_q][n_kv][n_groups][G][D] group partials
+  float* wg_ml;         // [n_q][n_kv][n_groups][G][2]
+  unsigned* counters;   // [n_q][n_kv][n_groups + 1] x decode_counter_stride, zero between launches
   int n_heads;
   int n_kv;
   int n_splits;
@@ -57,6 +59,9 @@ struct DecodeArgs {
   const float* k_new;   // optional (decode only): f32 K/V row appended at
   const float* v_new;   //   row pos0 before attention; null when not fused
 };
+
+// Compile-time batch size of a split merge.
+template <int N> struct merge_batch { static constexpr int value = N; };
 
 template <typename KV, int D, int G, int NIT, int NW>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
@@ -268,58 +273,116 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
   }
   if (single) return;
 
-  // Publish: every thread's coherent stores complete before the workgroup
-  // counts itself in; the last of the n_act workgroups merges.
-  wait_stores();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned* ctr = a.counters + ((long long)b * a.n_kv + kvh) * decode_counter_stride;
-    unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = (prev == (unsigned)(n_act - 1));
-    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = last;
-  }
-  __syncthreads();
-  if (!s_last) return;
+  // Merge.  Up to decode_merge_flat active splits, the last workgroup to
+  // arrive merges them all (batches of 8 independent loads, as many rounds
+  // as batches).  Beyond that the merge has two levels: splits form groups
+  // of decode_merge_group; the last workgroup of a group merges the group's
+  // partials in one batch into a group partial, and the last group merger
+  // merges the group partials.  A flat merge of a long MQA cache (C5: 256
+  // splits of one KV head) was ~100 us of dependent load rounds through one
+  // workgroup; the extra level costs ~1 us, so short split lists stay flat.
+  constexpr int GS = decode_merge_group;
+  const bool two_level = n_act > decode_merge_flat;
+  const int n_groups = (a.n_splits + GS - 1) / GS;  // group slots per (query, KV head)
+  const int n_grp = two_level ? (n_act + GS - 1) / GS : 1;
+  const int grp = two_level ? split / GS : 0;
+  const int members = two_level ? ((n_act - grp * GS) < GS ? n_act - grp * GS : GS) : n_act;
+  unsigned* ctr0 = a.counters + ((long long)b * a.n_kv + kvh) * (n_groups + 1) * decode_counter_stride;
 
-  // Merge n_act partials.  Each thread owns outputs (g, d); partials are
-  // consumed in batches of MB whose loads are all independent, with an
-  // online rescale between batches.
-  constexpr int MB = 8;
-  const long long part0 = ((long long)b * a.n_kv + kvh) * a.n_splits;
-  for (int idx = threadIdx.x; idx < G * D; idx += NT) {
-    const int g = idx / D, d = idx % D;
-    if (g >= gs) continue;
-    float Mx = -INFINITY, Ls = 0.0f, O = 0.0f;
-    for (int sp0 = 0; sp0 < n_act; sp0 += MB) {
-      float mv[MB], lv[MB], ov[MB];
+  // Arrival: every thread's coherent stores complete before the workgroup
+  // counts itself in.
+  auto arrive = [&](unsigned* ctr, int expect) -> bool {
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = (prev == (unsigned)(expect - 1));
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    return s_last != 0;
+  };
+  // Merge `count` partials src[first .. first+count) of this (query, KV
+  // head) -- [slot][G][D] values, [slot][G][2] (m, l) -- in batches of MB
+  // whose loads are all issued together, with an online rescale between
+  // batches.  Writes out = O / L, or the merged (O, m, l) into slot dst of
+  // the group partials.
+  auto merge = [&](auto batch, const float* src_o, const float* src_ml, long long first, int count, bool to_out,
+                   long long dst) {
+    constexpr int MB = decltype(batch)::value;
+    for (int idx = threadIdx.x; idx < G * D; idx += NT) {
+      const int g = idx / D, d = idx % D;
+      if (g >= gs) continue;
+      float M = -INFINITY, L = 0.0f, O = 0.0f;
+      for (int f0 = 0; f0 < count; f0 += MB) {
+        const int cnt = count - f0 < MB ? count - f0 : MB;
+        // A full batch is straight-line code, so all its loads are in flight
+        // together.  In a short final batch the slots past cnt are skipped
+        // by wave-uniform branches rather than clamped: repeated coherent
+        // loads of one address serialize.
+        float mv[MB], lv[MB], ov[MB];
+        if (cnt == MB) {
 #pragma unroll
-      for (int j = 0; j < MB; ++j) {
-        const int sp = sp0 + j < n_act ? sp0 + j : n_act - 1;
-        const long long pj = (part0 + sp) * G + g;
-        mv[j] = load_coherent(&a.ws_ml[pj * 2]);
-        lv[j] = load_coherent(&a.ws_ml[pj * 2 + 1]);
-        ov[j] = load_coherent(&a.ws_o[pj * D + d]);
+          for (int j = 0; j < MB; ++j) {
+            const long long pj = (first + f0 + j) * G + g;
+            mv[j] = load_coherent(&src_ml[pj * 2]);
+            lv[j] = load_coherent(&src_ml[pj * 2 + 1]);
+            ov[j] = load_coherent(&src_o[pj * D + d]);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < MB; ++j) {
+            mv[j] = -INFINITY;
+            lv[j] = 0.0f;
+            ov[j] = 0.0f;
+            if (j < cnt) {
+              const long long pj = (first + f0 + j) * G + g;
+              mv[j] = load_coherent(&src_ml[pj * 2]);
+              lv[j] = load_coherent(&src_ml[pj * 2 + 1]);
+              ov[j] = load_coherent(&src_o[pj * D + d]);
+            }
+          }
+        }
+        float Mb = M;
+#pragma unroll
+        for (int j = 0; j < MB; ++j) Mb = fmaxf(Mb, mv[j]);
+        if (Mb == -INFINITY) continue;  // nothing attended yet
+        const float c = exp2_fast(M - Mb);  // 0 while M is -inf
+        L *= c;
+        O *= c;
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+          if (mv[j] != -INFINITY) {
+            const float f = exp2_fast(mv[j] - Mb);
+            L += lv[j] * f;
+            O += ov[j] * f;
+          }
+        }
+        M = Mb;
       }
-      float mb = Mx;
-#pragma unroll
-      for (int j = 0; j < MB; ++j)
-        if (sp0 + j < n_act) mb = fmaxf(mb, mv[j]);
-      const float c = exp2_fast(Mx - mb);
-      Ls *= c;
-      O *= c;
-#pragma unroll
-      for (int j = 0; j < MB; ++j) {
-        if (sp0 + j < n_act) {
-          const float f = exp2_fast(mv[j] - mb);
-          Ls += lv[j] * f;
-          O += ov[j] * f;
+      if (to_out) {
+        a.out[((long long)b * a.n_heads + h_lo + g) * D + d] = O / L;
+      } else {
+        store_coherent(&a.wg_o[(dst * G + g) * D + d], O);
+        if (d == 0) {
+          store_coherent(&a.wg_ml[(dst * G + g) * 2 + 0], M);
+          store_coherent(&a.wg_ml[(dst * G + g) * 2 + 1], L);
         }
       }
-      Mx = mb;
     }
-    a.out[((long long)b * a.n_heads + h_lo + g) * D + d] = O / Ls;
+  };
+
+  if (!arrive(ctr0 + (long long)grp * decode_counter_stride, members)) return;
+  const long long part0 = ((long long)b * a.n_kv + kvh) * a.n_splits;
+  if (!two_level) {
+    merge(merge_batch<8>{}, a.ws_o, a.ws_ml, part0, n_act, true, 0);
+    return;
   }
+  const long long gpart0 = ((long long)b * a.n_kv + kvh) * n_groups;
+  merge(merge_batch<GS>{}, a.ws_o, a.ws_ml, part0 + (long long)grp * GS, members, false, gpart0 + grp);
+  if (!arrive(ctr0 + (long long)n_groups * decode_counter_stride, n_grp)) return;
+  merge(merge_batch<GS>{}, a.wg_o, a.wg_ml, gpart0, n_grp, true, 0);
 }
 
 }  // namespace vtb

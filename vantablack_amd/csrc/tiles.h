@@ -13,17 +13,40 @@ namespace vtb {
 #ifndef VTB_DECODE_WAVES1
 #define VTB_DECODE_WAVES1 4
 #endif
-constexpr int decode_nit(int g) { return g == 1 ? VTB_DECODE_NIT1 : g <= 4 ? 4 : (g == 8 ? 2 : 1); }
+#ifndef VTB_DECODE_NIT4
+#define VTB_DECODE_NIT4 4
+#endif
+#ifndef VTB_DECODE_NIT8
+#define VTB_DECODE_NIT8 2
+#endif
+constexpr int decode_nit(int g) {
+  return g == 1 ? VTB_DECODE_NIT1 : g <= 4 ? VTB_DECODE_NIT4 : (g == 8 ? VTB_DECODE_NIT8 : 1);
+}
 
 // Waves per decode workgroup.  For g = 1 one wave per SIMD streams best:
 // 16-wave workgroups keep 4x the loads in flight per CU and measured ~1.6 us
 // slower per C2 launch at 8K context (deeper DRAM queues, 4x the waves to
 // dispatch), with the same bytes moved.
-constexpr int decode_waves(int g) { return g == 1 ? VTB_DECODE_WAVES1 : (g <= 8 ? 8 : 4); }
+#ifndef VTB_DECODE_WAVES4
+#define VTB_DECODE_WAVES4 8
+#endif
+#ifndef VTB_DECODE_WAVES8
+#define VTB_DECODE_WAVES8 8
+#endif
+constexpr int decode_waves(int g) {
+  return g == 1 ? VTB_DECODE_WAVES1 : g <= 4 ? VTB_DECODE_WAVES4 : (g == 8 ? VTB_DECODE_WAVES8 : 4);
+}
 
 // Split-K arrival counters sit one per 128 bytes, so the atomics of
 // different (query, KV head) pairs never share a cache line.
 constexpr int decode_counter_stride = 32;
+
+// Split merge: up to decode_merge_flat active splits are merged by the
+// last workgroup alone; beyond that, groups of decode_merge_group splits are
+// merged by each group's last workgroup in one batch of loads, then the
+// group partials by the last group merger.
+constexpr int decode_merge_flat = 32;
+constexpr int decode_merge_group = 16;
 
 // Rows read by one wave load instruction (the split granularity).
 constexpr int decode_rows_per_load(int head_dim, int kv_bytes) {

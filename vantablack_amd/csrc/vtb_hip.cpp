@@ -45,6 +45,8 @@ struct DecodeArgs {
   float* out;
   float* ws_o;
   float* ws_ml;
+  float* wg_o;
+  float* wg_ml;
   unsigned* counters;
   int n_heads;
   int n_kv;
@@ -252,9 +254,13 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
   long long n_splits = (Lmax + rps - 1) / rps;
   if (n_splits > 65535) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "too many splits");
 
+  // Split partials, then group partials (two-level merge), each (o[G][D],
+  // m/l[G][2]); one arrival counter per group plus one for the groups.
+  const size_t n_groups = ((size_t)n_splits + vtb::decode_merge_group - 1) / vtb::decode_merge_group;
   const size_t n_part = n_q * n_kv * (size_t)n_splits * G;
-  const size_t ws_need = n_splits > 1 ? n_part * (head_dim + 2) * sizeof(float) : 0;
-  int rc = ensure_workspace(ctx, ws_need, n_q * n_kv * vtb::decode_counter_stride);
+  const size_t n_gpart = n_q * n_kv * n_groups * G;
+  const size_t ws_need = n_splits > 1 ? (n_part + n_gpart) * (head_dim + 2) * sizeof(float) : 0;
+  int rc = ensure_workspace(ctx, ws_need, n_q * n_kv * (n_groups + 1) * vtb::decode_counter_stride);
   if (rc) return rc;
 
   DecodeArgs a;
@@ -264,7 +270,9 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
   a.v = v;
   a.out = out;
   a.ws_o = (float*)ctx->ws;
-  a.ws_ml = (float*)ctx->ws + n_part * head_dim;
+  a.ws_ml = a.ws_o + n_part * head_dim;
+  a.wg_o = a.ws_ml + n_part * 2;
+  a.wg_ml = a.wg_o + n_gpart * head_dim;
   a.counters = ctx->counters;
   a.n_heads = (int)n_heads;
   a.n_kv = (int)n_kv;
