@@ -78,6 +78,39 @@ constexpr int DPP_XOR2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int DPP_HALF_MIRROR = 0x141; // lane i <- 7-i within 8
 constexpr int DPP_MIRROR = 0x140;      // lane i <- 15-i within 16
 
+constexpr int DPP_ROR8 = 0x128;        // lane i <- (i+8) mod 16 within 16, i.e. i ^ 8
+
+// Lane exchange across 16 or 32 lanes without LDS (gfx950 v_permlane16_swap
+// / v_permlane32_swap).  Called with x == y == v, the pair afterwards holds
+// {v[l], v[l ^ 16]} (or {v[l], v[l ^ 32]}) in every lane l, in some order, so
+// a symmetric combine of x and y is the butterfly step.  Inline asm because
+// the compiler's builtins for these instructions return the first register
+// for both results; the s_nop gives the two wait states a VALU write needs
+// before a permlane reads it.  Every lane of the wave must be active.
+__device__ inline void xchg16(float& x, float& y) {
+  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+}
+__device__ inline void xchg32(float& x, float& y) {
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+}
+// v[l] + v[l ^ M] (sum) or max of the two, for M in {8, 16, 32}.
+template <int M>
+__device__ inline float xor_sum(float v) {
+  static_assert(M == 8 || M == 16 || M == 32, "xor_sum: M must be 8, 16 or 32");
+  if constexpr (M == 8) return v + dpp<DPP_ROR8>(v);
+  float x = v, y = v;
+  if constexpr (M == 16) xchg16(x, y); else xchg32(x, y);
+  return x + y;
+}
+template <int M>
+__device__ inline float xor_max(float v) {
+  static_assert(M == 8 || M == 16 || M == 32, "xor_max: M must be 8, 16 or 32");
+  if constexpr (M == 8) return fmaxf(v, dpp<DPP_ROR8>(v));
+  float x = v, y = v;
+  if constexpr (M == 16) xchg16(x, y); else xchg32(x, y);
+  return fmaxf(x, y);
+}
+
 // Sum over aligned groups of N lanes; every lane of the group gets the sum.
 template <int N>
 __device__ inline float group_sum(float v) {
@@ -85,8 +118,8 @@ __device__ inline float group_sum(float v) {
   if constexpr (N >= 4) v += dpp<DPP_XOR2>(v);
   if constexpr (N >= 8) v += dpp<DPP_HALF_MIRROR>(v);
   if constexpr (N >= 16) v += dpp<DPP_MIRROR>(v);
-  if constexpr (N >= 32) v += __shfl_xor(v, 16, 64);
-  if constexpr (N >= 64) v += __shfl_xor(v, 32, 64);
+  if constexpr (N >= 32) v = xor_sum<16>(v);
+  if constexpr (N >= 64) v = xor_sum<32>(v);
   return v;
 }
 
@@ -94,14 +127,18 @@ __device__ inline float group_sum(float v) {
 // combines the row groups of a wave that share a column slot.
 template <int STRIDE>
 __device__ inline float stride_sum(float v) {
-#pragma unroll
-  for (int m = STRIDE; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
+  static_assert(STRIDE == 8 || STRIDE == 16 || STRIDE == 32 || STRIDE == 64, "stride_sum: unsupported stride");
+  if constexpr (STRIDE <= 8) v = xor_sum<8>(v);
+  if constexpr (STRIDE <= 16) v = xor_sum<16>(v);
+  if constexpr (STRIDE <= 32) v = xor_sum<32>(v);
   return v;
 }
 template <int STRIDE>
 __device__ inline float stride_max(float v) {
-#pragma unroll
-  for (int m = STRIDE; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  static_assert(STRIDE == 8 || STRIDE == 16 || STRIDE == 32 || STRIDE == 64, "stride_max: unsupported stride");
+  if constexpr (STRIDE <= 8) v = xor_max<8>(v);
+  if constexpr (STRIDE <= 16) v = xor_max<16>(v);
+  if constexpr (STRIDE <= 32) v = xor_max<32>(v);
   return v;
 }
 
@@ -139,6 +176,34 @@ __device__ inline float load_coherent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ inline void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Raw buffer resource over [base, base + bytes): loads at offsets >= bytes
+// return zero without a memory access (hardware range check).  Word 3 is the
+// gfx9 raw-buffer format (32-bit data, no swizzle).
+__device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// Agent-coherent (sc1) buffer loads: the counterpart of load_coherent for
+// data written by other workgroups with store_coherent.  Built from 32-bit
+// loads at consecutive offsets into separate float scalars, which the
+// backend merges into one buffer_load_dwordx4 / dwordx2; scalars rather than
+// a vector because a bit_cast of one ext-vector element reads element 0
+// with this compiler (see Unpack<kv_f32>).
+constexpr int kBufSc1 = 16;
+__device__ inline float buffer_load_coherent(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kBufSc1));
+}
+__device__ inline void buffer_load16_coherent(__amdgpu_buffer_rsrc_t r, int off, float& x, float& y, float& z,
+                                              float& w) {
+  x = buffer_load_coherent(r, off);
+  y = buffer_load_coherent(r, off + 4);
+  z = buffer_load_coherent(r, off + 8);
+  w = buffer_load_coherent(r, off + 12);
+}
+__device__ inline void buffer_load8_coherent(__amdgpu_buffer_rsrc_t r, int off, float& x, float& y) {
+  x = buffer_load_coherent(r, off);
+  y = buffer_load_coherent(r, off + 4);
+}
+
 // Wait for all of this wave's vector-memory loads, including buffer->LDS
 // transfers (their LDS writes have landed when vmcnt reaches zero).
 __device__ inline void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }

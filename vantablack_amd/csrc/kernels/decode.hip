@@ -16,13 +16,16 @@
 //   lanes, one 16-byte load per lane; RPW = 64/LPR rows are read per load
 //   instruction, NIT instructions per tile.  Tiles are double-buffered in
 //   registers: the next tile's loads are issued before this tile's math.
-//   Scores are reduced across the LPR lanes with DPP adds; the softmax is
-//   online (running max m, sum l, accumulator acc) per wave, in registers.
+//   Scores are reduced across the LPR lanes with DPP adds and the rows of a
+//   load instruction combined with DPP / permlane swaps (no LDS); the softmax
+//   is online (running max m, sum l, accumulator acc) per wave, in registers.
 //   The waves combine into one (m, l, o) partial per workgroup through
 //   per-wave LDS slots summed in a fixed order.  The last-arriving
-//   workgroup of each (query, KV head) merges the partials (log-sum-exp),
-//   loading them in independent batches, and writes out[h] = o/l.  It resets
-//   the arrival counter to zero, so no memset is needed between launches.
+//   workgroup of each (query, KV head) merges the partials (log-sum-exp):
+//   the lanes of each float4 column of the result share the partials, load
+//   theirs in one batch of 16-byte buffer loads and combine by a DPP
+//   butterfly, then write out[h] = o/l.  It resets the arrival counter to
+//   zero, so no memset is needed between launches.
 //   Partials travel through agent-coherent stores/loads and a relaxed
 //   counter; no device-wide fence (L2 writeback/invalidate) is executed.
 //
@@ -60,7 +63,7 @@ struct DecodeArgs {
   const float* v_new;   //   row pos0 before attention; null when not fused
 };
 
-// Compile-time batch size of a split merge.
+// Compile-time integer argument (merge batch size, DPP control) for lambdas.
 template <int N> struct merge_batch { static constexpr int value = N; };
 
 template <typename KV, int D, int G, int NIT, int NW>
@@ -119,12 +122,17 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
   const char* kbase = (const char*)a.k + ((long long)kvh * D + col * EPL) * KV::bytes;
   const char* vbase = (const char*)a.v + ((long long)kvh * D + col * EPL) * KV::bytes;
 
+  // Slots past the group (gs < G) reload head h_lo and are zeroed through the
+  // scale: every load is valid, so none is predicated.  A predicated load per
+  // element compiled to one dependent memory round trip each (~5 us of a
+  // 17 us GQA launch).
   float qv[G][EPL];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const float* qp = a.q + ((long long)b * a.n_heads + h_lo + (g < gs ? g : 0)) * D + col * EPL;
+    const float sc = g < gs ? a.scale_log2 : 0.0f;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) qv[g][e] = (g < gs) ? qp[e] * a.scale_log2 : 0.0f;
+    for (int e = 0; e < EPL; ++e) qv[g][e] = qp[e] * sc;
   }
 
   float m[G], l[G], acc[G][EPL];
@@ -304,68 +312,88 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     return s_last != 0;
   };
   // Merge `count` partials src[first .. first+count) of this (query, KV
-  // head) -- [slot][G][D] values, [slot][G][2] (m, l) -- in batches of MB
-  // whose loads are all issued together, with an online rescale between
-  // batches.  Writes out = O / L, or the merged (O, m, l) into slot dst of
-  // the group partials.
+  // head) -- [slot][G][D] values, [slot][G][2] (m, l) -- into out = O / L,
+  // or into slot dst of the group partials.  A partial is MC float4 columns;
+  // MP adjacent lanes share a column and lane p takes slots p, p + MP, ...:
+  // MB slots per lane per batch, all loads of a batch in flight together,
+  // then a log-sum-exp butterfly over the MP lanes (DPP, within a row).
+  // Slots past `count`, and lanes without a live column, load at an offset
+  // past the buffer's range: zeros, no memory access, no branch.
+  constexpr int MC = G * D / 4;
+  constexpr int MP = NT >= 16 * MC ? 16 : (NT >= MC ? NT / MC : 1);
+  constexpr int MCP = NT / MP;  // columns per pass
   auto merge = [&](auto batch, const float* src_o, const float* src_ml, long long first, int count, bool to_out,
                    long long dst) {
     constexpr int MB = decltype(batch)::value;
-    for (int idx = threadIdx.x; idx < G * D; idx += NT) {
-      const int g = idx / D, d = idx % D;
-      if (g >= gs) continue;
-      float M = -INFINITY, L = 0.0f, O = 0.0f;
-      for (int f0 = 0; f0 < count; f0 += MB) {
-        const int cnt = count - f0 < MB ? count - f0 : MB;
-        // A full batch is straight-line code, so all its loads are in flight
-        // together.  In a short final batch the slots past cnt are skipped
-        // by wave-uniform branches rather than clamped: repeated coherent
-        // loads of one address serialize.
-        float mv[MB], lv[MB], ov[MB];
-        if (cnt == MB) {
+    const int p = threadIdx.x % MP;
+    const auto ro = buffer_rsrc(src_o + first * G * D, (unsigned)count * G * D * 4);
+    const auto rm = buffer_rsrc(src_ml + first * G * 2, (unsigned)count * G * 8);
+    for (int c0 = 0; c0 < MC; c0 += MCP) {
+      const int c = c0 + (int)threadIdx.x / MP;
+      const int g = c / (D / 4), d4 = c % (D / 4);
+      const bool live = c < MC && g < gs;
+      float M = -INFINITY, L = 0.0f, O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int f0 = 0; f0 < count; f0 += MP * MB) {
+        float ov[MB][4], mv[MB], lv[MB];
 #pragma unroll
-          for (int j = 0; j < MB; ++j) {
-            const long long pj = (first + f0 + j) * G + g;
-            mv[j] = load_coherent(&src_ml[pj * 2]);
-            lv[j] = load_coherent(&src_ml[pj * 2 + 1]);
-            ov[j] = load_coherent(&src_o[pj * D + d]);
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < MB; ++j) {
-            mv[j] = -INFINITY;
-            lv[j] = 0.0f;
-            ov[j] = 0.0f;
-            if (j < cnt) {
-              const long long pj = (first + f0 + j) * G + g;
-              mv[j] = load_coherent(&src_ml[pj * 2]);
-              lv[j] = load_coherent(&src_ml[pj * 2 + 1]);
-              ov[j] = load_coherent(&src_o[pj * D + d]);
-            }
-          }
+        for (int i = 0; i < MB; ++i) {
+          const int sl = f0 + p + MP * i;
+          const int se = (live && sl < count) ? sl : count;
+          buffer_load16_coherent(ro, ((se * G + g) * D + d4 * 4) * 4, ov[i][0], ov[i][1], ov[i][2], ov[i][3]);
+          buffer_load8_coherent(rm, (se * G + g) * 8, mv[i], lv[i]);
         }
         float Mb = M;
 #pragma unroll
-        for (int j = 0; j < MB; ++j) Mb = fmaxf(Mb, mv[j]);
-        if (Mb == -INFINITY) continue;  // nothing attended yet
-        const float c = exp2_fast(M - Mb);  // 0 while M is -inf
-        L *= c;
-        O *= c;
+        for (int i = 0; i < MB; ++i) {
+          const bool ok = live && f0 + p + MP * i < count;
+          mv[i] = ok ? mv[i] : -INFINITY;
+          Mb = fmaxf(Mb, mv[i]);
+        }
+        // Branch-free (a branch here lets the compiler split the loads and
+        // sink the parts used under it, a second round trip): with nothing
+        // attended yet Mb stays -inf and every factor is 0.
+        const float Ms = Mb == -INFINITY ? 0.0f : Mb;
+        const float cm = M == -INFINITY ? 0.0f : exp2_fast(M - Ms);
+        L *= cm;
 #pragma unroll
-        for (int j = 0; j < MB; ++j) {
-          if (mv[j] != -INFINITY) {
-            const float f = exp2_fast(mv[j] - Mb);
-            L += lv[j] * f;
-            O += ov[j] * f;
-          }
+        for (int k = 0; k < 4; ++k) O[k] *= cm;
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+          const float f = mv[i] == -INFINITY ? 0.0f : exp2_fast(mv[i] - Ms);
+          L = fmaf(lv[i], f, L);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) O[k] = fmaf(ov[i][k], f, O[k]);
         }
         M = Mb;
       }
-      if (to_out) {
-        a.out[((long long)b * a.n_heads + h_lo + g) * D + d] = O / L;
-      } else {
-        store_coherent(&a.wg_o[(dst * G + g) * D + d], O);
-        if (d == 0) {
+      // Butterfly over the MP lanes of the column (every lane active).
+      auto fold = [&](auto ctrl) {
+        constexpr int CTRL = decltype(ctrl)::value;
+        const float Mo = dpp<CTRL>(M), Lo = dpp<CTRL>(L);
+        float Oo[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) Oo[k] = dpp<CTRL>(O[k]);
+        const float Mn = fmaxf(M, Mo);
+        const float fa = M == -INFINITY ? 0.0f : exp2_fast(M - Mn);
+        const float fb = Mo == -INFINITY ? 0.0f : exp2_fast(Mo - Mn);
+        L = L * fa + Lo * fb;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) O[k] = O[k] * fa + Oo[k] * fb;
+        M = Mn;
+      };
+      if constexpr (MP >= 2) fold(merge_batch<DPP_XOR1>{});
+      if constexpr (MP >= 4) fold(merge_batch<DPP_XOR2>{});
+      if constexpr (MP >= 8) fold(merge_batch<DPP_HALF_MIRROR>{});
+      if constexpr (MP >= 16) fold(merge_batch<DPP_MIRROR>{});
+      if (live && p == 0) {
+        if (to_out) {
+          float* op = a.out + ((long long)b * a.n_heads + h_lo + g) * D + d4 * 4;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) op[k] = O[k] / L;
+        } else {
+          float* op = a.wg_o + (dst * G + g) * D + d4 * 4;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) store_coherent(op + k, O[k]);
           store_coherent(&a.wg_ml[(dst * G + g) * 2 + 0], M);
           store_coherent(&a.wg_ml[(dst * G + g) * 2 + 1], L);
         }
@@ -376,13 +404,20 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
   if (!arrive(ctr0 + (long long)grp * decode_counter_stride, members)) return;
   const long long part0 = ((long long)b * a.n_kv + kvh) * a.n_splits;
   if (!two_level) {
-    merge(merge_batch<8>{}, a.ws_o, a.ws_ml, part0, n_act, true, 0);
+    // One slot per lane when the splits fit the column's lanes (C2's 8
+    // splits over 8 lanes); a batch of up to 16 slots per lane otherwise.
+    constexpr int MBF = (decode_merge_flat + MP - 1) / MP < 16 ? (decode_merge_flat + MP - 1) / MP : 16;
+    if (MBF > 1 && n_act <= MP)
+      merge(merge_batch<1>{}, a.ws_o, a.ws_ml, part0, n_act, true, 0);
+    else
+      merge(merge_batch<MBF>{}, a.ws_o, a.ws_ml, part0, n_act, true, 0);
     return;
   }
   const long long gpart0 = ((long long)b * a.n_kv + kvh) * n_groups;
-  merge(merge_batch<GS>{}, a.ws_o, a.ws_ml, part0 + (long long)grp * GS, members, false, gpart0 + grp);
+  constexpr int MBG = (GS + MP - 1) / MP;
+  merge(merge_batch<MBG>{}, a.ws_o, a.ws_ml, part0 + (long long)grp * GS, members, false, gpart0 + grp);
   if (!arrive(ctr0 + (long long)n_groups * decode_counter_stride, n_grp)) return;
-  merge(merge_batch<GS>{}, a.wg_o, a.wg_ml, gpart0, n_grp, true, 0);
+  merge(merge_batch<MBG>{}, a.wg_o, a.wg_ml, gpart0, n_grp, true, 0);
 }
 
 }  // namespace vtb
