@@ -150,13 +150,15 @@ def bench_decode(ctx, torch, args):
     }
 
 
-def bench_decode_cfg(ctx, torch, name, n_layers, n_heads, n_kv, d, kv, L, steps=8, warmup=2, seed=7):
+def bench_decode_cfg(ctx, torch, name, n_layers, n_heads, n_kv, d, kv, L, steps=8, warmup=2, seed=7, rope=False):
     """Decode of one BASELINE config shape: every step runs the fused
     append + attention launch for each of n_layers layers, the token at
     attended length L (the cache holds the L attended rows; a sliding
     window is the caller's offset shift of forward.zig:470-483, so only
     the window's rows need to exist).  Returns per-launch time from HIP
-    events on the context stream and the algorithmic GB/s."""
+    events on the context stream and the algorithmic GB/s.  rope=True fuses
+    the RoPE of q and k_cur at position L (interleaved form, base 10000) into
+    every launch (attn_decode_rope_append)."""
     import numpy as np
     import vantablack_amd as vb
     tdt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[kv]
@@ -184,8 +186,12 @@ def bench_decode_cfg(ctx, torch, name, n_layers, n_heads, n_kv, d, kv, L, steps=
 
     def one_step(seg):
         for l in range(n_layers):
-            seg.attn_decode_append(obs[l], qbs[l], kb, l * layer_bytes, vbuf, l * layer_bytes, kcs[l], vcs[l],
-                                   n_heads, n_kv, d, L, inv, vdt)
+            if rope:
+                seg.attn_decode_rope_append(obs[l], qbs[l], kb, l * layer_bytes, vbuf, l * layer_bytes, kcs[l],
+                                            vcs[l], n_heads, n_kv, d, L, inv, vdt, L, 10000.0, False)
+            else:
+                seg.attn_decode_append(obs[l], qbs[l], kb, l * layer_bytes, vbuf, l * layer_bytes, kcs[l], vcs[l],
+                                       n_heads, n_kv, d, L, inv, vdt)
 
     with ctx.segment() as seg:
         for _ in range(warmup):
@@ -406,6 +412,9 @@ def main():
         "C1": bench_decode_cfg(ctx, torch, "C1", 1, 32, 4, 64, "f32", 512, steps=64),
         "C3": bench_decode_cfg(ctx, torch, "C3", 32, 32, 8, 128, "bf16", 4096),
         "C5": bench_decode_cfg(ctx, torch, "C5", 26, 8, 1, 256, "bf16", 32768),
+        # C2's shape at 8K with the layer's RoPE of q and k_cur fused into
+        # the same launch (the next-row prologue), to price the rotation.
+        "C2_rope_fused": bench_decode_cfg(ctx, torch, "C2+RoPE", 32, 32, 32, 128, "f16", 8192, rope=True),
     }
     pre = {} if args.no_prefill else {
         "C4_L512": bench_prefill(ctx, torch, 32, 8, 128, 512),

@@ -137,6 +137,27 @@ void vtb_hip_segment_attn_decode_append(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbH
                                         size_t n_heads, size_t n_kv_heads, size_t head_dim,
                                         size_t seq_len, float inv_sqrt_hd, int kv_dtype);
 
+/* vtb_hip_segment_attn_decode_append with RoPE fused in front: q (all
+ * n_heads) and k_cur (all n_kv_heads) are rotated at absolute position
+ * rope_pos -- math.rope, interleaved pairs, or with rope_half math.ropeHalf,
+ * pairs (i, i + head_dim/2) (src/kernels/math.zig:85-133), angle
+ * rope_pos / rope_base^(2j/head_dim) -- before the slot write and the
+ * attention.  Replaces the Metal sequence seg.rope(q), seg.rope(k_cur)
+ * (forward.zig:463-464; kernel rope_inplace, bridge.m:130-150, which has
+ * only the interleaved form), seg.copy x2 (:467-468) and the attention trio
+ * (:481-483) with one launch.  q_buf and k_cur_buf are read, not rotated in
+ * place (nothing reads them afterwards in the reference).  rope_pos is
+ * separate from seq_len because a sliding window shifts the K/V view.  The
+ * first call per (rope_base, head_dim) uploads a head_dim/2-float table.
+ * rope_base finite and > 0; rope_pos <= 2^24. */
+void vtb_hip_segment_attn_decode_rope_append(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *q_buf,
+                                             VtbHipBuf *k_cache_buf, size_t k_cache_offset_bytes,
+                                             VtbHipBuf *v_cache_buf, size_t v_cache_offset_bytes,
+                                             VtbHipBuf *k_cur_buf, VtbHipBuf *v_cur_buf,
+                                             size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                             size_t seq_len, float inv_sqrt_hd, int kv_dtype,
+                                             size_t rope_pos, float rope_base, int rope_half);
+
 /* Causal prefill attention for n_tokens queries of one layer.  Query b sits
  * at absolute position pos0 + b and attends rows [window_start(pos0+b),
  * pos0+b] of the layer whose row 0 is at layer_offset_bytes in k/v, where
@@ -187,6 +208,15 @@ int vtb_hip_kv_cache_shrink_to_fit(VtbHipKvCache *cache, size_t new_max_seq);
 int vtb_hip_layer_attention(VtbHipSeg *seg, VtbHipKvCache *cache, const VtbHipAttnConfig *c,
                             size_t layer, VtbHipBuf *q, VtbHipBuf *k_cur, VtbHipBuf *v_cur,
                             VtbHipBuf *attn_out);
+
+/* vtb_hip_layer_attention with the layer's RoPE fused in: the whole of
+ * forward.zig:250-270 -- math.rope / math.ropeHalf (rope_half, LlamaConfig
+ * .rope_half, model.zig:57) of q per head and of k_cur per KV head at
+ * cache->pos with rope_base (LlamaConfig.rope_base, model.zig:50), the slot
+ * write, cpuAttention -- in one launch.  q and k_cur are not modified. */
+int vtb_hip_layer_attention_rope(VtbHipSeg *seg, VtbHipKvCache *cache, const VtbHipAttnConfig *c,
+                                 size_t layer, VtbHipBuf *q, VtbHipBuf *k_cur, VtbHipBuf *v_cur,
+                                 VtbHipBuf *attn_out, float rope_base, int rope_half);
 
 /* Prefill, one layer (prefill.zig:174-197): write the n_tokens rows of
  * k_cur/v_cur (f32 [n_tokens][kv_dim]) into slots pos..pos+n_tokens-1, then

@@ -96,6 +96,50 @@ void vtb_oracle_upcast_bf16(const uint16_t *src, float *dst, size_t n) {
 /* math.zig                                                                */
 /* ---------------------------------------------------------------------- */
 
+/* math.zig:85-107 -- math.rope: in-place RoPE of one head (x has head_dim
+ * elements) at absolute position pos.  Interleaved pairs (x[i], x[i+1]),
+ * i even, rotated by theta = pos * inv_freq with inv_freq = 1 / base^(i/d),
+ * all in f32; the exponent i/d is an f32 quotient (:94). */
+void vtb_oracle_rope(float *x, size_t head_dim, size_t pos, float base) {
+    const float pos_f = (float)pos;
+    for (size_t i = 0; i + 1 < head_dim; i += 2) {
+        const float e = (float)i / (float)head_dim;
+        const float inv_freq = 1.0f / powf(base, e);
+        const float theta = pos_f * inv_freq;
+        const float c = cosf(theta);
+        const float s = sinf(theta);
+        const float x0 = x[i];
+        const float x1 = x[i + 1];
+        x[i] = x0 * c - x1 * s;
+        x[i + 1] = x0 * s + x1 * c;
+    }
+}
+
+/* math.zig:109-133 -- math.ropeHalf: element i pairs with i + d/2, both
+ * rotated by theta_i = pos / base^(2i/d), i < d/2. */
+void vtb_oracle_rope_half(float *x, size_t head_dim, size_t pos, float base) {
+    const size_t half = head_dim / 2;
+    const float pos_f = (float)pos;
+    for (size_t i = 0; i < half; i++) {
+        const float e = (float)(2 * i) / (float)head_dim;
+        const float inv_freq = 1.0f / powf(base, e);
+        const float theta = pos_f * inv_freq;
+        const float c = cosf(theta);
+        const float s = sinf(theta);
+        const float x0 = x[i];
+        const float x1 = x[i + half];
+        x[i] = x0 * c - x1 * s;
+        x[i + half] = x0 * s + x1 * c;
+    }
+}
+
+/* The per-pair inverse frequencies both forms use, inv_freq[j] =
+ * 1 / base^(2j/d) for j < d/2 (math.zig:95-96 with i = 2j, :124-125). */
+void vtb_oracle_rope_inv_freq(float *out, size_t head_dim, float base) {
+    for (size_t j = 0; j < head_dim / 2; j++)
+        out[j] = 1.0f / powf(base, (float)(2 * j) / (float)head_dim);
+}
+
 /* math.zig:136-150 -- in-place softmax: max, exp(x-max) with a sequential
  * sum, then multiply by inv = 1/sum (a reciprocal multiply, not a divide). */
 void vtb_oracle_softmax(float *x, size_t n) {

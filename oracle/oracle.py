@@ -11,6 +11,7 @@ Contents:
     (src/runtime/prefill.zig:237-287), ``math.softmax`` (src/kernels/math.zig:
     136-150), the KvCache layout (src/runtime/kv_cache.zig) and the pool
     (src/runtime/pool.zig));
+  * ``math.rope`` / ``math.ropeHalf`` (src/kernels/math.zig:85-133);
   * the portable seeded input generator (SplitMix64 -> f64 Box-Muller -> f32
     -> KV dtype) used for every parity input;
   * exact dtype helpers (f32 -> f16/bf16 round-to-nearest-even, and the exact
@@ -60,6 +61,9 @@ def lib():
         L = ctypes.CDLL(_LIB_PATH)
         P, S, F = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float
         L.vtb_oracle_softmax.argtypes = [P, S]
+        L.vtb_oracle_rope.argtypes = [P, S, S, F]
+        L.vtb_oracle_rope_half.argtypes = [P, S, S, F]
+        L.vtb_oracle_rope_inv_freq.argtypes = [P, S, F]
         L.vtb_oracle_argmax.argtypes = [P, S]
         L.vtb_oracle_argmax.restype = S
         L.vtb_oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
@@ -183,6 +187,24 @@ def softmax(x: np.ndarray) -> np.ndarray:
     y = np.ascontiguousarray(x, dtype=np.float32).copy()
     lib().vtb_oracle_softmax(_ptr(y), y.size)
     return y
+
+
+def rope(x: np.ndarray, pos: int, base: float, half: bool = False) -> np.ndarray:
+    """math.rope / math.ropeHalf (src/kernels/math.zig:85-133) applied to every
+    head of x (shape [..., head_dim]); returns a rotated f32 copy."""
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    d = y.shape[-1]
+    fn = lib().vtb_oracle_rope_half if half else lib().vtb_oracle_rope
+    flat = y.reshape(-1, d)
+    for h in range(flat.shape[0]):
+        fn(flat.ctypes.data + h * d * 4, d, pos, base)
+    return y
+
+
+def rope_inv_freq(head_dim: int, base: float) -> np.ndarray:
+    out = np.empty(head_dim // 2, dtype=np.float32)
+    lib().vtb_oracle_rope_inv_freq(_ptr(out), head_dim, base)
+    return out
 
 
 def argmax(x: np.ndarray) -> int:

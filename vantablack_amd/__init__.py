@@ -7,6 +7,7 @@ vantablack's attention interface.  Build with `python -m vantablack_amd.build`.
 from . import hip  # noqa: F401
 from .hip import (  # noqa: F401
     BF16, F16, F32, NO_WINDOW, Buffer, Context, HipAttentionBackend, HipError, KvCache,
-    KvCacheFull, LlamaConfig, NewMaxSeqBelowPos, Segment, layer_attention, prefill_attention,
+    KvCacheFull, LlamaConfig, NewMaxSeqBelowPos, Segment, layer_attention, layer_attention_rope,
+    prefill_attention,
     step_attention,
 )

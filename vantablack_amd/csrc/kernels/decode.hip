@@ -61,7 +61,41 @@ struct DecodeArgs {
   int pad;
   const float* k_new;   // optional (decode only): f32 K/V row appended at
   const float* v_new;   //   row pos0 before attention; null when not fused
+  const float* rope_inv_freq;  // optional: [D/2] 1/base^(2j/D); RoPE of q and
+  long long rope_pos;          //   k_new at absolute position rope_pos is
+  int rope_half;               //   fused when set (half form if rope_half)
+  int pad2;
 };
+
+// sin and cos of an f32 RoPE angle.  The angle (up to ~2^24 rad) is
+// reduced in f64: theta / (2 pi) in revolutions, keeping the signed fraction
+// (absolute error < 1e-9 rev), then rounded to f32 (< 3e-8 rev) and fed to
+// the hardware v_sin / v_cos, which take revolutions.  About ten
+// instructions against the library sincosf's large-argument reduction; the
+// GPU RoPE tests hold the result to the host libm at 2e-6 of the row.
+__device__ inline void rope_sincos(float theta, float* sn, float* cs) {
+  const double rev = (double)theta * 0.15915494309189533577;  // 1 / (2 pi)
+  const float r = (float)(rev - __builtin_rint(rev));
+  *sn = __builtin_amdgcn_sinf(r);
+  *cs = __builtin_amdgcn_cosf(r);
+}
+
+// RoPE of element i of one head x[0..D) (math.rope / math.ropeHalf,
+// src/kernels/math.zig:85-133): pair partner i^1 (interleaved) or i +- D/2
+// (half form), angle pos * inv_freq[pair] (the f32 product the reference
+// forms), strict f32 products.
+template <int D>
+__device__ inline float rope_elem(const float* x, int i, const float* inv_freq, float pos_f, bool half) {
+#pragma clang fp contract(off)
+  const int j = half ? (i % (D / 2)) : (i >> 1);
+  float sn, cs;
+  rope_sincos(pos_f * inv_freq[j], &sn, &cs);
+  const bool first = half ? (i < D / 2) : ((i & 1) == 0);
+  const int i0 = half ? j : (i & ~1);
+  const int i1 = half ? j + D / 2 : (i | 1);
+  const float x0 = x[i0], x1 = x[i1];
+  return first ? x0 * cs - x1 * sn : x0 * sn + x1 * cs;
+}
 
 // Compile-time integer argument (merge batch size, DPP control) for lambdas.
 template <int N> struct merge_batch { static constexpr int value = N; };
@@ -108,8 +142,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
   // barrier, so the later loads from the same CU see them.
   if (a.k_new != nullptr && a.pos0 >= r0 && a.pos0 < r1) {
     const long long off = a.pos0 * (long long)a.n_kv * D + (long long)kvh * D;
+    const float* kn = a.k_new + (long long)kvh * D;
     for (int i = threadIdx.x; i < D; i += NT) {
-      store_kv<KV>((void*)a.k, off + i, a.k_new[(long long)kvh * D + i]);
+      const float kval = a.rope_inv_freq ? rope_elem<D>(kn, i, a.rope_inv_freq, (float)a.rope_pos, a.rope_half != 0)
+                                         : kn[i];
+      store_kv<KV>((void*)a.k, off + i, kval);
       store_kv<KV>((void*)a.v, off + i, a.v_new[(long long)kvh * D + i]);
     }
     wait_stores();
@@ -121,28 +158,6 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
   const long long row_stride = (long long)a.n_kv * D;  // elements
   const char* kbase = (const char*)a.k + ((long long)kvh * D + col * EPL) * KV::bytes;
   const char* vbase = (const char*)a.v + ((long long)kvh * D + col * EPL) * KV::bytes;
-
-  // Slots past the group (gs < G) reload head h_lo and are zeroed through the
-  // scale: every load is valid, so none is predicated.  A predicated load per
-  // element compiled to one dependent memory round trip each (~5 us of a
-  // 17 us GQA launch).
-  float qv[G][EPL];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float* qp = a.q + ((long long)b * a.n_heads + h_lo + (g < gs ? g : 0)) * D + col * EPL;
-    const float sc = g < gs ? a.scale_log2 : 0.0f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) qv[g][e] = qp[e] * sc;
-  }
-
-  float m[G], l[G], acc[G][EPL];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
-  }
 
   // This wave's contiguous rows [w0, w1): an equal share, rounded to RPW.
   const long long per_wave = ((r1 - r0 + NW - 1) / NW + RPW - 1) / RPW * RPW;
@@ -163,6 +178,75 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
       vr[i] = load16(vbase + rc * row_stride * KV::bytes);
     }
   };
+  // Slots past the group (gs < G) reload head h_lo and are zeroed through the
+  // scale: every load is valid, so none is predicated.  A predicated load per
+  // element compiled to one dependent memory round trip each (~5 us of a
+  // 17 us GQA launch).
+  float qv[G][EPL];
+  if (a.rope_inv_freq == nullptr) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float* qp = a.q + ((long long)b * a.n_heads + h_lo + (g < gs ? g : 0)) * D + col * EPL;
+      const float sc = g < gs ? a.scale_log2 : 0.0f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) qv[g][e] = qp[e] * sc;
+    }
+  } else {
+    // Fused RoPE of q (wave-uniform branch).  The lane's EPL elements hold
+    // whole interleaved pairs; in the half form their partners are the
+    // same positions in the other half, loaded alongside.  The angles
+    // depend only on the element index, so the G heads share them.
+#pragma clang fp contract(off)
+    const bool half = a.rope_half != 0;
+    const bool lower = col * EPL < D / 2;
+    const float pos_f = (float)a.rope_pos;
+    float cs[EPL], sn[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const int i = col * EPL + e;
+      if (half || (e & 1) == 0) {
+        rope_sincos(pos_f * a.rope_inv_freq[half ? (i % (D / 2)) : (i >> 1)], &sn[e], &cs[e]);
+      } else {  // the second element of an interleaved pair shares its angle
+        sn[e] = sn[e - 1];
+        cs[e] = cs[e - 1];
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float* qp = a.q + ((long long)b * a.n_heads + h_lo + (g < gs ? g : 0)) * D + col * EPL;
+      const float* pp = qp + (lower ? D / 2 : -(D / 2));
+      const float sc = g < gs ? a.scale_log2 : 0.0f;
+      float x[EPL], y[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) x[e] = qp[e];
+      if (half) {  // wave-uniform: only the half form reads the partner block
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) y[e] = pp[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) y[e] = 0.0f;
+      }
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        float r;
+        if (half)
+          r = lower ? x[e] * cs[e] - y[e] * sn[e] : y[e] * sn[e] + x[e] * cs[e];
+        else
+          r = (e & 1) == 0 ? x[e] * cs[e] - x[e + 1] * sn[e] : x[e - 1] * sn[e] + x[e] * cs[e];
+        qv[g][e] = r * sc;
+      }
+    }
+  }
+
+  float m[G], l[G], acc[G][EPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
+  }
+
   auto compute = [&](long long t0, const u32x4 (&kr)[NIT], const u32x4 (&vr)[NIT]) {
     float s[G][NIT];
 #pragma unroll

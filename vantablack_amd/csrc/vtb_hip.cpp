@@ -16,6 +16,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "tiles.h"
 
@@ -58,6 +59,10 @@ struct DecodeArgs {
   int pad;
   const float* k_new;
   const float* v_new;
+  const float* rope_inv_freq;
+  long long rope_pos;
+  int rope_half;
+  int pad2;
 };
 
 // Arguments of vtb_prefill_* / vtb_vt_* (layouts must match prefill.hip).
@@ -122,6 +127,15 @@ struct VtbHipCtx {
   // Prefill V^T scratch (f16, written by the vtb_vt_* pre-pass).
   void* vt = nullptr;
   size_t vt_bytes = 0;
+  // RoPE inverse-frequency tables 1/base^(2j/d) on the device, one per
+  // (base, head_dim) seen; the host copy stays alive for the async upload.
+  struct RopeTable {
+    float base;
+    size_t head_dim;
+    std::vector<float> host;
+    float* dev;
+  };
+  std::vector<RopeTable> rope_tables;
   std::string err;
 };
 
@@ -218,10 +232,42 @@ int env_int(const char* name, int dflt) {
 // pos0 + b and attend [window_start, pos0 + b] of the layer rows at k/v.
 // With k_new/v_new (decode, n_q == 1) the kernel first writes that f32 row,
 // rounded to the cache dtype, into row pos0 (the fused KV-slot append).
+// The device table inv_freq[j] = 1/base^(2j/d), j < d/2, exactly as
+// math.rope / math.ropeHalf compute it (src/kernels/math.zig:94-96, :123-125:
+// an f32 exponent, f32 pow, f32 reciprocal), built once per (base, d) with
+// the host libm and uploaded on the context stream.  The kernel then forms
+// each angle as the same f32 product pos * inv_freq[j].
+const float* rope_table(VtbHipCtx* ctx, float base, size_t head_dim) {
+  for (const auto& t : ctx->rope_tables)
+    if (t.base == base && t.head_dim == head_dim) return t.dev;
+  VtbHipCtx::RopeTable t{base, head_dim, std::vector<float>(head_dim / 2), nullptr};
+  for (size_t j = 0; j < head_dim / 2; ++j)
+    t.host[j] = 1.0f / powf(base, (float)(2 * j) / (float)head_dim);
+  if (hipMalloc((void**)&t.dev, t.host.size() * sizeof(float)) != hipSuccess) {
+    set_err(ctx, VTB_HIP_EDEVICE, "hipMalloc (rope table)");
+    return nullptr;
+  }
+  if (hipMemcpyAsync(t.dev, t.host.data(), t.host.size() * sizeof(float), hipMemcpyHostToDevice, ctx->stream) !=
+      hipSuccess) {
+    (void)hipFree(t.dev);
+    set_err(ctx, VTB_HIP_EDEVICE, "hipMemcpyAsync (rope table)");
+    return nullptr;
+  }
+  ctx->rope_tables.push_back(std::move(t));
+  return ctx->rope_tables.back().dev;
+}
+
+// RoPE fused into a decode launch: q and k_new are rotated at rope_pos.
+struct RopeArgs {
+  const float* inv_freq = nullptr;  // null: no RoPE
+  long long pos = 0;
+  int half = 0;
+};
+
 int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, const void* v,
                   size_t n_q, size_t n_heads, size_t n_kv, size_t head_dim, long long pos0,
                   long long window, float inv_sqrt_hd, int dtype, const float* k_new = nullptr,
-                  const float* v_new = nullptr) {
+                  const float* v_new = nullptr, RopeArgs rope = RopeArgs()) {
   const int di = d_index(head_dim);
   if (di < 0) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "head_dim must be 64, 128 or 256");
   if (dtype < 0 || dtype >= kNumKv) return set_err(ctx, VTB_HIP_EINVAL, "bad kv dtype");
@@ -284,6 +330,10 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
   if (k_new && (n_q != 1 || !v_new)) return set_err(ctx, VTB_HIP_EINVAL, "fused append needs one query");
   a.k_new = k_new;
   a.v_new = v_new;
+  if (rope.inv_freq && (n_q != 1 || !k_new)) return set_err(ctx, VTB_HIP_EINVAL, "fused RoPE needs the fused append");
+  a.rope_inv_freq = rope.inv_freq;
+  a.rope_pos = rope.pos;
+  a.rope_half = rope.half;
   return launch(ctx, ctx->f_decode[dtype][di][gi], (unsigned)n_splits, (unsigned)n_kv,
                 (unsigned)n_q, 64 * vtb::decode_waves(G), &a);
 }
@@ -427,6 +477,7 @@ extern "C" void vtb_hip_destroy(VtbHipCtx* ctx) {
   if (ctx->counters) (void)hipFree(ctx->counters);
   if (ctx->qconv) (void)hipFree(ctx->qconv);
   if (ctx->vt) (void)hipFree(ctx->vt);
+  for (auto& t : ctx->rope_tables) (void)hipFree(t.dev);
   if (ctx->mod_decode) (void)hipModuleUnload(ctx->mod_decode);
   if (ctx->mod_prefill) (void)hipModuleUnload(ctx->mod_prefill);
   if (ctx->mod_kvcopy) (void)hipModuleUnload(ctx->mod_kvcopy);
@@ -573,29 +624,69 @@ extern "C" void vtb_hip_segment_attn_decode(VtbHipSeg* seg, VtbHipBuf* out_buf, 
                               head_dim, (long long)seq_len - 1, 0, inv_sqrt_hd, kv_dtype));
 }
 
+// Shared body of the fused-append decode entries (with or without RoPE).
+static void decode_append_entry(const char* name, VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* q_buf,
+                                VtbHipBuf* k_cache_buf, size_t k_cache_offset_bytes, VtbHipBuf* v_cache_buf,
+                                size_t v_cache_offset_bytes, VtbHipBuf* k_cur_buf, VtbHipBuf* v_cur_buf,
+                                size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t seq_len,
+                                float inv_sqrt_hd, int kv_dtype, const RopeArgs& rope) {
+  VtbHipCtx* ctx = seg->ctx;
+  const std::string who(name);
+  const int eb = kv_bytes(kv_dtype);
+  if (!eb || n_heads == 0 || n_kv_heads == 0 || head_dim == 0 || n_heads > 65535 ||
+      n_kv_heads > 65535 || head_dim > 4096 || seq_len == 0)
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, (who + ": bad shape").c_str()));
+  const size_t qbytes = n_heads * head_dim * 4;
+  const size_t kv_dim = n_kv_heads * head_dim;
+  if (!buf_ok(out_buf, 0, qbytes) || !buf_ok(q_buf, 0, qbytes) || !buf_ok(k_cur_buf, 0, kv_dim * 4) ||
+      !buf_ok(v_cur_buf, 0, kv_dim * 4))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, (who + ": q/out/k_cur/v_cur too small").c_str()));
+  const size_t kv_rows_bytes = seq_len * kv_dim * eb;
+  if (!buf_ok(k_cache_buf, k_cache_offset_bytes, kv_rows_bytes) ||
+      !buf_ok(v_cache_buf, v_cache_offset_bytes, kv_rows_bytes))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, (who + ": K/V range outside buffer").c_str()));
+  seg_note(seg, launch_decode(ctx, (float*)out_buf->ptr, (const float*)q_buf->ptr,
+                              bptr(k_cache_buf, k_cache_offset_bytes), bptr(v_cache_buf, v_cache_offset_bytes),
+                              1, n_heads, n_kv_heads, head_dim, (long long)seq_len - 1, 0, inv_sqrt_hd,
+                              kv_dtype, (const float*)k_cur_buf->ptr, (const float*)v_cur_buf->ptr, rope));
+}
+
+// RoPE arguments for a fused launch, or an error (base must be finite and
+// positive, head_dim even, pos within 2^24 so (float)pos is exact).
+static int rope_args(VtbHipCtx* ctx, size_t head_dim, size_t pos, float base, int half, RopeArgs* out) {
+  if (!(base > 0.0f) || !std::isfinite(base) || head_dim % 2 != 0)
+    return set_err(ctx, VTB_HIP_EINVAL, "rope: base must be finite and > 0, head_dim even");
+  if (pos > ((size_t)1 << 24)) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "rope: position beyond 2^24");
+  const float* t = rope_table(ctx, base, head_dim);
+  if (!t) return VTB_HIP_EDEVICE;
+  out->inv_freq = t;
+  out->pos = (long long)pos;
+  out->half = half ? 1 : 0;
+  return VTB_HIP_OK;
+}
+
 extern "C" void vtb_hip_segment_attn_decode_append(
     VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* q_buf, VtbHipBuf* k_cache_buf, size_t k_cache_offset_bytes,
     VtbHipBuf* v_cache_buf, size_t v_cache_offset_bytes, VtbHipBuf* k_cur_buf, VtbHipBuf* v_cur_buf,
     size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t seq_len, float inv_sqrt_hd, int kv_dtype) {
   if (!seg) return;
-  VtbHipCtx* ctx = seg->ctx;
-  const int eb = kv_bytes(kv_dtype);
-  if (!eb || n_heads == 0 || n_kv_heads == 0 || head_dim == 0 || n_heads > 65535 ||
-      n_kv_heads > 65535 || head_dim > 4096 || seq_len == 0)
-    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_decode_append: bad shape"));
-  const size_t qbytes = n_heads * head_dim * 4;
-  const size_t kv_dim = n_kv_heads * head_dim;
-  if (!buf_ok(out_buf, 0, qbytes) || !buf_ok(q_buf, 0, qbytes) || !buf_ok(k_cur_buf, 0, kv_dim * 4) ||
-      !buf_ok(v_cur_buf, 0, kv_dim * 4))
-    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_decode_append: q/out/k_cur/v_cur too small"));
-  const size_t kv_rows_bytes = seq_len * kv_dim * eb;
-  if (!buf_ok(k_cache_buf, k_cache_offset_bytes, kv_rows_bytes) ||
-      !buf_ok(v_cache_buf, v_cache_offset_bytes, kv_rows_bytes))
-    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_decode_append: K/V range outside buffer"));
-  seg_note(seg, launch_decode(ctx, (float*)out_buf->ptr, (const float*)q_buf->ptr,
-                              bptr(k_cache_buf, k_cache_offset_bytes), bptr(v_cache_buf, v_cache_offset_bytes),
-                              1, n_heads, n_kv_heads, head_dim, (long long)seq_len - 1, 0, inv_sqrt_hd,
-                              kv_dtype, (const float*)k_cur_buf->ptr, (const float*)v_cur_buf->ptr));
+  decode_append_entry("attn_decode_append", seg, out_buf, q_buf, k_cache_buf, k_cache_offset_bytes, v_cache_buf,
+                      v_cache_offset_bytes, k_cur_buf, v_cur_buf, n_heads, n_kv_heads, head_dim, seq_len,
+                      inv_sqrt_hd, kv_dtype, RopeArgs());
+}
+
+extern "C" void vtb_hip_segment_attn_decode_rope_append(
+    VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* q_buf, VtbHipBuf* k_cache_buf, size_t k_cache_offset_bytes,
+    VtbHipBuf* v_cache_buf, size_t v_cache_offset_bytes, VtbHipBuf* k_cur_buf, VtbHipBuf* v_cur_buf,
+    size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t seq_len, float inv_sqrt_hd, int kv_dtype,
+    size_t rope_pos, float rope_base, int rope_half) {
+  if (!seg) return;
+  RopeArgs rope;
+  const int rc = rope_args(seg->ctx, head_dim, rope_pos, rope_base, rope_half, &rope);
+  if (rc) return seg_note(seg, rc);
+  decode_append_entry("attn_decode_rope_append", seg, out_buf, q_buf, k_cache_buf, k_cache_offset_bytes,
+                      v_cache_buf, v_cache_offset_bytes, k_cur_buf, v_cur_buf, n_heads, n_kv_heads, head_dim,
+                      seq_len, inv_sqrt_hd, kv_dtype, rope);
 }
 
 extern "C" void vtb_hip_segment_attn_prefill(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* q_buf,
@@ -742,9 +833,9 @@ static int check_cfg(const VtbHipKvCache* c, const VtbHipAttnConfig* cfg) {
   return VTB_HIP_OK;
 }
 
-extern "C" int vtb_hip_layer_attention(VtbHipSeg* seg, VtbHipKvCache* c, const VtbHipAttnConfig* cfg,
-                                       size_t layer, VtbHipBuf* q, VtbHipBuf* k_cur, VtbHipBuf* v_cur,
-                                       VtbHipBuf* attn_out) {
+static int layer_attention_impl(VtbHipSeg* seg, VtbHipKvCache* c, const VtbHipAttnConfig* cfg, size_t layer,
+                                VtbHipBuf* q, VtbHipBuf* k_cur, VtbHipBuf* v_cur, VtbHipBuf* attn_out,
+                                const float* rope_base, int rope_half) {
   if (!seg) return VTB_HIP_EINVAL;
   VtbHipCtx* ctx = seg->ctx;
   int rc = check_cfg(c, cfg);
@@ -756,16 +847,34 @@ extern "C" int vtb_hip_layer_attention(VtbHipSeg* seg, VtbHipKvCache* c, const V
   if (!buf_ok(q, 0, qn * 4) || !buf_ok(attn_out, 0, qn * 4) || !buf_ok(k_cur, 0, kv_dim * 4) ||
       !buf_ok(v_cur, 0, kv_dim * 4))
     return set_err(ctx, VTB_HIP_EINVAL, "layer_attention: buffer too small");
-  // One launch: the decode kernel writes the slot at pos (fused append),
-  // then attends [window_start(pos), pos].
+  RopeArgs rope;
+  if (rope_base) {
+    rc = rope_args(ctx, cfg->head_dim, c->pos, *rope_base, rope_half, &rope);
+    if (rc) return rc;
+  }
+  // One launch: the decode kernel (rotates q and k_cur at pos when RoPE is
+  // fused,) writes the slot at pos (fused append), then attends
+  // [window_start(pos), pos].
   const size_t lo = vtb_hip_kv_cache_layer_offset(c, layer);
   const float inv_sqrt_hd = 1.0f / sqrtf((float)cfg->head_dim);
   rc = launch_decode(ctx, (float*)attn_out->ptr, (const float*)q->ptr, bptr(c->k, lo), bptr(c->v, lo), 1,
                      cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, (long long)c->pos,
                      window_arg(cfg->sliding_window), inv_sqrt_hd, c->dtype, (const float*)k_cur->ptr,
-                     (const float*)v_cur->ptr);
+                     (const float*)v_cur->ptr, rope);
   seg_note(seg, rc);
   return rc;
+}
+
+extern "C" int vtb_hip_layer_attention(VtbHipSeg* seg, VtbHipKvCache* c, const VtbHipAttnConfig* cfg,
+                                       size_t layer, VtbHipBuf* q, VtbHipBuf* k_cur, VtbHipBuf* v_cur,
+                                       VtbHipBuf* attn_out) {
+  return layer_attention_impl(seg, c, cfg, layer, q, k_cur, v_cur, attn_out, nullptr, 0);
+}
+
+extern "C" int vtb_hip_layer_attention_rope(VtbHipSeg* seg, VtbHipKvCache* c, const VtbHipAttnConfig* cfg,
+                                            size_t layer, VtbHipBuf* q, VtbHipBuf* k_cur, VtbHipBuf* v_cur,
+                                            VtbHipBuf* attn_out, float rope_base, int rope_half) {
+  return layer_attention_impl(seg, c, cfg, layer, q, k_cur, v_cur, attn_out, &rope_base, rope_half);
 }
 
 extern "C" int vtb_hip_prefill_attention(VtbHipSeg* seg, VtbHipKvCache* c, const VtbHipAttnConfig* cfg,

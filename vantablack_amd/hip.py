@@ -12,6 +12,7 @@ Mirrors, by reference file:
   * ``LlamaConfig``                        -- the attention fields of
     src/runtime/model.zig LlamaConfig (:40-70);
   * ``layer_attention``                    -- KV write + cpuAttention
+  * ``layer_attention_rope``               -- RoPE + KV write + cpuAttention
     (src/runtime/forward.zig:267-270, :187-228);
   * ``prefill_attention``                  -- prefill KV write + the
     ``for b: attentionCausal`` loop (src/runtime/prefill.zig:174-197);
@@ -84,6 +85,8 @@ SIGNATURES = {
     "vtb_hip_segment_kv_append": ([_P, _P, _S, _I, _P, _S, _S], None),
     "vtb_hip_segment_attn_decode": ([_P, _P, _P, _P, _S, _P, _S, _S, _S, _S, _S, _F, _I], None),
     "vtb_hip_segment_attn_decode_append": ([_P, _P, _P, _P, _S, _P, _S, _P, _P, _S, _S, _S, _S, _F, _I], None),
+    "vtb_hip_segment_attn_decode_rope_append": ([_P, _P, _P, _P, _S, _P, _S, _P, _P, _S, _S, _S, _S, _F, _I,
+                                                 _S, _F, _I], None),
     "vtb_hip_segment_attn_prefill": ([_P, _P, _P, _P, _P, _S, _S, _S, _S, _S, _S, _S, _F, _I], None),
     "vtb_hip_kv_cache_init": ([_P, _S, _S, _S, _S, _I], _P),
     "vtb_hip_kv_cache_deinit": ([_P], None),
@@ -99,6 +102,7 @@ SIGNATURES = {
     "vtb_hip_kv_cache_v": ([_P], _P),
     "vtb_hip_kv_cache_shrink_to_fit": ([_P, _S], _I),
     "vtb_hip_layer_attention": ([_P, _P, ctypes.POINTER(AttnConfigC), _S, _P, _P, _P, _P], _I),
+    "vtb_hip_layer_attention_rope": ([_P, _P, ctypes.POINTER(AttnConfigC), _S, _P, _P, _P, _P, _F, _I], _I),
     "vtb_hip_prefill_attention": ([_P, _P, ctypes.POINTER(AttnConfigC), _S, _S, _P, _P, _P, _P], _I),
 }
 
@@ -135,6 +139,8 @@ class LlamaConfig:
     head_dim: int
     max_seq: int
     sliding_window: int = NO_WINDOW
+    rope_base: float = 10000.0  # model.zig:50
+    rope_half: bool = False     # model.zig:57
 
     def c(self) -> AttnConfigC:
         return AttnConfigC(self.n_heads, self.n_kv_heads, self.head_dim, self.max_seq,
@@ -200,6 +206,17 @@ class Segment:
                            seq_len: int, inv_sqrt_hd: float, kv_dtype: int):
         lib().vtb_hip_segment_attn_decode_append(self.h, out.h, q.h, k.h, k_off, v.h, v_off, k_cur.h, v_cur.h,
                                                  n_heads, n_kv_heads, head_dim, seq_len, inv_sqrt_hd, kv_dtype)
+
+    def attn_decode_rope_append(self, out: Buffer, q: Buffer, k: Buffer, k_off: int, v: Buffer, v_off: int,
+                                k_cur: Buffer, v_cur: Buffer, n_heads: int, n_kv_heads: int, head_dim: int,
+                                seq_len: int, inv_sqrt_hd: float, kv_dtype: int, rope_pos: int,
+                                rope_base: float, rope_half: bool = False):
+        """attn_decode_append with RoPE of q and k_cur at rope_pos fused in
+        (the Metal seg.rope x2 + seg.copy x2 + attention, forward.zig:463-483)."""
+        lib().vtb_hip_segment_attn_decode_rope_append(self.h, out.h, q.h, k.h, k_off, v.h, v_off, k_cur.h,
+                                                      v_cur.h, n_heads, n_kv_heads, head_dim, seq_len,
+                                                      inv_sqrt_hd, kv_dtype, rope_pos, rope_base,
+                                                      1 if rope_half else 0)
 
     def attn_prefill(self, out: Buffer, q: Buffer, k: Buffer, v: Buffer, layer_off: int, n_tokens: int,
                      pos0: int, sliding_window: int, n_heads: int, n_kv_heads: int, head_dim: int,
@@ -402,6 +419,17 @@ def layer_attention(seg: Segment, cache: KvCache, c: LlamaConfig, layer: int, q:
                                                     v_cur.h, attn_out.h), "layer_attention")
 
 
+def layer_attention_rope(seg: Segment, cache: KvCache, c: LlamaConfig, layer: int, q: Buffer,
+                         k_cur: Buffer, v_cur: Buffer, attn_out: Buffer):
+    """forward.zig:250-270 + cpuAttention for one layer: RoPE of q and k_cur
+    at cache.pos (math.rope, or math.ropeHalf when c.rope_half), the slot
+    write and the attention, in one launch.  q and k_cur are left unrotated."""
+    cc = c.c()
+    _check(seg.ctx.h, lib().vtb_hip_layer_attention_rope(seg.h, cache.h, ctypes.byref(cc), layer, q.h, k_cur.h,
+                                                         v_cur.h, attn_out.h, c.rope_base,
+                                                         1 if c.rope_half else 0), "layer_attention_rope")
+
+
 def prefill_attention(seg: Segment, cache: KvCache, c: LlamaConfig, layer: int, n_tokens: int, q: Buffer,
                       k_cur: Buffer, v_cur: Buffer, attn_out: Buffer):
     """prefill.zig:174-197 for one layer: write n_tokens K/V rows at
@@ -431,10 +459,15 @@ class HipAttentionBackend:
         self._seg = None
 
     def layer_step(self, cache: KvCache, c: LlamaConfig, layer: int, q: Buffer, k_cur: Buffer,
-                   v_cur: Buffer, attn_out: Buffer):
+                   v_cur: Buffer, attn_out: Buffer, rope: bool = False):
+        """rope=False: q / k_cur are already rotated (forward.zig:250-265 ran
+        on the host); rope=True: they are not, and RoPE is fused in."""
         if self._seg is None:
             self._seg = self.ctx.segment()
-        layer_attention(self._seg, cache, c, layer, q, k_cur, v_cur, attn_out)
+        if rope:
+            layer_attention_rope(self._seg, cache, c, layer, q, k_cur, v_cur, attn_out)
+        else:
+            layer_attention(self._seg, cache, c, layer, q, k_cur, v_cur, attn_out)
 
     def finalize_token(self):
         if self._seg is not None:
