@@ -222,3 +222,29 @@ def test_c4_llama3_prefill_full_size(ctx, orc, B):
 def test_c5_gemma_prefill_full_size(ctx, orc):
     # BASELINE config 5 prefill: 8 q heads, 1 KV head (MQA), d256, bf16, 4096 tokens.
     prefill_case(ctx, orc, 8, 1, 256, "bf16", 4096, seed=500, rows=_sample_rows(4096))
+
+
+# The wide (8-wave, 256-query) kernel is chosen only when it still yields two
+# workgroups per CU, so the small shapes above run the 4-wave kernel; these
+# force the wide one (the launcher reads VTB_PREFILL_WIDE_MIN_WGS per launch).
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("n_heads,n_kv,d,B", [
+    (32, 8, 128, 300),   # C4 heads, two blocks of 256
+    (8, 8, 64, 257),     # MHA d64, one query past a block
+    (6, 2, 128, 513),    # GQA 3:1, three blocks
+])
+def test_prefill_wide_kernel_shapes(ctx, orc, monkeypatch, dtype, n_heads, n_kv, d, B):
+    monkeypatch.setenv("VTB_PREFILL_WIDE_MIN_WGS", "1")
+    prefill_case(ctx, orc, n_heads, n_kv, d, dtype, B, seed=B + d)
+
+
+@pytest.mark.parametrize("B", [1, 31, 32, 33, 255, 256, 257])
+def test_prefill_wide_kernel_lengths(ctx, orc, monkeypatch, B):
+    monkeypatch.setenv("VTB_PREFILL_WIDE_MIN_WGS", "1")
+    prefill_case(ctx, orc, 4, 2, 128, "bf16", B, seed=B)
+
+
+@pytest.mark.parametrize("pos0,B,window", [(37, 300, None), (0, 600, 64), (500, 260, 300)])
+def test_prefill_wide_kernel_offsets_and_windows(ctx, orc, monkeypatch, pos0, B, window):
+    monkeypatch.setenv("VTB_PREFILL_WIDE_MIN_WGS", "1")
+    prefill_case(ctx, orc, 8, 2, 128, "bf16", B, pos0=pos0, window=window, seed=pos0 + B)

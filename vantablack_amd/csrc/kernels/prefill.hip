@@ -143,16 +143,17 @@ __device__ __forceinline__ void vt_body(const VtArgs& a) {
 }
 
 // ---------------------------------------------------------------- attention
-template <typename DT, int D>
+template <typename DT, int D, int NW>
 __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
-  constexpr int BM = prefill_block_m(D);      // queries per workgroup (4 waves x 32)
+  constexpr int NT = 64 * NW;                 // threads per workgroup
+  constexpr int BM = 32 * NW;                 // queries per workgroup (NW waves x 32)
   constexpr int BN = prefill_block_n(D);      // keys per tile
   constexpr int KCH = D / 8;                  // 16-byte chunks per K row
   constexpr int VCH = BN / 8;                 // 16-byte chunks per V^T row
   constexpr int KPB = (KCH + 1) * 16;         // LDS pitch of a K row: one pad chunk
   constexpr int VPB = (VCH + 1) * 16;         // LDS pitch of a V^T row
-  constexpr int CPT = BN * KCH / 256;         // 16-byte chunks per thread per tile (K; V^T alike)
-  static_assert(BN * KCH % 256 == 0, "tile does not match 256 threads");
+  constexpr int CPT = BN * KCH / NT;          // 16-byte chunks per thread per tile (K; V^T alike)
+  static_assert(BN * KCH % NT == 0 && D * (BN / 8) == BN * KCH, "tile does not match the workgroup");
   constexpr int NS = BN / 32;                 // 32-key S^T tiles per key tile
   constexpr int ND = D / 32;                  // 32-dim O^T tiles
   constexpr int KS = D / 16;                  // k-steps of the QK product
@@ -166,7 +167,6 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   constexpr int KB = NS < VTB_PF_KB ? NS : VTB_PF_KB;  // S^T tiles per K-fragment batch
   constexpr int VB = ND < VTB_PF_VB ? ND : VTB_PF_VB;  // O^T tiles per V-fragment batch
   static_assert(NS % KB == 0 && ND % VB == 0, "batches must divide the tiles");
-  static_assert(BM == 128, "4 waves x 32 queries");
   typedef typename Mfma<DT>::frag frag;
 
   // Two K and two V^T stages: tile j is read from stage j%2 while tile j+1
@@ -220,33 +220,33 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   const _Float16* vtg = a.vt + (long long)kvh * D * a.vt_ld;
 
   // Tile staging through registers: thread chunk i of a tile is K row
-  // (tid + 256i) / KCH, chunk (tid + 256i) % KCH, and V^T row (tid + 256i) /
-  // VCH, chunk (tid + 256i) % VCH.  K rows at or past kend are clamped to
+  // (tid + NT i) / KCH, chunk (tid + NT i) % KCH, and V^T row (tid + NT i) /
+  // VCH, chunk (tid + NT i) % VCH.  K rows at or past kend are clamped to
   // kend - 1 (those keys are masked for every query here).
   u32x4 kpre[CPT], vpre[CPT];
   auto fetch = [&](long long kt0) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NT * i;
       long long row = kt0 + c / KCH;
       row = row < kend ? row : kend - 1;
       kpre[i] = load16_cached(kg + row * row_stride + 8 * (c % KCH));
     }
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NT * i;
       vpre[i] = load16_cached(vtg + (long long)(c / VCH) * a.vt_ld + kt0 + 8 * (c % VCH));
     }
   };
   auto stage = [&](char* kl, char* vl) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NT * i;
       *reinterpret_cast<u32x4*>(kl + (c / KCH) * KPB + 16 * (c % KCH)) = kpre[i];
     }
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NT * i;
       *reinterpret_cast<u32x4*>(vl + (c / VCH) * VPB + 16 * (c % VCH)) = vpre[i];
     }
   };
@@ -445,11 +445,26 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
 #define VTB_PREFILL(DTN, DTT, D)                                                           \
   extern "C" __global__ __launch_bounds__(256, vtb::prefill_waves_per_simd(D))                  \
   void vtb_prefill_##DTN##_d##D(vtb::PrefillArgs a) {                                         \
-    vtb::prefill_body<vtb::DTT, D>(a);                                                     \
+    vtb::prefill_body<vtb::DTT, D, 4>(a);                                                  \
   }                                                                                        \
   extern "C" __global__ __launch_bounds__(256) void vtb_vt_##DTN##_d##D(vtb::VtArgs a) {   \
     vtb::vt_body<vtb::DTT, D>(a);                                                          \
   }
+
+// Wide variant (d <= 128): 8 waves x 32 queries share one set of staged
+// K / V^T tiles.  At the same 70 KB of LDS per workgroup two workgroups fit
+// a CU, so 16 waves (4 per SIMD, <= 128 VGPRs) instead of 8, and each staged
+// byte feeds twice the queries.
+#define VTB_PREFILL_WIDE(DTN, DTT, D)                                                      \
+  extern "C" __global__ __launch_bounds__(512, 2)                                          \
+  void vtb_prefill8_##DTN##_d##D(vtb::PrefillArgs a) {                                        \
+    vtb::prefill_body<vtb::DTT, D, 8>(a);                                                  \
+  }
+
+VTB_PREFILL_WIDE(bf16, kv_bf16, 64)
+VTB_PREFILL_WIDE(bf16, kv_bf16, 128)
+VTB_PREFILL_WIDE(f16, kv_f16, 64)
+VTB_PREFILL_WIDE(f16, kv_f16, 128)
 
 VTB_PREFILL(bf16, kv_bf16, 64)
 VTB_PREFILL(bf16, kv_bf16, 128)

@@ -113,6 +113,7 @@ struct VtbHipCtx {
   hipModule_t mod_decode = nullptr, mod_prefill = nullptr, mod_kvcopy = nullptr;
   hipFunction_t f_decode[kNumKv][kNumD][kNumG] = {};
   hipFunction_t f_prefill[kNumKv][kNumD] = {};
+  hipFunction_t f_prefill8[kNumKv][kNumD] = {};  // wide (8-wave) variant, d <= 128
   hipFunction_t f_vt[kNumKv][kNumD] = {};
   hipFunction_t f_append[kNumKv] = {};
   hipFunction_t f_copy = nullptr;
@@ -349,7 +350,14 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const void* q, const void* k
     return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prefill kernel not built for this shape");
   if (!aligned16(k) || !aligned16(v) || !aligned16(q))
     return set_err(ctx, VTB_HIP_EINVAL, "q/K/V not 16-byte aligned");
-  const size_t bm = (size_t)vtb::prefill_block_m((int)head_dim);
+  // The wide kernel (8 waves, 256 queries per workgroup) when it still gives
+  // at least VTB_PREFILL_WIDE_MIN_WGS workgroups (default 2 per CU); short
+  // prompts keep the 4-wave kernel's parallelism.
+  const size_t bm_wide = (size_t)vtb::prefill_block_m_wide;
+  const long long wide_min = env_int("VTB_PREFILL_WIDE_MIN_WGS", 2LL * std::max(ctx->cu_count, 1));
+  const bool wide = ctx->f_prefill8[dtype][di] != nullptr &&
+                    (long long)(n_heads * ((n_q + bm_wide - 1) / bm_wide)) >= wide_min;
+  const size_t bm = wide ? bm_wide : (size_t)vtb::prefill_block_m((int)head_dim);
   const size_t nblk = (n_q + bm - 1) / bm;
   if (nblk > 65535 || n_heads > 0x7fffffff) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "grid too large");
   // V pre-pass: V^T as f16 for keys [0, pos0 + n_q), padded to whole tiles.
@@ -392,7 +400,8 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const void* q, const void* k
   a.scale_log2 = inv_sqrt_hd * 1.4426950408889634f;
   // x = head (fastest), y = query block: the longest (causal) blocks of every
   // head are dispatched first.
-  return launch(ctx, ctx->f_prefill[dtype][di], (unsigned)n_heads, (unsigned)nblk, 1, 256, &a);
+  return launch(ctx, wide ? ctx->f_prefill8[dtype][di] : ctx->f_prefill[dtype][di], (unsigned)n_heads,
+                (unsigned)nblk, 1, wide ? 512 : 256, &a);
 }
 
 int launch_append(VtbHipCtx* ctx, void* dst, const float* src, size_t n, int dtype) {
@@ -451,6 +460,9 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
         snprintf(name, sizeof name, "vtb_prefill_%s_d%d", kKvNames[kv], D);
         if (hipModuleGetFunction(&ctx->f_prefill[kv][di], ctx->mod_prefill, name) != hipSuccess)
           ctx->f_prefill[kv][di] = nullptr;  // shape not built: reported at launch
+        snprintf(name, sizeof name, "vtb_prefill8_%s_d%d", kKvNames[kv], D);
+        if (D > 128 || hipModuleGetFunction(&ctx->f_prefill8[kv][di], ctx->mod_prefill, name) != hipSuccess)
+          ctx->f_prefill8[kv][di] = nullptr;  // not built for d256: the 4-wave kernel runs
         snprintf(name, sizeof name, "vtb_vt_%s_d%d", kKvNames[kv], D);
         if (hipModuleGetFunction(&ctx->f_vt[kv][di], ctx->mod_prefill, name) != hipSuccess)
           ctx->f_vt[kv][di] = nullptr;
