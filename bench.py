@@ -257,6 +257,70 @@ def bench_prefill(ctx, torch, n_heads, n_kv, d, L, reps=5, warmup=2):
     return {"avg_launch_s": t, "flops": fl, "tflops": fl / t / 1e12}
 
 
+QUANT_BLOCK = {"q8_0": (34, 32), "q4_k": (144, 256), "q5_k": (176, 256), "q6_k": (210, 256)}
+# Llama-2-7B projections per layer: q, k, v, o (4096 x 4096), gate, up
+# (11008 x 4096), down (4096 x 11008) -- segMatmulQuant's shapes
+# (forward.zig:400-417) on either side of the attention.
+LLAMA2_7B_PROJ = [("qkvo", 4096, 4096, 4), ("gate_up", 11008, 4096, 2), ("down", 4096, 11008, 1)]
+
+
+def bench_gemv(ctx, torch, kind, m, k, reps=20, pool_bytes=512 << 20):
+    """One quantised GEMV (m x k, `kind` blocks) per launch, cycling over
+    enough distinct weight copies (>= pool_bytes) that every launch streams
+    its weights from HBM rather than the 256 MB MALL.  Random weight bytes
+    (the arithmetic does not depend on them).  Returns us/launch and the
+    algorithmic GB/s (weights + activations + outputs)."""
+    import vantablack_amd as vb
+    bb, be = QUANT_BLOCK[kind]
+    row_bytes = k // be * bb
+    wbytes = m * row_bytes
+    copies = max(2, -(-pool_bytes // wbytes))
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    w = torch.randint(0, 256, (copies, wbytes), generator=g, dtype=torch.uint8, device=dev)
+    x = torch.randn(k, generator=g, device=dev)
+    out = torch.empty(m, device=dev)
+    torch.cuda.synchronize()
+    wb, xb, ob = ctx.wrap_tensor(w), ctx.wrap_tensor(x), ctx.wrap_tensor(out)
+    stream = torch.cuda.ExternalStream(ctx.stream)
+    with ctx.segment() as seg:
+        for i in range(copies):
+            seg.matmul_quant(kind, ob, wb, i * wbytes, xb, m, k)
+    ctx.wait_idle()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    with ctx.segment() as seg:
+        for i in range(reps):
+            seg.matmul_quant(kind, ob, wb, (i % copies) * wbytes, xb, m, k)
+    e1.record(stream)
+    ctx.wait_idle()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / reps
+    for b in (wb, xb, ob):
+        b.release()
+    del w
+    torch.cuda.empty_cache()
+    nbytes = wbytes + 4 * k + 4 * m
+    log(f"gemv {kind} {m}x{k}: {t * 1e6:.2f} us/launch -> {nbytes / t / 1e9:.1f} GB/s")
+    return {"us_per_launch": round(t * 1e6, 3), "gbs": round(nbytes / t / 1e9, 1),
+            "pct_of_hbm_peak": round(100.0 * nbytes / t / 1e9 / HBM_PEAK_GBS, 2), "bytes_per_launch": nbytes}
+
+
+def bench_gemv_layer(ctx, torch, kind):
+    """The seven Llama-2-7B projections of one layer in `kind`: per-shape
+    figures and the layer total (time-weighted GB/s)."""
+    res, tot_t, tot_b = {}, 0.0, 0
+    for name, m, k, count in LLAMA2_7B_PROJ:
+        r = bench_gemv(ctx, torch, kind, m, k)
+        res[name] = r
+        tot_t += count * r["us_per_launch"]
+        tot_b += count * r["bytes_per_launch"]
+    res["layer"] = {"us": round(tot_t, 2), "gbs": round(tot_b / (tot_t * 1e-6) / 1e9, 1),
+                    "pct_of_hbm_peak": round(100.0 * tot_b / (tot_t * 1e-6) / 1e9 / HBM_PEAK_GBS, 2)}
+    return res
+
+
 def cpu_baseline(seconds_budget=12.0):
     """Time the CPU oracle on a bounded sample of the decode workload: one
     C2 layer at L=8192 (f32 values of the f16 cache, as vantablack's f32
@@ -396,6 +460,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-more", action="store_true", help="skip the C1/C3/C5 decode lines")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the quantised GEMV lines")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; the path's multi-GPU sharding is "
@@ -461,6 +526,14 @@ def main():
     }
     if dec_more:
         line["decode_other_configs"] = dec_more
+    if not args.no_gemv:
+        # The next row beside attention: segMatmulQuant's GEMVs at Llama-2-7B
+        # shapes, HBM-bound (weights streamed once per launch).
+        line["quant_gemv"] = {
+            "workload": "Llama-2-7B layer projections q,k,v,o 4096x4096, gate,up 11008x4096, down 4096x11008; "
+                        "f32 activations; weights cycled over >= 512 MB so each launch reads HBM",
+            **{kind: bench_gemv_layer(ctx, torch, kind) for kind in ("q4_k", "q5_k", "q6_k", "q8_0")},
+        }
     if pre:
         p8 = pre["C4_L8192"]
         line["prefill"] = {

@@ -173,6 +173,35 @@ void vtb_hip_segment_attn_prefill(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf 
                                   size_t sliding_window, size_t n_heads, size_t n_kv_heads,
                                   size_t head_dim, float inv_sqrt_hd, int dtype);
 
+/* ---- Quantised matrix-vector products: out[i] = sum_j W[i, j] * acts[j] for
+ * m rows of k weights stored as GGUF blocks (layouts of src/kernels/simd.zig:
+ * Q8_0 34 B / 32 weights, Q4_K 144 B / 256, Q5_K 176 B / 256, Q6_K 210 B / 256),
+ * row 0 at w_offset in w_buf; acts f32 [k] (16-byte aligned), out f32 [m].
+ * Each weight is dequantised exactly as the CPU reference does; the dot runs
+ * in f32 (results agree with the CPU path to ~1e-6 relative; the Metal path's
+ * own bar is 1e-4, bridge.zig:466-470).  k a multiple of the block size; the
+ * weights 4-byte aligned and below 2 GiB.
+ * Segment encoders replace vtb_metal_segment_matmul_{q8_0,q4_k,q5_k,q6_k}
+ * (bridge.h:93-113, dispatched by segMatmulQuant, forward.zig:400-417); the
+ * vtb_hip_matmul_* forms run synchronously, as vtb_metal_matmul_* do
+ * (bridge.h:41-70): 0 on success. */
+void vtb_hip_segment_matmul_q8_0(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                                 VtbHipBuf *acts_buf, size_t m, size_t k);
+void vtb_hip_segment_matmul_q4_k(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                                 VtbHipBuf *acts_buf, size_t m, size_t k);
+void vtb_hip_segment_matmul_q5_k(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                                 VtbHipBuf *acts_buf, size_t m, size_t k);
+void vtb_hip_segment_matmul_q6_k(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                                 VtbHipBuf *acts_buf, size_t m, size_t k);
+int vtb_hip_matmul_q8_0(VtbHipCtx *ctx, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                        VtbHipBuf *acts_buf, size_t m, size_t k);
+int vtb_hip_matmul_q4_k(VtbHipCtx *ctx, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                        VtbHipBuf *acts_buf, size_t m, size_t k);
+int vtb_hip_matmul_q5_k(VtbHipCtx *ctx, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                        VtbHipBuf *acts_buf, size_t m, size_t k);
+int vtb_hip_matmul_q6_k(VtbHipCtx *ctx, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                        VtbHipBuf *acts_buf, size_t m, size_t k);
+
 /* ---- KvCache, device-handle mode (kv_cache.zig:20-196).  Layer-major
  * [n_layers][max_seq][n_kv_heads][head_dim] of dtype in HBM; no host slices. */
 VtbHipKvCache *vtb_hip_kv_cache_init(VtbHipCtx *ctx, size_t n_layers, size_t n_kv_heads,

@@ -12,6 +12,8 @@ Contents:
     136-150), the KvCache layout (src/runtime/kv_cache.zig) and the pool
     (src/runtime/pool.zig));
   * ``math.rope`` / ``math.ropeHalf`` (src/kernels/math.zig:85-133);
+  * the quantised matmuls of src/kernels/simd.zig (Q8_0, Q4_K, Q5_K, Q6_K) in
+    ``quant_oracle.c``;
   * the portable seeded input generator (SplitMix64 -> f64 Box-Muller -> f32
     -> KV dtype) used for every parity input;
   * exact dtype helpers (f32 -> f16/bf16 round-to-nearest-even, and the exact
@@ -62,6 +64,12 @@ def lib():
         P, S, F = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float
         L.vtb_oracle_softmax.argtypes = [P, S]
         L.vtb_oracle_rope.argtypes = [P, S, S, F]
+        L.vtb_oracle_quant_block_bytes.argtypes = [ctypes.c_int]
+        L.vtb_oracle_quant_block_bytes.restype = S
+        L.vtb_oracle_quant_block_elems.argtypes = [ctypes.c_int]
+        L.vtb_oracle_quant_block_elems.restype = S
+        L.vtb_oracle_dequant_block.argtypes = [ctypes.c_int, P, P]
+        L.vtb_oracle_matmul_quant.argtypes = [ctypes.c_int, P, P, P, S, S]
         L.vtb_oracle_rope_half.argtypes = [P, S, S, F]
         L.vtb_oracle_rope_inv_freq.argtypes = [P, S, F]
         L.vtb_oracle_argmax.argtypes = [P, S]
@@ -204,6 +212,38 @@ def rope(x: np.ndarray, pos: int, base: float, half: bool = False) -> np.ndarray
 def rope_inv_freq(head_dim: int, base: float) -> np.ndarray:
     out = np.empty(head_dim // 2, dtype=np.float32)
     lib().vtb_oracle_rope_inv_freq(_ptr(out), head_dim, base)
+    return out
+
+
+QUANT_KINDS = {"q8_0": 0, "q4_k": 1, "q5_k": 2, "q6_k": 3}
+
+
+def quant_block(kind: str):
+    """(block_bytes, block_elems) of a GGUF block format (simd.zig)."""
+    i = QUANT_KINDS[kind]
+    return int(lib().vtb_oracle_quant_block_bytes(i)), int(lib().vtb_oracle_quant_block_elems(i))
+
+
+def dequant(kind: str, blocks: np.ndarray) -> np.ndarray:
+    """Dequantise whole blocks (uint8 bytes) to f32 (simd.zig dequantBlock*)."""
+    bb, be = quant_block(kind)
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+    assert b.size % bb == 0
+    n = b.size // bb
+    out = np.empty(n * be, np.float32)
+    for i in range(n):
+        lib().vtb_oracle_dequant_block(QUANT_KINDS[kind], b.ctypes.data + i * bb, out.ctypes.data + i * be * 4)
+    return out
+
+
+def matmul_quant(kind: str, w: np.ndarray, x: np.ndarray, m: int, k: int) -> np.ndarray:
+    """out = W @ x for m rows of quantised weights (simd.zig matmul_*)."""
+    wb = np.ascontiguousarray(w, dtype=np.uint8)
+    xa = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(m, np.float32)
+    rc = lib().vtb_oracle_matmul_quant(QUANT_KINDS[kind], _ptr(out), _ptr(wb), _ptr(xa), m, k)
+    if rc != 0:
+        raise ValueError("matmul_quant: k is not a whole number of blocks")
     return out
 
 

@@ -1,0 +1,92 @@
+"""Quantised GEMV on the GPU, through the C ABI, against the oracle's restatement
+of src/kernels/simd.zig matmul_* (Q8_0, Q4_K, Q5_K, Q6_K).
+
+Bars: the reference's own Metal check (bridge.zig:466-470: 1e-4 relative per
+output on a random-byte fixture) and, stronger, |got - ref| <= 1e-5 *
+sum_j |W_ij x_j| per row, which holds however much a row's sum cancels.
+"""
+import numpy as np
+import pytest
+
+from tests.quant import BLOCK, np_dequant, random_weights
+
+pytestmark = pytest.mark.gpu
+KINDS = ["q8_0", "q4_k", "q5_k", "q6_k"]
+
+
+def gemv_case(ctx, orc, kind, m, k, seed, w_offset=0, x=None):
+    import vantablack_amd as vb
+    w = random_weights(kind, m, k, seed)
+    if x is None:
+        rng = np.random.default_rng(seed + 1)
+        x = ((rng.random(k, dtype=np.float32) - 0.5) * 2.0).astype(np.float32)
+    wbuf = ctx.to_device(np.concatenate([np.zeros(w_offset, np.uint8), w]))
+    xb, ob = ctx.to_device(x), ctx.alloc(m * 4)
+    with ctx.segment() as seg:
+        seg.matmul_quant(kind, ob, wbuf, w_offset, xb, m, k)
+    got = ctx.download(ob, np.float32, m).astype(np.float64)
+    ref = orc.matmul_quant(kind, w, x, m, k).astype(np.float64)
+    cond = np.abs(np_dequant(kind, w).astype(np.float64).reshape(m, k)) @ np.abs(x.astype(np.float64))
+    err = np.abs(got - ref)
+    assert np.all(err <= 1e-5 * cond), f"{kind} m{m} k{k}: max err/cond {np.max(err / cond):.2e}"
+    big = np.abs(ref) > 1e-3 * cond
+    assert np.all(err[big] <= 1e-4 * np.abs(ref[big])), f"{kind} m{m} k{k}: relative error above 1e-4"
+    return got
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_reference_parity_fixture(ctx, orc, kind):
+    # bridge.zig:383-472: m = 4 rows, k = two blocks, random bytes with small
+    # finite f16 super-scales, activations uniform in [-1, 1).
+    gemv_case(ctx, orc, kind, 4, 2 * BLOCK[kind][1], seed=0xDEADBEEF % 1000 + len(kind))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("m,k", [(4096, 4096), (11008, 4096), (4096, 11008)])
+def test_llama2_7b_projection_shapes(ctx, orc, kind, m, k):
+    gemv_case(ctx, orc, kind, m, k, seed=m + k + len(kind))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("m,k", [(1, 256), (13, 2304), (1023, 512), (37, 4352)])
+def test_ragged_shapes(ctx, orc, kind, m, k):
+    # m not a multiple of the rows per workgroup; k ending inside a 2048-wide
+    # step (2304 = 9 blocks, 4352 = 17 blocks).
+    gemv_case(ctx, orc, kind, m, k, seed=m * 3 + k)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_weight_offset(ctx, orc, kind):
+    gemv_case(ctx, orc, kind, 64, 1024, seed=9, w_offset=4100)
+
+
+@pytest.mark.parametrize("rows", ["1", "2", "4"])
+@pytest.mark.parametrize("kind", KINDS)
+def test_every_rows_per_wave_variant(ctx, orc, monkeypatch, kind, rows):
+    monkeypatch.setenv("VTB_GEMV_R", rows)
+    gemv_case(ctx, orc, kind, 523, 2048, seed=int(rows) + 100)
+
+
+def test_rejects_bad_shapes_and_alignment(ctx):
+    import vantablack_amd as vb
+    w = ctx.alloc(1 << 16)
+    x = ctx.alloc(4096 * 4)
+    o = ctx.alloc(4096 * 4)
+    for kind, m, k, off in [("q4_k", 4, 300, 0),      # k not a whole number of blocks
+                            ("q8_0", 4, 64, 2),       # weights not 4-byte aligned
+                            ("q6_k", 400, 512, 0)]:   # weights beyond the buffer
+        with pytest.raises(vb.HipError):
+            with ctx.segment() as seg:
+                seg.matmul_quant(kind, o, w, off, x, m, k)
+
+
+def test_synchronous_entry(ctx, orc):
+    import vantablack_amd as vb
+    kind, m, k = "q4_k", 32, 512
+    w = random_weights(kind, m, k, seed=3)
+    x = orc.normal(4, k)
+    wb, xb, ob = ctx.to_device(w), ctx.to_device(x), ctx.alloc(m * 4)
+    assert vb.hip.lib().vtb_hip_matmul_q4_k(ctx.h, ob.h, wb.h, 0, xb.h, m, k) == 0
+    got = ctx.download(ob, np.float32, m)
+    ref = orc.matmul_quant(kind, w, x, m, k)
+    assert np.max(np.abs(got - ref)) <= 1e-4 * np.max(np.abs(ref))

@@ -25,6 +25,7 @@ extern "C" {
 extern const unsigned char vtb_blob_decode[];
 extern const unsigned char vtb_blob_prefill[];
 extern const unsigned char vtb_blob_kvcopy[];
+extern const unsigned char vtb_blob_gemv[];
 }
 
 namespace {
@@ -106,17 +107,37 @@ struct CopyArgs {
 
 }  // namespace
 
+// Quantised GEMV formats (GGUF blocks, src/kernels/simd.zig) and rows per wave.
+constexpr int kNumQuant = 4;
+const char* const kQuantNames[kNumQuant] = {"q8_0", "q4_k", "q5_k", "q6_k"};
+constexpr size_t kQuantBlockBytes[kNumQuant] = {34, 144, 176, 210};
+constexpr size_t kQuantBlockElems[kNumQuant] = {32, 256, 256, 256};
+constexpr int kNumGemvR = 3;
+constexpr int kGemvRs[kNumGemvR] = {1, 2, 4};
+
+// Arguments of vtb_gemv_* (layout must match gemv.hip).
+struct GemvArgs {
+  const void* w;
+  const float* x;
+  float* out;
+  unsigned w_bytes;
+  int m;
+  int k;
+  int row_bytes;
+};
+
 struct VtbHipCtx {
   int device = 0;
   int cu_count = 0;
   hipStream_t stream = nullptr;
-  hipModule_t mod_decode = nullptr, mod_prefill = nullptr, mod_kvcopy = nullptr;
+  hipModule_t mod_decode = nullptr, mod_prefill = nullptr, mod_kvcopy = nullptr, mod_gemv = nullptr;
   hipFunction_t f_decode[kNumKv][kNumD][kNumG] = {};
   hipFunction_t f_prefill[kNumKv][kNumD] = {};
   hipFunction_t f_prefill8[kNumKv][kNumD] = {};  // wide (8-wave) variant, d <= 128
   hipFunction_t f_vt[kNumKv][kNumD] = {};
   hipFunction_t f_append[kNumKv] = {};
   hipFunction_t f_copy = nullptr;
+  hipFunction_t f_gemv[kNumQuant][kNumGemvR] = {};  // vtb_gemv_<kind>_r<1|2|4>
   // Split-K workspace and arrival counters (counters are zero between launches).
   void* ws = nullptr;
   size_t ws_bytes = 0;
@@ -189,9 +210,9 @@ int kv_bytes(int dtype) { return (dtype >= 0 && dtype < kNumKv) ? kKvBytes[dtype
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int launch(VtbHipCtx* ctx, hipFunction_t f, unsigned gx, unsigned gy, unsigned gz, unsigned bx,
-           void* args) {
+           void* args, unsigned lds_bytes = 0) {
   void* params[] = {args};
-  HIP_TRY(ctx, hipModuleLaunchKernel(f, gx, gy, gz, bx, 1, 1, 0, ctx->stream, params, nullptr),
+  HIP_TRY(ctx, hipModuleLaunchKernel(f, gx, gy, gz, bx, 1, 1, lds_bytes, ctx->stream, params, nullptr),
           "hipModuleLaunchKernel");
   return VTB_HIP_OK;
 }
@@ -404,6 +425,52 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const void* q, const void* k
                 (unsigned)nblk, 1, wide ? 512 : 256, &a);
 }
 
+// Quantised GEMV launcher: out[m] = W[m, k] . x.  One workgroup per R rows
+// with one wave per 2048 columns (k <= 32768; R = 4 only up to 16384); R is
+// the largest of 4 / 2 / 1 that still gives two workgroups per CU
+// (VTB_GEMV_R overrides).
+int launch_gemv(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* x, size_t m, size_t k) {
+  if (qk < 0 || qk >= kNumQuant) return set_err(ctx, VTB_HIP_EINVAL, "bad quant kind");
+  if (m == 0 || k == 0 || k % kQuantBlockElems[qk] != 0)
+    return set_err(ctx, VTB_HIP_EINVAL, "matmul: k must be a positive multiple of the block size");
+  if (k > 16 * 2048) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul: k above 32768");
+  const size_t row_bytes = k / kQuantBlockElems[qk] * kQuantBlockBytes[qk];
+  // Offsets stay below 2^31 with room for one block past the end, where
+  // the kernel points the loads of rows past m.
+  if (m > 0x7fff0000 / row_bytes) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul: weights beyond 2 GiB");
+  if ((uintptr_t)w % 4 != 0) return set_err(ctx, VTB_HIP_EINVAL, "matmul: weights not 4-byte aligned");
+  if (!aligned16(x)) return set_err(ctx, VTB_HIP_EINVAL, "matmul: activations not 16-byte aligned");
+  int ri = 0;
+  const long long forced = env_int("VTB_GEMV_R", 0);
+  for (int i = kNumGemvR - 1; i >= 0; --i) {
+    const long long wgs = ((long long)m + kGemvRs[i] - 1) / kGemvRs[i];
+    if (kGemvRs[i] == 4 && k > 8 * 2048) continue;  // the R = 4 kernels take at most 8 waves
+    if (forced ? forced == kGemvRs[i] : wgs >= 2LL * std::max(ctx->cu_count, 1)) {
+      ri = i;
+      break;
+    }
+  }
+  GemvArgs a;
+  memset(&a, 0, sizeof a);
+  a.w = w;
+  a.x = x;
+  a.out = out;
+  // The range is rounded up to whole dwords: a raw buffer load returns zero
+  // for a dword only partly in range, and the last field of a 34- or
+  // 210-byte block can end two bytes into one.  With the base 4-byte
+  // aligned that dword lies in the page holding the tensor's last bytes.
+  a.w_bytes = (unsigned)((m * row_bytes + 3) & ~(size_t)3);
+  a.m = (int)m;
+  a.k = (int)k;
+  a.row_bytes = (int)row_bytes;
+  const unsigned waves = (unsigned)((k + 2047) / 2048);
+  const size_t R = (size_t)kGemvRs[ri];
+  // Per wave the kernel stages its 2048 activations as 8 rows of (64 + 4)
+  // float4 in dynamic LDS.
+  const unsigned lds = waves * 8u * (64u + 4u) * 16u;
+  return launch(ctx, ctx->f_gemv[qk][ri], (unsigned)((m + R - 1) / R), 1, 1, 64 * waves, &a, lds);
+}
+
 int launch_append(VtbHipCtx* ctx, void* dst, const float* src, size_t n, int dtype) {
   if (n == 0) return VTB_HIP_OK;
   if (dtype < 0 || dtype >= kNumKv) return set_err(ctx, VTB_HIP_EINVAL, "bad kv dtype");
@@ -448,6 +515,7 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
   ok = ok && hipModuleLoadData(&ctx->mod_decode, vtb_blob_decode) == hipSuccess;
   ok = ok && hipModuleLoadData(&ctx->mod_prefill, vtb_blob_prefill) == hipSuccess;
   ok = ok && hipModuleLoadData(&ctx->mod_kvcopy, vtb_blob_kvcopy) == hipSuccess;
+  ok = ok && hipModuleLoadData(&ctx->mod_gemv, vtb_blob_gemv) == hipSuccess;
   char name[96];
   for (int kv = 0; ok && kv < kNumKv; ++kv) {
     for (int di = 0; ok && di < kNumD; ++di) {
@@ -474,6 +542,11 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
     }
   }
   ok = ok && hipModuleGetFunction(&ctx->f_copy, ctx->mod_kvcopy, "vtb_copy_f32") == hipSuccess;
+  for (int qk = 0; ok && qk < kNumQuant; ++qk)
+    for (int ri = 0; ok && ri < kNumGemvR; ++ri) {
+      snprintf(name, sizeof name, "vtb_gemv_%s_r%d", kQuantNames[qk], kGemvRs[ri]);
+      ok = hipModuleGetFunction(&ctx->f_gemv[qk][ri], ctx->mod_gemv, name) == hipSuccess;
+    }
   (void)hipGetLastError();  // absent optional kernels are not an error for the caller
   if (!ok) {
     vtb_hip_destroy(ctx);
@@ -493,6 +566,7 @@ extern "C" void vtb_hip_destroy(VtbHipCtx* ctx) {
   if (ctx->mod_decode) (void)hipModuleUnload(ctx->mod_decode);
   if (ctx->mod_prefill) (void)hipModuleUnload(ctx->mod_prefill);
   if (ctx->mod_kvcopy) (void)hipModuleUnload(ctx->mod_kvcopy);
+  if (ctx->mod_gemv) (void)hipModuleUnload(ctx->mod_gemv);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -734,6 +808,38 @@ extern "C" void vtb_hip_segment_attn_prefill(VtbHipSeg* seg, VtbHipBuf* out_buf,
                              head_dim, (long long)pos0, w, inv_sqrt_hd, dtype);
   seg_note(seg, rc);
 }
+
+// ============================================================== quantised GEMV
+
+static int matmul_entry(VtbHipCtx* ctx, int qk, VtbHipBuf* out_buf, VtbHipBuf* w_buf, size_t w_offset,
+                        VtbHipBuf* acts_buf, size_t m, size_t k) {
+  if (!ctx || !out_buf || !w_buf || !acts_buf) return VTB_HIP_EINVAL;
+  if (m == 0 || k == 0 || k % kQuantBlockElems[qk] != 0 || m > ((size_t)1 << 31) || k > ((size_t)1 << 31))
+    return set_err(ctx, VTB_HIP_EINVAL, "matmul: bad shape");
+  const size_t row_bytes = k / kQuantBlockElems[qk] * kQuantBlockBytes[qk];
+  if (!buf_ok(w_buf, w_offset, m * row_bytes) || !buf_ok(acts_buf, 0, k * 4) || !buf_ok(out_buf, 0, m * 4))
+    return set_err(ctx, VTB_HIP_EINVAL, "matmul: buffer too small");
+  return launch_gemv(ctx, qk, (float*)out_buf->ptr, bptr(w_buf, w_offset), (const float*)acts_buf->ptr, m, k);
+}
+
+#define VTB_MATMUL_ENTRIES(NAME, QK)                                                                     \
+  extern "C" void vtb_hip_segment_matmul_##NAME(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* w_buf,   \
+                                                size_t w_offset, VtbHipBuf* acts_buf, size_t m, size_t k) { \
+    if (!seg) return;                                                                                   \
+    seg_note(seg, matmul_entry(seg->ctx, QK, out_buf, w_buf, w_offset, acts_buf, m, k));                \
+  }                                                                                                     \
+  extern "C" int vtb_hip_matmul_##NAME(VtbHipCtx* ctx, VtbHipBuf* out_buf, VtbHipBuf* w_buf,           \
+                                       size_t w_offset, VtbHipBuf* acts_buf, size_t m, size_t k) {        \
+    int rc = matmul_entry(ctx, QK, out_buf, w_buf, w_offset, acts_buf, m, k);                            \
+    if (rc) return rc;                                                                                  \
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");                            \
+    return VTB_HIP_OK;                                                                                  \
+  }
+
+VTB_MATMUL_ENTRIES(q8_0, 0)
+VTB_MATMUL_ENTRIES(q4_k, 1)
+VTB_MATMUL_ENTRIES(q5_k, 2)
+VTB_MATMUL_ENTRIES(q6_k, 3)
 
 // ============================================================== KvCache
 

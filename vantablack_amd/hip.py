@@ -103,6 +103,14 @@ SIGNATURES = {
     "vtb_hip_kv_cache_shrink_to_fit": ([_P, _S], _I),
     "vtb_hip_layer_attention": ([_P, _P, ctypes.POINTER(AttnConfigC), _S, _P, _P, _P, _P], _I),
     "vtb_hip_layer_attention_rope": ([_P, _P, ctypes.POINTER(AttnConfigC), _S, _P, _P, _P, _P, _F, _I], _I),
+    "vtb_hip_segment_matmul_q8_0": ([_P, _P, _P, _S, _P, _S, _S], None),
+    "vtb_hip_matmul_q8_0": ([_P, _P, _P, _S, _P, _S, _S], _I),
+    "vtb_hip_segment_matmul_q4_k": ([_P, _P, _P, _S, _P, _S, _S], None),
+    "vtb_hip_matmul_q4_k": ([_P, _P, _P, _S, _P, _S, _S], _I),
+    "vtb_hip_segment_matmul_q5_k": ([_P, _P, _P, _S, _P, _S, _S], None),
+    "vtb_hip_matmul_q5_k": ([_P, _P, _P, _S, _P, _S, _S], _I),
+    "vtb_hip_segment_matmul_q6_k": ([_P, _P, _P, _S, _P, _S, _S], None),
+    "vtb_hip_matmul_q6_k": ([_P, _P, _P, _S, _P, _S, _S], _I),
     "vtb_hip_prefill_attention": ([_P, _P, ctypes.POINTER(AttnConfigC), _S, _S, _P, _P, _P, _P], _I),
 }
 
@@ -129,6 +137,9 @@ def _check(ctx_h, rc: int, what: str):
     if rc != OK:
         msg = lib().vtb_hip_last_error(ctx_h) if ctx_h else b""
         raise _ERR_CLASS.get(rc, HipError)(rc, f"{what}: {(msg or b'').decode()}")
+
+
+QUANT_KINDS = ("q8_0", "q4_k", "q5_k", "q6_k")
 
 
 @dataclasses.dataclass
@@ -217,6 +228,13 @@ class Segment:
                                                       v_cur.h, n_heads, n_kv_heads, head_dim, seq_len,
                                                       inv_sqrt_hd, kv_dtype, rope_pos, rope_base,
                                                       1 if rope_half else 0)
+
+    def matmul_quant(self, kind: str, out: Buffer, w: Buffer, w_offset: int, acts: Buffer, m: int, k: int):
+        """out = W @ acts for m rows of `kind` blocks (q8_0, q4_k, q5_k, q6_k):
+        segMatmulQuant (forward.zig:400-417) on the segment."""
+        if kind not in QUANT_KINDS:
+            raise ValueError(f"unknown quant kind {kind!r}")
+        getattr(lib(), f"vtb_hip_segment_matmul_{kind}")(self.h, out.h, w.h, w_offset, acts.h, m, k)
 
     def attn_prefill(self, out: Buffer, q: Buffer, k: Buffer, v: Buffer, layer_off: int, n_tokens: int,
                      pos0: int, sliding_window: int, n_heads: int, n_kv_heads: int, head_dim: int,
