@@ -21,20 +21,31 @@
 // lane L's runs is stored at [idx][L] (rows padded so that the reads of 16
 // consecutive lanes never share a bank), then each lane reads its 8 float4
 // back.  Each lane issues all its loads before it waits for any: the
-// activations, then the raw words of every row.
+// activations, then the raw words of every row.  (Measured against this: a
+// persistent-wave variant that stages x once per workgroup and loops over
+// row groups was slower on the Llama-2-7B projection shapes in all formats
+// but Q6_K with k = 11008, its per-workgroup staging sitting in front of
+// every first weight load.)
 //
-// Per row the part's dot is formed in factored form,
+// Arithmetic.  Per row the part's dot is formed in factored form,
 //   sum_l (s q_l - mn) x_l = s sum_l q_l x_l - mn sum_l x_l,
-// with s and mn the reference's f32 products (d*sc, dmin*mn) and the sums
-// over one 16-column run; the wave sums its lanes (DPP / permlane) and the
-// waves' partials are added in wave order through LDS, so results do not
-// depend on timing.  The factoring changes only the rounding order (the GPU
-// bar is 1e-4 relative, the reference's own Metal bar, bridge.zig:466-470).
+// with s and mn the reference's f32 products (d*sc, dmin*mn) and the x sums
+// over one 16-column run.  The quant sums sum_l q_l x_l use v_fma_mix_f32: a
+// small unsigned quant q placed in the low bits of a 16-bit half (below
+// 0x400) is exactly the f16 subnormal q * 2^-24 (q * 2^-20 four bits up),
+// so masking a quant word yields two weights at once and the mixed fma takes
+// them without a conversion; the power of two is removed exactly at the end.
+// The wave sums its lanes (DPP / permlane) and the waves' partials are added
+// in wave order through LDS, so results do not depend on timing.  The
+// factoring changes only the rounding order (the GPU bar is 1e-4 relative,
+// the reference's own Metal bar, bridge.zig:466-470).
 //
 // Weights are read through a raw buffer resource over the m rows, its range
 // rounded up to whole dwords: the aligned-dword reads that cover a 2-byte
 // aligned field (Q8_0 blocks are 34 bytes, Q6_K 210) never fault, and a field
-// ending two bytes into the last dword still reads its own bytes.
+// ending two bytes into the last dword still reads its own bytes.  Rows past
+// m and columns past k read from the end of the range, where buffer loads
+// return zero without touching memory, so every load is branch-free.
 #include "common.h"
 
 namespace vtb {
@@ -58,10 +69,12 @@ __device__ inline uint32_t wload(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
 
-// N consecutive dwords from a 4-byte aligned offset; consecutive 32-bit
-// buffer loads are merged by the backend into dwordx4 / x2 loads.  Loads and
-// use are split so that every load of a lane is in flight before any result
-// is waited for.
+// N consecutive weight dwords from a 4-byte aligned offset; consecutive
+// 32-bit buffer loads are merged by the backend into dwordx4 / x2 loads.
+// Loads and use are split so that every load of a lane is in flight before
+// any result is waited for.  Cached loads: with the nontemporal policy the
+// 34- and 210-byte blocks, whose neighbouring lanes share cache lines, ran
+// 20-40% slower on MI355X (Q4_K unchanged).
 template <int N> struct Words {
   uint32_t t[N];
   __device__ void load(__amdgpu_buffer_rsrc_t r, int off) {
@@ -70,31 +83,35 @@ template <int N> struct Words {
   }
 };
 
-// Byte selectors for v_perm_b32 over {hi, lo}: the dword starting at byte 0,
-// 2 or 4 of lo.
-constexpr uint32_t kPerm0 = 0x03020100u, kPerm2 = 0x05040302u, kPerm4 = 0x07060504u;
+// v_perm_b32 over {hi, lo}: selector byte n < 4 picks byte n of lo, 4..7
+// byte n - 4 of hi, 0x0c a zero byte.
 __device__ inline uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
+constexpr uint32_t kPerm0 = 0x03020100u, kPerm2 = 0x05040302u;
+// Bytes (0, 2) and (1, 3) of a dword as two 16-bit halves.
+constexpr uint32_t kSplit02 = 0x0c020c00u, kSplit13 = 0x0c030c01u;
 
-__device__ inline float f16bits(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu)); }
+// Halves of v as f16, converted to f32 (exact).
+__device__ inline float h_lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu)); }
+__device__ inline float h_hi(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
 
-// Byte j of v (each byte holding a small unsigned field) as f32: one
-// v_cvt_f32_ubyte<j> per value.
+// acc + lo(p) * xa + hi(p) * xb, as two v_fma_mix_f32: with quant patterns
+// below 0x400 in the halves this adds 2^-24 * (qa * xa + qb * xb).
+__device__ inline float mix2(uint32_t p, float xa, float xb, float acc) {
+  return fmaf(h_hi(p), xb, fmaf(h_lo(p), xa, acc));
+}
+constexpr float kTwo24 = 16777216.0f, kTwo20 = 1048576.0f;
+
+// Byte j of v as f32 (one v_cvt_f32_ubyte<j>).
 __device__ inline float ubyte_f(uint32_t v, int j) { return (float)((v >> (8 * j)) & 0xffu); }
 
-// Keeps the optimiser from folding a per-byte mask into one bitfield extract
-// per weight (bfe + cvt instead of a single cvt_ubyte<j>).
-__device__ inline uint32_t opaque(uint32_t v) {
-  asm("" : "+v"(v));
-  return v;
-}
-
-// Sum over a 16-weight run: 4 dwords of byte fields against 16 activations.
-__device__ inline float run_dot(const uint32_t (&u)[4], const float* x) {
+// 2^-24 * sum over a 16-weight run whose quants are the bytes (all below
+// 0x400 as 16-bit values) of u[0..4), against x[0..16).
+__device__ inline float byte_run(const uint32_t (&u)[4], const float* x) {
   float acc = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc = fmaf(ubyte_f(u[i], j), x[4 * i + j], acc);
+    acc = mix2(perm(0u, u[i], kSplit02), x[4 * i], x[4 * i + 2], acc);
+    acc = mix2(perm(0u, u[i], kSplit13), x[4 * i + 1], x[4 * i + 3], acc);
   }
   return acc;
 }
@@ -126,46 +143,46 @@ template <> struct Fmt<GQ8_0> {
   __device__ static int block(int lane, int c0) { return c0 / BE + lane; }
   struct Raw {
     Words<9> w;
-    uint32_t sel;  // picks qs dword i out of {w[i+1], w[i]}
-    int dsh;       // bit offset of d in w[0]
+    uint32_t s02, s13;  // selectors: qs bytes (4i, 4i+2) / (4i+1, 4i+3) from {w[i+1], w[i]}
+    int dsh;            // bit offset of d in w[0]
   };
   __device__ static void load(__amdgpu_buffer_rsrc_t r, int blk, int, Raw& raw) {
     raw.w.load(r, blk & ~3);
+    // qs starts 2 bytes into w[0] when the block is 4-aligned, else 4.
     const bool sh = (blk & 2) != 0;
-    raw.sel = sh ? kPerm4 : kPerm2;
+    raw.s02 = sh ? 0x0c060c04u : 0x0c040c02u;
+    raw.s13 = sh ? 0x0c070c05u : 0x0c050c03u;
     raw.dsh = sh ? 16 : 0;
   }
   __device__ static float dot(const Raw& raw, int, const XPart& x) {
-    const float d = f16bits(raw.w.t[0] >> raw.dsh);
-    // Flipping each byte's sign bit gives u = q + 128 (unsigned), so
+    const float d = h_lo(raw.w.t[0] >> raw.dsh);
+    // Flipping each byte's sign bit gives u = q + 128 (0..255), so
     // sum q x = sum u x - 128 sum x.
-    uint32_t u0[4], u1[4];
+    float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      u0[i] = perm(raw.w.t[i + 1], raw.w.t[i], raw.sel) ^ 0x80808080u;
-      u1[i] = perm(raw.w.t[i + 5], raw.w.t[i + 4], raw.sel) ^ 0x80808080u;
+    for (int i = 0; i < 8; ++i) {
+      const float* xv = x.v + 4 * i;
+      acc = mix2(perm(raw.w.t[i + 1], raw.w.t[i], raw.s02) ^ 0x00800080u, xv[0], xv[2], acc);
+      acc = mix2(perm(raw.w.t[i + 1], raw.w.t[i], raw.s13) ^ 0x00800080u, xv[1], xv[3], acc);
     }
-    const float acc = run_dot(u0, x.v) + run_dot(u1, x.v + 16);
-    return d * (acc - 128.0f * (x.s0 + x.s1));
+    return d * (acc * kTwo24 - 128.0f * (x.s0 + x.s1));
   }
 };
 
-// simd.zig:211-219: 6-bit (scale, min) of sub-blocks 2j and 2j + 1 from the
-// 12 packed bytes at block bytes 4..16 (header dwords 1..3), branch-free in j.
-__device__ inline void k4_scale_min_pair(int j, const uint32_t (&h)[4], uint32_t (&sc)[2], uint32_t (&mn)[2]) {
-  const int sft = 16 * (j & 1);
-  // bytes s, s + 4 and s + 8 of the packed scales, s = 2 (j & 1) + t
-  const uint32_t a = h[1] >> sft, b = h[2] >> sft, c = h[3] >> sft;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const uint32_t at = (a >> (8 * t)) & 0xffu, bt = (b >> (8 * t)) & 0xffu, ct = (c >> (8 * t)) & 0xffu;
-    // sub-block s < 4: scales[s] & 63 and scales[s + 4] & 63;
-    // sub-block s + 4: low nibble of scales[s + 8] | top 2 bits of scales[s],
-    //                  high nibble of scales[s + 8] | top 2 bits of scales[s + 4]
-    const uint32_t sc_hi = (ct & 0x0Fu) | ((at >> 6) << 4), mn_hi = (ct >> 4) | ((bt >> 6) << 4);
-    sc[t] = j < 2 ? (at & 0x3Fu) : sc_hi;
-    mn[t] = j < 2 ? (bt & 0x3Fu) : mn_hi;
-  }
+// simd.zig:211-219: the 6-bit scales and mins of sub-blocks 2j and 2j + 1 as
+// bytes [sc0, sc1, mn0, mn1], from the 12 packed bytes at block bytes 4..16
+// (header dwords 1..3).  With s' = 2 (j & 1) + t and bytes A = scales[s'],
+// B = scales[s' + 4], C = scales[s' + 8]:
+//   j < 2  (sub-block s'):     sc = A & 63, mn = B & 63
+//   j >= 2 (sub-block s' + 4): sc = (C & 15) | (A >> 6) << 4,
+//                              mn = (C >> 4) | (B >> 6) << 4
+__device__ inline uint32_t k4_scale_min_pair(int j, const uint32_t (&h)[4]) {
+  const bool odd = (j & 1) != 0;
+  const uint32_t p = perm(h[2], h[1], odd ? 0x07060302u : 0x05040100u);  // [A0 A1 B0 B1]
+  const uint32_t q = perm(h[3], h[3], odd ? 0x03020302u : 0x01000100u);  // [C0 C1 C0 C1]
+  const uint32_t lo = p & 0x3F3F3F3Fu;
+  const uint32_t hi = ((q >> 4) & 0x0F0F0000u) | (q & 0x00000F0Fu) | ((p >> 2) & 0x30303030u);
+  return j < 2 ? lo : hi;
 }
 
 // simd.zig:192-243 (Q4_K), 275-317 (Q5_K).  Lane c = 0..7 of a block reads
@@ -196,23 +213,38 @@ template <bool FIVE> struct FmtK45 {
   }
   __device__ static float dot(const Raw& raw, int c, const XPart& x) {
     const int j = c >> 1;
-    uint32_t sc[2], mn[2];
-    k4_scale_min_pair(j, raw.h.t, sc, mn);
-    const float d = f16bits(raw.h.t[0]), dmin = f16bits(raw.h.t[0] >> 16);
-    uint32_t lo[4], hi[4];
+    float a0, a1;  // run sums, as 2^-24 (Q4_K run 1: 2^-20) * sum q x
+    if constexpr (FIVE) {
+      uint32_t lo[4], hi[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t l = raw.q.t[i] & 0x0F0F0F0Fu, h = (raw.q.t[i] >> 4) & 0x0F0F0F0Fu;
-      if constexpr (FIVE) {
-        l |= ((raw.qh.t[i] >> (2 * j)) & 0x01010101u) << 4;
-        h |= ((raw.qh.t[i] >> (2 * j + 1)) & 0x01010101u) << 4;
+      for (int i = 0; i < 4; ++i) {
+        lo[i] = (raw.q.t[i] & 0x0F0F0F0Fu) | (((raw.qh.t[i] >> (2 * j)) & 0x01010101u) << 4);
+        hi[i] = ((raw.q.t[i] >> 4) & 0x0F0F0F0Fu) | (((raw.qh.t[i] >> (2 * j + 1)) & 0x01010101u) << 4);
       }
-      lo[i] = opaque(l);
-      hi[i] = opaque(h);
+      a0 = byte_run(lo, x.v) * kTwo24;
+      a1 = byte_run(hi, x.v + 16) * kTwo24;
+    } else {
+      // q & 0x000F000F: low nibbles of bytes 0 and 2 (weights 4i, 4i + 2 of
+      // run 0); & 0x00F000F0: their high nibbles (run 1), four bits up; the
+      // same of q >> 8 for bytes 1 and 3.
+      float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w = raw.q.t[i], w8 = w >> 8;
+        const float* x0 = x.v + 4 * i;
+        const float* x1 = x.v + 16 + 4 * i;
+        s0 = mix2(w & 0x000F000Fu, x0[0], x0[2], s0);
+        s0 = mix2(w8 & 0x000F000Fu, x0[1], x0[3], s0);
+        s1 = mix2(w & 0x00F000F0u, x1[0], x1[2], s1);
+        s1 = mix2(w8 & 0x00F000F0u, x1[1], x1[3], s1);
+      }
+      a0 = s0 * kTwo24;
+      a1 = s1 * kTwo20;
     }
-    const float a0 = run_dot(lo, x.v), a1 = run_dot(hi, x.v + 16);
-    return (d * (float)sc[0]) * a0 - (dmin * (float)mn[0]) * x.s0 + (d * (float)sc[1]) * a1 -
-           (dmin * (float)mn[1]) * x.s1;
+    const uint32_t v = k4_scale_min_pair(j, raw.h.t);
+    const float d = h_lo(raw.h.t[0]), dmin = h_hi(raw.h.t[0]);
+    return (d * ubyte_f(v, 0)) * a0 - (dmin * ubyte_f(v, 2)) * x.s0 + (d * ubyte_f(v, 1)) * a1 -
+           (dmin * ubyte_f(v, 3)) * x.s1;
   }
 };
 template <> struct Fmt<GQ4_K> : FmtK45<false> {};
@@ -263,11 +295,11 @@ template <> struct Fmt<GQ6_K> {
     for (int i = 0; i < 4; ++i) {
       const uint32_t w = perm(raw.ql.t[i + 1], raw.ql.t[i], raw.sel);
       const uint32_t q = perm(raw.qh.t[i + 1], raw.qh.t[i], raw.sel);
-      lo[i] = opaque((w & 0x0F0F0F0Fu) | (((q >> (2 * a)) & 0x03030303u) << 4));
-      hi[i] = opaque(((w >> 4) & 0x0F0F0F0Fu) | (((q >> (2 * a + 4)) & 0x03030303u) << 4));
+      lo[i] = (w & 0x0F0F0F0Fu) | (((q >> (2 * a)) & 0x03030303u) << 4);
+      hi[i] = ((w >> 4) & 0x0F0F0F0Fu) | (((q >> (2 * a + 4)) & 0x03030303u) << 4);
     }
-    const float a0 = run_dot(lo, x.v), a1 = run_dot(hi, x.v + 16);
-    const float d = f16bits(raw.d.t[0] >> raw.dsh);
+    const float a0 = byte_run(lo, x.v) * kTwo24, a1 = byte_run(hi, x.v + 16) * kTwo24;
+    const float d = h_lo(raw.d.t[0] >> raw.dsh);
     // sc[8h + t] and sc[8h + t + 4], t = lh + 2a: byte t of the two realigned
     // scale dwords.
     const int t = lh + 2 * a;

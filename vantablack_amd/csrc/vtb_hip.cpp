@@ -426,9 +426,10 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const void* q, const void* k
 }
 
 // Quantised GEMV launcher: out[m] = W[m, k] . x.  One workgroup per R rows
-// with one wave per 2048 columns (k <= 32768; R = 4 only up to 16384); R is
-// the largest of 4 / 2 / 1 that still gives two workgroups per CU
-// (VTB_GEMV_R overrides).
+// with one wave per 2048 columns (k <= 32768; R = 4 only up to 16384).  R is
+// 4 where it still gives two workgroups per CU, except for Q6_K with k above
+// 8192 (R = 4: 15.3 us, R = 2: 14.4 us for 4096 x 11008), else 2, else 1;
+// VTB_GEMV_R overrides.
 int launch_gemv(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* x, size_t m, size_t k) {
   if (qk < 0 || qk >= kNumQuant) return set_err(ctx, VTB_HIP_EINVAL, "bad quant kind");
   if (m == 0 || k == 0 || k % kQuantBlockElems[qk] != 0)
@@ -445,6 +446,7 @@ int launch_gemv(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* 
   for (int i = kNumGemvR - 1; i >= 0; --i) {
     const long long wgs = ((long long)m + kGemvRs[i] - 1) / kGemvRs[i];
     if (kGemvRs[i] == 4 && k > 8 * 2048) continue;  // the R = 4 kernels take at most 8 waves
+    if (!forced && kGemvRs[i] == 4 && qk == 3 && k > 4 * 2048) continue;
     if (forced ? forced == kGemvRs[i] : wgs >= 2LL * std::max(ctx->cu_count, 1)) {
       ri = i;
       break;
