@@ -487,6 +487,10 @@ def main():
         "C4_L8192": bench_prefill(ctx, torch, 32, 8, 128, 8192),
         "C5_L4096": bench_prefill(ctx, torch, 8, 1, 256, 4096),
     }
+    # The next row beside attention: segMatmulQuant's GEMVs at Llama-2-7B
+    # shapes, HBM-bound (weights streamed once per launch).
+    gemv = None if args.no_gemv else {kind: bench_gemv_layer(ctx, torch, kind)
+                                       for kind in ("q4_k", "q5_k", "q6_k", "q8_0")}
     cpu = None if args.no_cpu else cpu_baseline()
     ctx.close()
     traffic = load_traffic()
@@ -526,13 +530,11 @@ def main():
     }
     if dec_more:
         line["decode_other_configs"] = dec_more
-    if not args.no_gemv:
-        # The next row beside attention: segMatmulQuant's GEMVs at Llama-2-7B
-        # shapes, HBM-bound (weights streamed once per launch).
+    if gemv:
         line["quant_gemv"] = {
             "workload": "Llama-2-7B layer projections q,k,v,o 4096x4096, gate,up 11008x4096, down 4096x11008; "
                         "f32 activations; weights cycled over >= 512 MB so each launch reads HBM",
-            **{kind: bench_gemv_layer(ctx, torch, kind) for kind in ("q4_k", "q5_k", "q6_k", "q8_0")},
+            **gemv,
         }
     if pre:
         p8 = pre["C4_L8192"]
