@@ -202,6 +202,35 @@ int vtb_hip_matmul_q5_k(VtbHipCtx *ctx, VtbHipBuf *out_buf, VtbHipBuf *w_buf, si
 int vtb_hip_matmul_q6_k(VtbHipCtx *ctx, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
                         VtbHipBuf *acts_buf, size_t m, size_t k);
 
+/* ---- Batched quantised matmuls (prefill projections): out[b][i] =
+ * sum_j W[i, j] * acts[b][j] for B tokens; W as above (m rows of k weights in
+ * GGUF blocks at w_offset), acts f32 [B][k] (16-byte aligned), out f32
+ * [B][m].  Replace matmulBatched (prefill.zig:325-378, called at :170-226 for
+ * the q/k/v/o and FFN projections of a prompt), which dequantises each row
+ * (dequantToF32, forward.zig:654-730) and takes simd.dot_f32 with every
+ * token.  Computed on MFMA from an exact three-piece bf16 split of acts:
+ * every product is exact and sums are f32 (results agree with the CPU path
+ * to ~1e-6 relative).  k a multiple of the block size and at most 32768 (the
+ * reference's MAX_K: error 5 above it); weights 4-byte aligned, below 2 GiB.
+ * The context keeps a scratch of 6*Bp*k + Bp*k/4 bytes (Bp = B rounded up to
+ * 128), grown on demand.  vtb_hip_matmul_batched_* run synchronously. */
+void vtb_hip_segment_matmul_batched_q8_0(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                                         VtbHipBuf *acts_buf, size_t m, size_t k, size_t B);
+void vtb_hip_segment_matmul_batched_q4_k(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                                         VtbHipBuf *acts_buf, size_t m, size_t k, size_t B);
+void vtb_hip_segment_matmul_batched_q5_k(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                                         VtbHipBuf *acts_buf, size_t m, size_t k, size_t B);
+void vtb_hip_segment_matmul_batched_q6_k(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                                         VtbHipBuf *acts_buf, size_t m, size_t k, size_t B);
+int vtb_hip_matmul_batched_q8_0(VtbHipCtx *ctx, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                                VtbHipBuf *acts_buf, size_t m, size_t k, size_t B);
+int vtb_hip_matmul_batched_q4_k(VtbHipCtx *ctx, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                                VtbHipBuf *acts_buf, size_t m, size_t k, size_t B);
+int vtb_hip_matmul_batched_q5_k(VtbHipCtx *ctx, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                                VtbHipBuf *acts_buf, size_t m, size_t k, size_t B);
+int vtb_hip_matmul_batched_q6_k(VtbHipCtx *ctx, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
+                                VtbHipBuf *acts_buf, size_t m, size_t k, size_t B);
+
 /* ---- KvCache, device-handle mode (kv_cache.zig:20-196).  Layer-major
  * [n_layers][max_seq][n_kv_heads][head_dim] of dtype in HBM; no host slices. */
 VtbHipKvCache *vtb_hip_kv_cache_init(VtbHipCtx *ctx, size_t n_layers, size_t n_kv_heads,

@@ -70,6 +70,7 @@ def lib():
         L.vtb_oracle_quant_block_elems.restype = S
         L.vtb_oracle_dequant_block.argtypes = [ctypes.c_int, P, P]
         L.vtb_oracle_matmul_quant.argtypes = [ctypes.c_int, P, P, P, S, S]
+        L.vtb_oracle_matmul_batched.argtypes = [ctypes.c_int, P, P, P, S, S, S]
         L.vtb_oracle_rope_half.argtypes = [P, S, S, F]
         L.vtb_oracle_rope_inv_freq.argtypes = [P, S, F]
         L.vtb_oracle_argmax.argtypes = [P, S]
@@ -245,6 +246,19 @@ def matmul_quant(kind: str, w: np.ndarray, x: np.ndarray, m: int, k: int) -> np.
     if rc != 0:
         raise ValueError("matmul_quant: k is not a whole number of blocks")
     return out
+
+
+def matmul_batched(kind: str, w: np.ndarray, acts: np.ndarray, m: int, k: int, B: int) -> np.ndarray:
+    """out[B, m]: dequantised weight rows . each token's activations
+    (prefill.zig matmulBatched: dequantToF32 + simd.dot_f32)."""
+    wb = np.ascontiguousarray(w, dtype=np.uint8)
+    xa = np.ascontiguousarray(acts, dtype=np.float32).reshape(-1)
+    assert xa.size == B * k
+    out = np.empty(B * m, np.float32)
+    rc = lib().vtb_oracle_matmul_batched(QUANT_KINDS[kind], _ptr(out), _ptr(wb), _ptr(xa), m, k, B)
+    if rc != 0:
+        raise ValueError("matmul_batched: k is not a whole number of blocks or above 32768")
+    return out.reshape(B, m)
 
 
 def argmax(x: np.ndarray) -> int:

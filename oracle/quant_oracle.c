@@ -15,6 +15,7 @@
  * level only; the GPU bar is 1e-4 relative, bridge.zig:466-470). */
 #include <stddef.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 float vtb_oracle_f16_to_f32(uint16_t h); /* attn_oracle.c */
 
@@ -147,5 +148,39 @@ int vtb_oracle_matmul_quant(int kind, float *out, const uint8_t *w, const float 
         }
         out[i] = total;
     }
+    return 0;
+}
+
+/* simd.zig:13-29 (dot_f32): eight lane accumulators over the whole length,
+ * each product rounded then added (no contraction), reduced in lane order,
+ * then the tail (none for whole blocks). */
+static float dot_f32(const float *a, const float *b, size_t n) {
+    float acc[8] = {0};
+    size_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; l++) acc[l] += a[i + l] * b[i + l];
+    float sum = reduce8(acc);
+    for (; i < n; i++) sum += a[i] * b[i];
+    return sum;
+}
+
+/* prefill.zig:325-378 (matmulBatched / matmulBatchedWorker): for each weight
+ * row, dequantise the whole row (forward.zig:654-730 dequantToF32, block by
+ * block) and take dot_f32 with every token's activations:
+ *   out[b*m + row] = dot_f32(dequant(W[row]), acts[b*k .. b*k + k]).
+ * 0, or -1 for an unknown kind, k not a whole number of blocks or k above
+ * the reference's MAX_K of 32768 (which returns DimTooLarge). */
+int vtb_oracle_matmul_batched(int kind, float *out, const uint8_t *w, const float *acts, size_t m, size_t k,
+                              size_t B) {
+    if (kind < 0 || kind > 3 || k % block_elems[kind] != 0 || k > 32768) return -1;
+    const size_t be = block_elems[kind], bb = block_bytes[kind];
+    const size_t nb = k / be, row_bytes = nb * bb;
+    float *dq = (float *)malloc(k * sizeof(float));
+    if (!dq) return -1;
+    for (size_t row = 0; row < m; row++) {
+        for (size_t b = 0; b < nb; b++) vtb_oracle_dequant_block(kind, w + row * row_bytes + b * bb, dq + b * be);
+        for (size_t t = 0; t < B; t++) out[t * m + row] = dot_f32(dq, acts + t * k, k);
+    }
+    free(dq);
     return 0;
 }

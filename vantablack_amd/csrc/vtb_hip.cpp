@@ -26,6 +26,7 @@ extern const unsigned char vtb_blob_decode[];
 extern const unsigned char vtb_blob_prefill[];
 extern const unsigned char vtb_blob_kvcopy[];
 extern const unsigned char vtb_blob_gemv[];
+extern const unsigned char vtb_blob_qgemm[];
 }
 
 namespace {
@@ -126,11 +127,37 @@ struct GemvArgs {
   int row_bytes;
 };
 
+// Mirrors vtb::XSplitArgs / vtb::QGemmArgs (kernels/qgemm.hip).
+struct XSplitArgs {
+  const float* x;
+  uint16_t* planes;
+  float* sums;
+  int B;
+  int Bp;
+  int k;
+  int pad;
+};
+struct QGemmArgs {
+  const void* w;
+  const uint16_t* planes;
+  const float* sums;
+  float* out;
+  unsigned w_bytes;
+  int m;
+  int k;
+  int B;
+  int Bp;
+  int row_bytes;
+  int n_rb;
+  int n_tb;
+};
+
 struct VtbHipCtx {
   int device = 0;
   int cu_count = 0;
   hipStream_t stream = nullptr;
-  hipModule_t mod_decode = nullptr, mod_prefill = nullptr, mod_kvcopy = nullptr, mod_gemv = nullptr;
+  hipModule_t mod_decode = nullptr, mod_prefill = nullptr, mod_kvcopy = nullptr, mod_gemv = nullptr,
+              mod_qgemm = nullptr;
   hipFunction_t f_decode[kNumKv][kNumD][kNumG] = {};
   hipFunction_t f_prefill[kNumKv][kNumD] = {};
   hipFunction_t f_prefill8[kNumKv][kNumD] = {};  // wide (8-wave) variant, d <= 128
@@ -138,6 +165,8 @@ struct VtbHipCtx {
   hipFunction_t f_append[kNumKv] = {};
   hipFunction_t f_copy = nullptr;
   hipFunction_t f_gemv[kNumQuant][kNumGemvR] = {};  // vtb_gemv_<kind>_r<1|2|4>
+  hipFunction_t f_xsplit = nullptr;
+  hipFunction_t f_qgemm[kNumQuant] = {};  // vtb_qgemm_<kind>
   // Split-K workspace and arrival counters (counters are zero between launches).
   void* ws = nullptr;
   size_t ws_bytes = 0;
@@ -149,6 +178,10 @@ struct VtbHipCtx {
   // Prefill V^T scratch (f16, written by the vtb_vt_* pre-pass).
   void* vt = nullptr;
   size_t vt_bytes = 0;
+  // Batched-matmul activation scratch: three bf16 planes [3][Bp][k] and the
+  // 16-column sums [Bp][k/16], written by vtb_xsplit.
+  void* qg = nullptr;
+  size_t qg_bytes = 0;
   // RoPE inverse-frequency tables 1/base^(2j/d) on the device, one per
   // (base, head_dim) seen; the host copy stays alive for the async upload.
   struct RopeTable {
@@ -473,6 +506,65 @@ int launch_gemv(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* 
   return launch(ctx, ctx->f_gemv[qk][ri], (unsigned)((m + R - 1) / R), 1, 1, 64 * waves, &a, lds);
 }
 
+// Batched quantised matmul launcher: out[B][m] = acts[B][k] . W^T.  The
+// pre-pass splits acts into three bf16 planes and 16-column sums in the
+// context's scratch (grown on demand, after the stream drains); the GEMM
+// then runs one workgroup per 128 tokens x 128 rows.
+int launch_qgemm(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* acts, size_t m, size_t k,
+                 size_t B) {
+  if (qk < 0 || qk >= kNumQuant) return set_err(ctx, VTB_HIP_EINVAL, "bad quant kind");
+  if (m == 0 || k == 0 || B == 0 || k % kQuantBlockElems[qk] != 0 || k % 32 != 0)
+    return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: k must be a positive multiple of the block size");
+  // prefill.zig MAX_K: the reference returns DimTooLarge above it.
+  if (k > 32768) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul_batched: k above 32768");
+  const size_t row_bytes = k / kQuantBlockElems[qk] * kQuantBlockBytes[qk];
+  if (m > 0x7fff0000 / row_bytes) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul_batched: weights beyond 2 GiB");
+  if (B > (1u << 24) || m > (1u << 24)) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul_batched: too many tokens or rows");
+  if ((uintptr_t)w % 4 != 0) return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: weights not 4-byte aligned");
+  if (!aligned16(acts)) return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: activations not 16-byte aligned");
+  const size_t Bp = (B + 127) / 128 * 128;
+  const size_t planes_bytes = 3 * Bp * k * 2, sums_bytes = Bp * (k / 16) * 4;
+  const size_t need = planes_bytes + sums_bytes;
+  if (need > ctx->qg_bytes) {
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (ctx->qg) HIP_TRY(ctx, hipFree(ctx->qg), "hipFree");
+    ctx->qg = nullptr;
+    ctx->qg_bytes = 0;
+    HIP_TRY(ctx, hipMalloc(&ctx->qg, need), "hipMalloc(batched matmul scratch)");
+    ctx->qg_bytes = need;
+  }
+  uint16_t* planes = (uint16_t*)ctx->qg;
+  float* sums = (float*)((char*)ctx->qg + planes_bytes);
+  XSplitArgs xa;
+  memset(&xa, 0, sizeof xa);
+  xa.x = acts;
+  xa.planes = planes;
+  xa.sums = sums;
+  xa.B = (int)B;
+  xa.Bp = (int)Bp;
+  xa.k = (int)k;
+  const size_t groups = Bp * (k / 16);
+  int rc = launch(ctx, ctx->f_xsplit, (unsigned)((groups + 255) / 256), 1, 1, 256, &xa);
+  if (rc) return rc;
+  QGemmArgs a;
+  memset(&a, 0, sizeof a);
+  a.w = w;
+  a.planes = planes;
+  a.sums = sums;
+  a.out = out;
+  // Rounded up to whole dwords: the last 2-byte-aligned field can end two
+  // bytes into one (see launch_gemv).
+  a.w_bytes = (unsigned)((m * row_bytes + 3) & ~(size_t)3);
+  a.m = (int)m;
+  a.k = (int)k;
+  a.B = (int)B;
+  a.Bp = (int)Bp;
+  a.row_bytes = (int)row_bytes;
+  a.n_rb = (int)((m + 127) / 128);
+  a.n_tb = (int)(Bp / 128);
+  return launch(ctx, ctx->f_qgemm[qk], (unsigned)(a.n_rb * a.n_tb), 1, 1, 256, &a);
+}
+
 int launch_append(VtbHipCtx* ctx, void* dst, const float* src, size_t n, int dtype) {
   if (n == 0) return VTB_HIP_OK;
   if (dtype < 0 || dtype >= kNumKv) return set_err(ctx, VTB_HIP_EINVAL, "bad kv dtype");
@@ -518,6 +610,7 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
   ok = ok && hipModuleLoadData(&ctx->mod_prefill, vtb_blob_prefill) == hipSuccess;
   ok = ok && hipModuleLoadData(&ctx->mod_kvcopy, vtb_blob_kvcopy) == hipSuccess;
   ok = ok && hipModuleLoadData(&ctx->mod_gemv, vtb_blob_gemv) == hipSuccess;
+  ok = ok && hipModuleLoadData(&ctx->mod_qgemm, vtb_blob_qgemm) == hipSuccess;
   char name[96];
   for (int kv = 0; ok && kv < kNumKv; ++kv) {
     for (int di = 0; ok && di < kNumD; ++di) {
@@ -549,6 +642,11 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
       snprintf(name, sizeof name, "vtb_gemv_%s_r%d", kQuantNames[qk], kGemvRs[ri]);
       ok = hipModuleGetFunction(&ctx->f_gemv[qk][ri], ctx->mod_gemv, name) == hipSuccess;
     }
+  ok = ok && hipModuleGetFunction(&ctx->f_xsplit, ctx->mod_qgemm, "vtb_xsplit") == hipSuccess;
+  for (int qk = 0; ok && qk < kNumQuant; ++qk) {
+    snprintf(name, sizeof name, "vtb_qgemm_%s", kQuantNames[qk]);
+    ok = hipModuleGetFunction(&ctx->f_qgemm[qk], ctx->mod_qgemm, name) == hipSuccess;
+  }
   (void)hipGetLastError();  // absent optional kernels are not an error for the caller
   if (!ok) {
     vtb_hip_destroy(ctx);
@@ -564,11 +662,13 @@ extern "C" void vtb_hip_destroy(VtbHipCtx* ctx) {
   if (ctx->counters) (void)hipFree(ctx->counters);
   if (ctx->qconv) (void)hipFree(ctx->qconv);
   if (ctx->vt) (void)hipFree(ctx->vt);
+  if (ctx->qg) (void)hipFree(ctx->qg);
   for (auto& t : ctx->rope_tables) (void)hipFree(t.dev);
   if (ctx->mod_decode) (void)hipModuleUnload(ctx->mod_decode);
   if (ctx->mod_prefill) (void)hipModuleUnload(ctx->mod_prefill);
   if (ctx->mod_kvcopy) (void)hipModuleUnload(ctx->mod_kvcopy);
   if (ctx->mod_gemv) (void)hipModuleUnload(ctx->mod_gemv);
+  if (ctx->mod_qgemm) (void)hipModuleUnload(ctx->mod_qgemm);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -842,6 +942,39 @@ VTB_MATMUL_ENTRIES(q8_0, 0)
 VTB_MATMUL_ENTRIES(q4_k, 1)
 VTB_MATMUL_ENTRIES(q5_k, 2)
 VTB_MATMUL_ENTRIES(q6_k, 3)
+
+static int matmul_batched_entry(VtbHipCtx* ctx, int qk, VtbHipBuf* out_buf, VtbHipBuf* w_buf, size_t w_offset,
+                                VtbHipBuf* acts_buf, size_t m, size_t k, size_t B) {
+  if (!ctx || !out_buf || !w_buf || !acts_buf) return VTB_HIP_EINVAL;
+  if (m == 0 || k == 0 || B == 0 || k % kQuantBlockElems[qk] != 0 || m > ((size_t)1 << 31) ||
+      k > ((size_t)1 << 31) || B > ((size_t)1 << 31))
+    return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: bad shape");
+  const size_t row_bytes = k / kQuantBlockElems[qk] * kQuantBlockBytes[qk];
+  if (!buf_ok(w_buf, w_offset, m * row_bytes) || !buf_ok(acts_buf, 0, B * k * 4) || !buf_ok(out_buf, 0, B * m * 4))
+    return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: buffer too small");
+  return launch_qgemm(ctx, qk, (float*)out_buf->ptr, bptr(w_buf, w_offset), (const float*)acts_buf->ptr, m, k, B);
+}
+
+#define VTB_MATMUL_BATCHED_ENTRIES(NAME, QK)                                                              \
+  extern "C" void vtb_hip_segment_matmul_batched_##NAME(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* w_buf, \
+                                                        size_t w_offset, VtbHipBuf* acts_buf, size_t m,      \
+                                                        size_t k, size_t B) {                                \
+    if (!seg) return;                                                                                      \
+    seg_note(seg, matmul_batched_entry(seg->ctx, QK, out_buf, w_buf, w_offset, acts_buf, m, k, B));        \
+  }                                                                                                        \
+  extern "C" int vtb_hip_matmul_batched_##NAME(VtbHipCtx* ctx, VtbHipBuf* out_buf, VtbHipBuf* w_buf,        \
+                                               size_t w_offset, VtbHipBuf* acts_buf, size_t m, size_t k,     \
+                                               size_t B) {                                                  \
+    int rc = matmul_batched_entry(ctx, QK, out_buf, w_buf, w_offset, acts_buf, m, k, B);                    \
+    if (rc) return rc;                                                                                     \
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");                               \
+    return VTB_HIP_OK;                                                                                     \
+  }
+
+VTB_MATMUL_BATCHED_ENTRIES(q8_0, 0)
+VTB_MATMUL_BATCHED_ENTRIES(q4_k, 1)
+VTB_MATMUL_BATCHED_ENTRIES(q5_k, 2)
+VTB_MATMUL_BATCHED_ENTRIES(q6_k, 3)
 
 // ============================================================== KvCache
 

@@ -111,6 +111,14 @@ SIGNATURES = {
     "vtb_hip_matmul_q5_k": ([_P, _P, _P, _S, _P, _S, _S], _I),
     "vtb_hip_segment_matmul_q6_k": ([_P, _P, _P, _S, _P, _S, _S], None),
     "vtb_hip_matmul_q6_k": ([_P, _P, _P, _S, _P, _S, _S], _I),
+    "vtb_hip_segment_matmul_batched_q8_0": ([_P, _P, _P, _S, _P, _S, _S, _S], None),
+    "vtb_hip_matmul_batched_q8_0": ([_P, _P, _P, _S, _P, _S, _S, _S], _I),
+    "vtb_hip_segment_matmul_batched_q4_k": ([_P, _P, _P, _S, _P, _S, _S, _S], None),
+    "vtb_hip_matmul_batched_q4_k": ([_P, _P, _P, _S, _P, _S, _S, _S], _I),
+    "vtb_hip_segment_matmul_batched_q5_k": ([_P, _P, _P, _S, _P, _S, _S, _S], None),
+    "vtb_hip_matmul_batched_q5_k": ([_P, _P, _P, _S, _P, _S, _S, _S], _I),
+    "vtb_hip_segment_matmul_batched_q6_k": ([_P, _P, _P, _S, _P, _S, _S, _S], None),
+    "vtb_hip_matmul_batched_q6_k": ([_P, _P, _P, _S, _P, _S, _S, _S], _I),
     "vtb_hip_prefill_attention": ([_P, _P, ctypes.POINTER(AttnConfigC), _S, _S, _P, _P, _P, _P], _I),
 }
 
@@ -235,6 +243,15 @@ class Segment:
         if kind not in QUANT_KINDS:
             raise ValueError(f"unknown quant kind {kind!r}")
         getattr(lib(), f"vtb_hip_segment_matmul_{kind}")(self.h, out.h, w.h, w_offset, acts.h, m, k)
+
+    def matmul_batched(self, kind: str, out: Buffer, w: Buffer, w_offset: int, acts: Buffer, m: int, k: int,
+                       n_tokens: int):
+        """out[b] = W @ acts[b] for n_tokens tokens (prefill.zig matmulBatched)
+        on the segment; acts f32 [n_tokens][k], out f32 [n_tokens][m]."""
+        if kind not in QUANT_KINDS:
+            raise ValueError(f"unknown quant kind {kind!r}")
+        getattr(lib(), f"vtb_hip_segment_matmul_batched_{kind}")(self.h, out.h, w.h, w_offset, acts.h, m, k,
+                                                                  n_tokens)
 
     def attn_prefill(self, out: Buffer, q: Buffer, k: Buffer, v: Buffer, layer_off: int, n_tokens: int,
                      pos0: int, sliding_window: int, n_heads: int, n_kv_heads: int, head_dim: int,
