@@ -321,6 +321,61 @@ def bench_gemv_layer(ctx, torch, kind):
     return res
 
 
+# Llama-3-8B (C4's model) layer projections: (name, m, k, count per layer).
+LLAMA3_8B_PROJ = (("q_o", 4096, 4096, 2), ("k_v", 1024, 4096, 2), ("gate_up", 14336, 4096, 2),
+                  ("down", 4096, 14336, 1))
+
+
+def bench_qgemm_layer(ctx, torch, kind, n_tokens, reps=3):
+    """matmulBatched's seven projections of one Llama-3-8B layer for a prompt
+    of n_tokens (the C4 prefill's other half), `kind` weights.  Reference
+    flops are 2*m*k*B per projection; the MFMA work is three times that (the
+    activations enter as three exact bf16 pieces), reported against the
+    dense bf16 peak."""
+    import vantablack_amd as vb
+    bb, be = QUANT_BLOCK[kind]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+    res, tot_t, tot_f = {}, 0.0, 0.0
+    for name, m, k, count in LLAMA3_8B_PROJ:
+        wbytes = m * (k // be * bb)
+        w = torch.randint(0, 256, (wbytes,), generator=g, dtype=torch.uint8, device=dev)
+        x = torch.randn(n_tokens, k, generator=g, device=dev)
+        out = torch.empty(n_tokens, m, device=dev)
+        torch.cuda.synchronize()
+        wb, xb, ob = ctx.wrap_tensor(w), ctx.wrap_tensor(x), ctx.wrap_tensor(out)
+        with ctx.segment() as seg:
+            seg.matmul_batched(kind, ob, wb, 0, xb, m, k, n_tokens)
+        ctx.wait_idle()
+        stream = torch.cuda.ExternalStream(ctx.stream)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        with ctx.segment() as seg:
+            for _ in range(reps):
+                seg.matmul_batched(kind, ob, wb, 0, xb, m, k, n_tokens)
+        e1.record(stream)
+        ctx.wait_idle()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / reps
+        for b in (wb, xb, ob):
+            b.release()
+        del w, x, out
+        torch.cuda.empty_cache()
+        fl = 2.0 * m * k * n_tokens
+        log(f"qgemm {kind} {m}x{k} B={n_tokens}: {t * 1e6:.1f} us -> {fl / t / 1e12:.1f} TFLOP/s "
+            f"(MFMA {3 * fl / t / 1e12:.1f})")
+        res[name] = {"us": round(t * 1e6, 1), "tflops": round(fl / t / 1e12, 1),
+                     "mfma_tflops": round(3 * fl / t / 1e12, 1),
+                     "pct_of_bf16_peak": round(100.0 * 3 * fl / t / 1e12 / BF16_PEAK_TFLOPS, 2)}
+        tot_t += count * t
+        tot_f += count * fl
+    res["layer"] = {"us": round(tot_t * 1e6, 1), "tflops": round(tot_f / tot_t / 1e12, 1),
+                    "mfma_tflops": round(3 * tot_f / tot_t / 1e12, 1),
+                    "pct_of_bf16_peak": round(100.0 * 3 * tot_f / tot_t / 1e12 / BF16_PEAK_TFLOPS, 2)}
+    return res
+
+
 def cpu_baseline(seconds_budget=12.0):
     """Time the CPU oracle on a bounded sample of the decode workload: one
     C2 layer at L=8192 (f32 values of the f16 cache, as vantablack's f32
@@ -460,7 +515,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-more", action="store_true", help="skip the C1/C3/C5 decode lines")
-    ap.add_argument("--no-gemv", action="store_true", help="skip the quantised GEMV lines")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the quantised GEMV / batched matmul lines")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; the path's multi-GPU sharding is "
@@ -491,6 +546,8 @@ def main():
     # shapes, HBM-bound (weights streamed once per launch).
     gemv = None if args.no_gemv else {kind: bench_gemv_layer(ctx, torch, kind)
                                        for kind in ("q4_k", "q5_k", "q6_k", "q8_0")}
+    # matmulBatched (the prefill projections) at the C4 prompt length.
+    qgemm = None if args.no_gemv else bench_qgemm_layer(ctx, torch, "q4_k", 8192)
     cpu = None if args.no_cpu else cpu_baseline()
     ctx.close()
     traffic = load_traffic()
@@ -535,6 +592,13 @@ def main():
             "workload": "Llama-2-7B layer projections q,k,v,o 4096x4096, gate,up 11008x4096, down 4096x11008; "
                         "f32 activations; weights cycled over >= 512 MB so each launch reads HBM",
             **gemv,
+        }
+    if qgemm:
+        line["prefill_projections"] = {
+            "workload": "Llama-3-8B layer projections (q,o 4096x4096; k,v 1024x4096; gate,up 14336x4096; "
+                        "down 4096x14336), Q4_K weights, f32 activations, 8192 tokens (C4 prompt length)",
+            "flops": "reference flops 2*m*k*B; MFMA work 3x (activations as three exact bf16 pieces)",
+            "q4_k": qgemm,
         }
     if pre:
         p8 = pre["C4_L8192"]
