@@ -208,12 +208,13 @@ int vtb_hip_matmul_q6_k(VtbHipCtx *ctx, VtbHipBuf *out_buf, VtbHipBuf *w_buf, si
  * [B][m].  Replace matmulBatched (prefill.zig:325-378, called at :170-226 for
  * the q/k/v/o and FFN projections of a prompt), which dequantises each row
  * (dequantToF32, forward.zig:654-730) and takes simd.dot_f32 with every
- * token.  Computed on MFMA from an exact three-piece bf16 split of acts:
- * every product is exact and sums are f32 (results agree with the CPU path
- * to ~1e-6 relative).  k a multiple of the block size and at most 32768 (the
+ * token.  Computed on MFMA from a two-piece f16 split of each token's acts
+ * scaled by a power of two (22 significant bits per activation); products
+ * are exact and sums f32 (results agree with the CPU path to ~1e-6 of
+ * sum |W||x|).  k a multiple of the block size and at most 32768 (the
  * reference's MAX_K: error 5 above it); weights 4-byte aligned, below 2 GiB.
- * The context keeps a scratch of 6*Bp*k + Bp*k/4 bytes (Bp = B rounded up to
- * 128), grown on demand.  vtb_hip_matmul_batched_* run synchronously. */
+ * The context keeps a scratch of 4*Bp*k + Bp*k/4 + 4*Bp bytes (Bp = B
+ * rounded up to 128), grown on demand.  vtb_hip_matmul_batched_* run synchronously. */
 void vtb_hip_segment_matmul_batched_q8_0(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,
                                          VtbHipBuf *acts_buf, size_t m, size_t k, size_t B);
 void vtb_hip_segment_matmul_batched_q4_k(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_offset,

@@ -60,10 +60,12 @@ def test_weight_offset(ctx, orc, kind):
 
 
 def test_activation_extremes(ctx, orc):
-    # magnitudes spread over 80 binades and exact zeros: the bf16 split must
-    # stay exact.  With this range a sum near 1e-3 of sum |W||x| has lost its
-    # small terms in either f32 accumulation order (the oracle's and the
-    # GPU's alike), so only the conditioning-relative bar applies.
+    # magnitudes spread over 80 binades and exact zeros: the per-token
+    # power-of-two scaling and the two-piece split must hold every value to
+    # 22 bits (or 2^-40 of the token's largest).  With this range a sum near
+    # 1e-3 of sum |W||x| has lost its small terms in either f32 accumulation
+    # order (the oracle's and the GPU's alike), so only the
+    # conditioning-relative bar applies.
     rng = np.random.default_rng(3)
     B, k = 64, 1024
     x = (rng.standard_normal((B, k)) * np.exp2(rng.integers(-40, 40, (B, k)))).astype(np.float32)

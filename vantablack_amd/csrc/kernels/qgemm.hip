@@ -6,16 +6,20 @@
 // every weight row dequantised as dequantToF32 does
 // (src/runtime/forward.zig:654-730) and dotted with each token in f32.
 //
-// Exactness.  Every quant is a small integer, exact in bf16.  Each f32
-// activation is cut into three bf16 pieces by truncation (pre-pass
-// vtb_xsplit): x1 = the top 8 significant bits of x, x2 = the top 8 of
-// x - x1, x3 = the rest, which has at most 8 significant bits left -- so
-// x1 + x2 + x3 == x exactly (normal f32).  Products of 8-bit operands are
-// exact and v_mfma_f32_32x32x16_bf16 accumulates them in f32, so the sum
-// over a scale unit is an f32 sum of exact products, as the reference's is
-// (only the order of the additions differs).  Quants enter as the exact
-// bf16 of the integer the reference scales: q (Q4_K, Q5_K, signed Q8_0) and
-// q - 32 (Q6_K), converted once per workgroup as they are staged.
+// Precision.  Every quant is a small integer, exact in f16.  Each token's
+// activations are scaled by a power of two 2^e that puts the token's largest
+// |x| in [2^14, 2^15), then cut into two f16 pieces rounded to nearest
+// (pre-pass vtb_xsplit): h1 = f16(x 2^e), h2 = f16(x 2^e - h1).  h1 + h2
+// holds x 2^e to 22 significant bits (to an absolute 2^-25 where the
+// remainder falls below f16's normal range, i.e. 2^-40 of the token's
+// largest |x|), so the GPU sum differs from the reference's f32 one by
+// ~2^-22 of sum |W||x| at most, far inside the parity bar.  Products of
+// f16 operands are exact and v_mfma_f32_32x32x16_f16 accumulates them in
+// f32; the token's 2^-e comes back out exactly in the epilogue.  (Three
+// truncated bf16 pieces would be exact, at 3/2 the MFMA work and operand
+// traffic: measured 4-16% slower over the Llama-3-8B shapes.)  Quants enter
+// as the f16 of the integer the reference scales: q (Q4_K, Q5_K, signed
+// Q8_0) and q - 32 (Q6_K), converted once per workgroup as they are staged.
 //
 // Per scale unit (Q4_K/Q5_K sub-block and Q8_0 block of 32 columns, Q6_K
 // group of 16) the MFMAs give T = sum q x over the unit, and
@@ -29,8 +33,8 @@
 // weight row, 16 tokens per lane, so a lane needs one scale per tile).  The
 // K loop steps 32 columns: the next step's activation pieces, x sums and raw
 // weight words are loaded into registers while the current step's MFMAs run
-// from LDS; weights are converted to bf16 as they are stored.  LDS rows are
-// padded to 40 bf16 (80 bytes) so that 16 lanes' 16-byte fragment reads
+// from LDS; weights are converted to f16 as they are stored.  LDS rows are
+// padded to 40 halves (80 bytes) so that 16 lanes' 16-byte fragment reads
 // never share a bank.  Workgroup ids are remapped so that each XCD works
 // through contiguous (token block, row block) ranges, token block major:
 // the activation pieces of a token block stay in that XCD's L2.
@@ -40,72 +44,98 @@ namespace vtb {
 
 struct XSplitArgs {
   const float* x;     // [B][k]
-  uint16_t* planes;   // [3][Bp][k] bf16 bits: x1, x2, x3
-  float* sums;        // [Bp][k / 16]: sum of each 16-column group
+  uint16_t* planes;   // [2][Bp][k] f16 bits: h1, h2 of x * 2^e
+  float* sums;        // [Bp][k / 16]: sum of each 16-column group of x * 2^e
+  float* inv_scale;   // [Bp]: 2^-e of each token
   int B;
   int Bp;             // B rounded up to the token tile; rows >= B are zero
   int k;
   int pad;
 };
 
-// One thread per 16-column group of one token.
+__device__ inline float wave_max(float v) {
+  v = fmaxf(v, dpp<DPP_XOR1>(v));
+  v = fmaxf(v, dpp<DPP_XOR2>(v));
+  v = fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp<DPP_MIRROR>(v));
+  v = xor_max<16>(v);
+  return xor_max<32>(v);
+}
+
+// One workgroup (256 threads) per token: the row's largest |x| fixes the
+// token's power of two, then each thread splits 16-column groups.
 extern "C" __global__ __launch_bounds__(256) void vtb_xsplit(XSplitArgs a) {
-  const long long g = (long long)blockIdx.x * 256 + threadIdx.x;
+  __shared__ float s_max[4];
+  const int t = (int)blockIdx.x, tid = (int)threadIdx.x;
   const int gpr = a.k >> 4;
-  if (g >= (long long)a.Bp * gpr) return;
-  const int t = (int)(g / gpr), c = (int)(g % gpr) * 16;
-  float v[16];
-  if (t < a.B) {
-    const float4* p = reinterpret_cast<const float4*>(a.x + (size_t)t * a.k + c);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 q = p[i];
-      v[4 * i] = q.x;
-      v[4 * i + 1] = q.y;
-      v[4 * i + 2] = q.z;
-      v[4 * i + 3] = q.w;
+  const bool live = t < a.B;
+  const float* row = a.x + (size_t)t * a.k;
+  float mx = 0.0f;
+  if (live)
+    for (int c = 4 * tid; c < a.k; c += 1024) {
+      const float4 v = *reinterpret_cast<const float4*>(row + c);
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = 0.0f;
-  }
-  uint32_t w1[8], w2[8], w3[8];
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    s += v[j];
-    const uint32_t h1 = __builtin_bit_cast(uint32_t, v[j]) & 0xffff0000u;
-    const float r1 = v[j] - __builtin_bit_cast(float, h1);  // exact
-    const uint32_t h2 = __builtin_bit_cast(uint32_t, r1) & 0xffff0000u;
-    const float r2 = r1 - __builtin_bit_cast(float, h2);    // exact, <= 8 significant bits
-    const uint32_t h3 = __builtin_bit_cast(uint32_t, r2) & 0xffff0000u;
-    if (j & 1) {
-      w1[j >> 1] |= h1;
-      w2[j >> 1] |= h2;
-      w3[j >> 1] |= h3;
-    } else {
-      w1[j >> 1] = h1 >> 16;
-      w2[j >> 1] = h2 >> 16;
-      w3[j >> 1] = h3 >> 16;
-    }
-  }
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) s_max[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+  // 2^e with mx 2^e in [2^14, 2^15); e clamped so that 2^e and 2^-e stay
+  // normal f32 (a row that small is then scaled less, not wrongly).
+  int e = mx > 0.0f ? 14 - ilogbf(mx) : 0;
+  e = e > 100 ? 100 : (e < -100 ? -100 : e);
+  const float scale = ldexpf(1.0f, e);
+  if (tid == 0) a.inv_scale[t] = ldexpf(1.0f, -e);
   const size_t plane = (size_t)a.Bp * a.k;
-  uint4* d1 = reinterpret_cast<uint4*>(a.planes + (size_t)t * a.k + c);
-  uint4* d2 = reinterpret_cast<uint4*>(a.planes + plane + (size_t)t * a.k + c);
-  uint4* d3 = reinterpret_cast<uint4*>(a.planes + 2 * plane + (size_t)t * a.k + c);
-  d1[0] = make_uint4(w1[0], w1[1], w1[2], w1[3]);
-  d1[1] = make_uint4(w1[4], w1[5], w1[6], w1[7]);
-  d2[0] = make_uint4(w2[0], w2[1], w2[2], w2[3]);
-  d2[1] = make_uint4(w2[4], w2[5], w2[6], w2[7]);
-  d3[0] = make_uint4(w3[0], w3[1], w3[2], w3[3]);
-  d3[1] = make_uint4(w3[4], w3[5], w3[6], w3[7]);
-  a.sums[(size_t)t * gpr + (c >> 4)] = s;
+  for (int g = tid; g < gpr; g += 256) {
+    const int c = 16 * g;
+    float v[16];
+    if (live) {
+      const float4* p = reinterpret_cast<const float4*>(row + c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 q = p[i];
+        v[4 * i] = q.x;
+        v[4 * i + 1] = q.y;
+        v[4 * i + 2] = q.z;
+        v[4 * i + 3] = q.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+    }
+    uint32_t w1[8], w2[8];
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float xs = v[j] * scale;  // exact (power of two)
+      sum += xs;
+      const _Float16 h1 = (_Float16)xs;                 // round to nearest even
+      const _Float16 h2 = (_Float16)(xs - (float)h1);  // the difference is exact in f32
+      const uint32_t b1 = __builtin_bit_cast(uint16_t, h1), b2 = __builtin_bit_cast(uint16_t, h2);
+      if (j & 1) {
+        w1[j >> 1] |= b1 << 16;
+        w2[j >> 1] |= b2 << 16;
+      } else {
+        w1[j >> 1] = b1;
+        w2[j >> 1] = b2;
+      }
+    }
+    uint4* d1 = reinterpret_cast<uint4*>(a.planes + (size_t)t * a.k + c);
+    uint4* d2 = reinterpret_cast<uint4*>(a.planes + plane + (size_t)t * a.k + c);
+    d1[0] = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+    d1[1] = make_uint4(w1[4], w1[5], w1[6], w1[7]);
+    d2[0] = make_uint4(w2[0], w2[1], w2[2], w2[3]);
+    d2[1] = make_uint4(w2[4], w2[5], w2[6], w2[7]);
+    a.sums[(size_t)t * gpr + g] = sum;
+  }
 }
 
 struct QGemmArgs {
   const uint8_t* w;         // m rows of row_bytes
-  const uint16_t* planes;   // [3][Bp][k] from vtb_xsplit
-  const float* sums;        // [Bp][k / 16]
+  const uint16_t* planes;   // [2][Bp][k] f16 bits from vtb_xsplit
+  const float* sums;        // [Bp][k / 16] (of x * 2^e)
+  const float* inv_scale;   // [Bp]: 2^-e
   float* out;               // [B][m]
   unsigned w_bytes;         // m * row_bytes rounded up to a multiple of 4
   int m;
@@ -118,7 +148,7 @@ struct QGemmArgs {
 };
 
 constexpr int kQgTile = 128;  // tokens and rows per workgroup
-constexpr int kQgLd = 40;     // LDS row stride in bf16 (80 bytes)
+constexpr int kQgLd = 40;     // LDS row stride in 16-bit elements (80 bytes)
 
 __device__ inline uint32_t qload(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
@@ -127,28 +157,28 @@ __device__ inline uint32_t qperm(uint32_t hi, uint32_t lo, uint32_t sel) { retur
 __device__ inline float qh_lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu)); }
 __device__ inline float qh_hi(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
 
-// The high halves of two f32 (exact bf16 values) as one bf16 pair.
-__device__ inline uint32_t bf16_pair(float lo, float hi) {
-  return qperm(__builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo), 0x07060302u);
+// Two f32 holding small integers as one f16 pair (exact).
+__device__ inline uint32_t f16_pair(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
 }
 
-// Eight bf16 pairs (16 weights) of the byte fields of u[0..4), minus `bias`:
-// small integers, so every value is exact in bf16.
+// Eight f16 pairs (16 weights) of the byte fields of u[0..4), minus `bias`:
+// small integers, so every value is exact in f16.
 __device__ inline void byte_pairs(const uint32_t (&u)[4], float bias, uint32_t (&o)[8]) {
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
     float f[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) f[e] = (float)((u[d] >> (8 * e)) & 0xffu) - bias;
-    o[2 * d] = bf16_pair(f[0], f[1]);
-    o[2 * d + 1] = bf16_pair(f[2], f[3]);
+    o[2 * d] = f16_pair(f[0], f[1]);
+    o[2 * d + 1] = f16_pair(f[2], f[3]);
   }
 }
 
 // Per-thread staging of the weights of one K step (32 columns): thread
 // (row, half) owns columns [16 half, 16 half + 16) of the step in one row.
 // load() issues the raw loads (rows past m read zeros from the end of the
-// range); store() converts to 16 bf16 and the row's scale pair(s).
+// range); store() converts to 16 f16 and the row's scale pair(s).
 enum { QG8_0 = 0, QG4_K = 1, QG5_K = 2, QG6_K = 3 };
 template <int KIND> struct QgFmt;
 
@@ -170,7 +200,7 @@ template <> struct QgFmt<QG8_0> {
     raw.dw = qload(r, blk & ~3);
     raw.sh = blk & 2;
   }
-  // Signed quants as bf16(q): sign-extend, convert, keep the high half.
+  // Signed quants as f16(q).
   __device__ static void store(const Raw& raw, int half, uint32_t (&o)[8], float& s, float& corr, int&) {
     const uint32_t sel = raw.sh ? kPerm0 : kPerm2;  // qs starts 2 bytes into t[0] when the block is 4-aligned
 #pragma unroll
@@ -179,8 +209,8 @@ template <> struct QgFmt<QG8_0> {
       float f[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) f[e] = (float)(int)(int8_t)((u >> (8 * e)) & 0xffu);
-      o[2 * d] = bf16_pair(f[0], f[1]);
-      o[2 * d + 1] = bf16_pair(f[2], f[3]);
+      o[2 * d] = f16_pair(f[0], f[1]);
+      o[2 * d + 1] = f16_pair(f[2], f[3]);
     }
     s = qh_lo(raw.dw >> (raw.sh ? 16 : 0));
     corr = 0.0f;
@@ -296,7 +326,8 @@ template <> struct QgFmt<QG6_K> {
 template <int KIND>
 __device__ __forceinline__ void qgemm_body(const QGemmArgs& a) {
   using F = QgFmt<KIND>;
-  __shared__ __attribute__((aligned(16))) uint16_t s_x[3][kQgTile][kQgLd];
+  __shared__ __attribute__((aligned(16))) uint16_t s_x[2][kQgTile][kQgLd];
+  __shared__ float s_inv[kQgTile];
   __shared__ __attribute__((aligned(16))) uint16_t s_w[kQgTile][kQgLd];
   __shared__ float s_scale[2][2][kQgTile];  // [group][s, corr][row]
   __shared__ __attribute__((aligned(16))) float s_sum[3][kQgTile];  // [group 0, group 1, both][token]
@@ -319,11 +350,11 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& a) {
   const int gpr = a.k >> 4;
 
   typename F::Raw raw;
-  u32x4 xr[6];
+  u32x4 xr[4];
   float2 sr = make_float2(0.0f, 0.0f);
   auto load_step = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 6; ++j) {
+    for (int j = 0; j < 4; ++j) {
       const int c = tid + 256 * j;
       const int piece = c >> 9, token = (c & 511) >> 2, part = c & 3;
       xr[j] = *reinterpret_cast<const u32x4*>(a.planes + piece * plane + (size_t)(tok0 + token) * a.k + k0 + 8 * part);
@@ -333,7 +364,7 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& a) {
   };
   auto store_step = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 6; ++j) {
+    for (int j = 0; j < 4; ++j) {
       const int c = tid + 256 * j;
       const int piece = c >> 9, token = (c & 511) >> 2, part = c & 3;
       *reinterpret_cast<u32x4*>(&s_x[piece][token][8 * part]) = xr[j];
@@ -379,17 +410,17 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) T[tt][rt][i] = 0.0f;
     for (int kh = kh_lo; kh < kh_hi; ++kh) {
-      bf16x8 b[2];
+      f16x8 b[2];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
-        b[rt] = *reinterpret_cast<const bf16x8*>(&s_w[64 * rw + 32 * rt + fl][16 * kh + fk]);
+        b[rt] = *reinterpret_cast<const f16x8*>(&s_w[64 * rw + 32 * rt + fl][16 * kh + fk]);
 #pragma unroll
-      for (int p = 0; p < 3; ++p) {
+      for (int p = 0; p < 2; ++p) {
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
-          const bf16x8 av = *reinterpret_cast<const bf16x8*>(&s_x[p][64 * tw + 32 * tt + fl][16 * kh + fk]);
+          const f16x8 av = *reinterpret_cast<const f16x8*>(&s_x[p][64 * tw + 32 * tt + fl][16 * kh + fk]);
 #pragma unroll
-          for (int rt = 0; rt < 2; ++rt) T[tt][rt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b[rt], T[tt][rt], 0, 0, 0);
+          for (int rt = 0; rt < 2; ++rt) T[tt][rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, b[rt], T[tt][rt], 0, 0, 0);
         }
       }
     }
@@ -418,6 +449,7 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& a) {
   };
 
   const int nks = a.k / 32;
+  if (tid < kQgTile) s_inv[tid] = a.inv_scale[tok0 + tid];
   load_step(0);
   for (int ks = 0; ks < nks; ++ks) {
     __syncthreads();
@@ -443,8 +475,8 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& a) {
       const int row = row0 + 64 * rw + 32 * rt + fl;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int tok = tok0 + 64 * tw + 32 * tt + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (row < a.m && tok < a.B) a.out[(size_t)tok * a.m + row] = acc[tt][rt][i];
+        const int tl = 64 * tw + 32 * tt + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        if (row < a.m && tok0 + tl < a.B) a.out[(size_t)(tok0 + tl) * a.m + row] = acc[tt][rt][i] * s_inv[tl];
       }
     }
 }

@@ -132,6 +132,7 @@ struct XSplitArgs {
   const float* x;
   uint16_t* planes;
   float* sums;
+  float* inv_scale;
   int B;
   int Bp;
   int k;
@@ -141,6 +142,7 @@ struct QGemmArgs {
   const void* w;
   const uint16_t* planes;
   const float* sums;
+  const float* inv_scale;
   float* out;
   unsigned w_bytes;
   int m;
@@ -507,7 +509,8 @@ int launch_gemv(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* 
 }
 
 // Batched quantised matmul launcher: out[B][m] = acts[B][k] . W^T.  The
-// pre-pass splits acts into three bf16 planes and 16-column sums in the
+// pre-pass scales each token by a power of two and splits it into two f16
+// planes, 16-column sums and the token's inverse scale in the
 // context's scratch (grown on demand, after the stream drains); the GEMM
 // then runs one workgroup per 128 tokens x 128 rows.
 int launch_qgemm(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* acts, size_t m, size_t k,
@@ -523,8 +526,8 @@ int launch_qgemm(VtbHipCtx* ctx, int qk, float* out, const void* w, const float*
   if ((uintptr_t)w % 4 != 0) return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: weights not 4-byte aligned");
   if (!aligned16(acts)) return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: activations not 16-byte aligned");
   const size_t Bp = (B + 127) / 128 * 128;
-  const size_t planes_bytes = 3 * Bp * k * 2, sums_bytes = Bp * (k / 16) * 4;
-  const size_t need = planes_bytes + sums_bytes;
+  const size_t planes_bytes = 2 * Bp * k * 2, sums_bytes = Bp * (k / 16) * 4, inv_bytes = Bp * 4;
+  const size_t need = planes_bytes + sums_bytes + inv_bytes;
   if (need > ctx->qg_bytes) {
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     if (ctx->qg) HIP_TRY(ctx, hipFree(ctx->qg), "hipFree");
@@ -535,22 +538,24 @@ int launch_qgemm(VtbHipCtx* ctx, int qk, float* out, const void* w, const float*
   }
   uint16_t* planes = (uint16_t*)ctx->qg;
   float* sums = (float*)((char*)ctx->qg + planes_bytes);
+  float* inv_scale = (float*)((char*)ctx->qg + planes_bytes + sums_bytes);
   XSplitArgs xa;
   memset(&xa, 0, sizeof xa);
   xa.x = acts;
   xa.planes = planes;
   xa.sums = sums;
+  xa.inv_scale = inv_scale;
   xa.B = (int)B;
   xa.Bp = (int)Bp;
   xa.k = (int)k;
-  const size_t groups = Bp * (k / 16);
-  int rc = launch(ctx, ctx->f_xsplit, (unsigned)((groups + 255) / 256), 1, 1, 256, &xa);
+  int rc = launch(ctx, ctx->f_xsplit, (unsigned)Bp, 1, 1, 256, &xa);
   if (rc) return rc;
   QGemmArgs a;
   memset(&a, 0, sizeof a);
   a.w = w;
   a.planes = planes;
   a.sums = sums;
+  a.inv_scale = inv_scale;
   a.out = out;
   // Rounded up to whole dwords: the last 2-byte-aligned field can end two
   // bytes into one (see launch_gemv).
