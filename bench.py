@@ -518,8 +518,9 @@ def main():
     ap.add_argument("--no-gemv", action="store_true", help="skip the quantised GEMV / batched matmul lines")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU; the path's multi-GPU sharding is "
-                                   "design-only (DESIGN.md). Run with --gpus 1."}))
+        print(json.dumps({"error": "this build measures one GPU; how the path would shard across GPUs "
+                                   "is a design only (head-parallel decode/prefill, no exchange inside "
+                                   "attention). Run with --gpus 1."}))
         sys.exit(2)
 
     import torch
