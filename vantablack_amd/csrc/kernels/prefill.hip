@@ -452,9 +452,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   }
 
 // Wide variant (d <= 128): 8 waves x 32 queries share one set of staged
-// K / V^T tiles.  At the same 70 KB of LDS per workgroup two workgroups fit
-// a CU, so 16 waves (4 per SIMD, <= 128 VGPRs) instead of 8, and each staged
-// byte feeds twice the queries.
+// K / V^T tiles.  The body needs ~214 VGPRs, so a CU holds one such
+// workgroup: the same 8 waves (2 per SIMD) as two 4-wave workgroups, with
+// each staged byte feeding twice the queries.
 #define VTB_PREFILL_WIDE(DTN, DTT, D)                                                      \
   extern "C" __global__ __launch_bounds__(512, 2)                                          \
   void vtb_prefill8_##DTN##_d##D(vtb::PrefillArgs a) {                                        \
