@@ -221,6 +221,18 @@ def prefill_flops(L, n_heads, d):
     return 4 * n_heads * d * L * (L + 1) // 2
 
 
+def prefill_kernel_name(torch, n_heads, n_q, d, dt="bf16"):
+    """The attention kernel one attn_prefill call runs, by the launcher's rule
+    (launch_prefill_mfma in vantablack_amd/csrc/vtb_hip.cpp): the 8-wave
+    kernel (256 queries per workgroup, d <= 128) when it still yields at
+    least VTB_PREFILL_WIDE_MIN_WGS workgroups (default two per CU), else the
+    4-wave kernel."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    wide_min = int(os.environ.get("VTB_PREFILL_WIDE_MIN_WGS", 2 * max(cus, 1)))
+    wide = d <= 128 and n_heads * -(-n_q // 256) >= wide_min
+    return f"vtb_prefill{'8' if wide else ''}_{dt}_d{d}"
+
+
 def bench_prefill(ctx, torch, n_heads, n_kv, d, L, reps=5, warmup=2):
     """Causal prefill of L tokens (pos0 = 0), bf16 Q/K/V resident in HBM.
     Returns the average launch time from HIP events on the context stream."""
@@ -254,7 +266,8 @@ def bench_prefill(ctx, torch, n_heads, n_kv, d, L, reps=5, warmup=2):
     for b in (qb, kb, vbuf, ob):
         b.release()
     log(f"prefill h{n_heads}/{n_kv} d{d} L{L}: {t * 1e6:.1f} us/launch -> {fl / t / 1e12:.1f} TFLOP/s")
-    return {"avg_launch_s": t, "flops": fl, "tflops": fl / t / 1e12}
+    return {"avg_launch_s": t, "flops": fl, "tflops": fl / t / 1e12,
+            "kernel": prefill_kernel_name(torch, n_heads, L, d)}
 
 
 QUANT_BLOCK = {"q8_0": (34, 32), "q4_k": (144, 256), "q5_k": (176, 256), "q6_k": (210, 256)}
@@ -414,7 +427,8 @@ def pmc_workload(ctx_rows=8192):
     """One dispatch of each measured kernel shape, for rocprofv3 --pmc runs:
     the calibration copy (vtb_copy_f32), one C2 decode launch at L = ctx+1
     with the KV append fused (vtb_decode_f16_d128_g1), and one C4 prefill of
-    8192 tokens (vtb_vt_bf16_d128 + vtb_prefill_bf16_d128)."""
+    8192 tokens (vtb_vt_bf16_d128 + the attention kernel the launcher picks,
+    vtb_prefill8_bf16_d128 on a 256-CU MI355X)."""
     import numpy as np
     import torch
     import vantablack_amd as vb
@@ -553,7 +567,8 @@ def main():
     ctx.close()
     traffic = load_traffic()
     dec_tr = traffic.get("vtb_decode_f16_d128_g1", {}).get("traffic_bytes")
-    pre_tr = traffic.get("vtb_prefill_bf16_d128", {}).get("traffic_bytes")
+    pre_kernel = pre["C4_L8192"]["kernel"] if pre else None
+    pre_tr = traffic.get(pre_kernel, {}).get("traffic_bytes") if pre_kernel else None
 
     line = {
         "metric": METRIC,
@@ -610,7 +625,9 @@ def main():
             "pct_of_bf16_peak": round(100.0 * p8["tflops"] / BF16_PEAK_TFLOPS, 2),
             "roofline": {"bound": "mfma", "achieved": round(p8["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(p8["tflops"] / BF16_PEAK_TFLOPS, 4), "traffic": pre_tr,
-                         "kernel": "vtb_prefill_bf16_d128", "avg_launch_us": round(p8["avg_launch_s"] * 1e6, 2),
+                         "kernel": pre_kernel, "avg_launch_us": round(p8["avg_launch_s"] * 1e6, 2),
+                         "timed_span": "one attn_prefill call: the V^T pre-pass (vtb_vt_bf16_d128, ~1.5% of "
+                                       "the call) and the attention kernel",
                          "flops_per_launch": p8["flops"]},
             "all": {k: {"tflops": round(v["tflops"], 2), "us": round(v["avg_launch_s"] * 1e6, 2)}
                     for k, v in pre.items()},
