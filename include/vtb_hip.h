@@ -94,6 +94,27 @@ int vtb_hip_segment_commit(VtbHipSeg *seg);
 /* Blocks until all work enqueued on ctx has finished (bridge.h:84-87). */
 int vtb_hip_wait_idle(VtbHipCtx *ctx);
 
+/* The small ops a full-GPU decode layer chains between its matmuls
+ * (gpuLayerStep, src/runtime/forward.zig:419-503), over f32 arrays of n
+ * elements.  Bad ranges are recorded on the segment (commit reports them).
+ *   rmsnorm:      out = in * w * inv, inv = 1/sqrt(sum(in^2)/n + eps), w the
+ *                 f32 weights at weight_offset bytes (out may be in).  Replaces
+ *                 vtb_metal_segment_rmsnorm (bridge.h:115-122); math.rmsNorm
+ *                 (src/kernels/math.zig:11-32).
+ *   swiglu:       gate = gate / (1 + exp(-gate)) * up.  Replaces
+ *                 vtb_metal_segment_swiglu (bridge.h:132-136); math.swiglu
+ *                 (math.zig:154-161).
+ *   gelu_approx:  gate = 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3))) * up.
+ *                 Replaces vtb_metal_segment_gelu_approx (bridge.h:138-143);
+ *                 math.gegluApprox (math.zig:166-175).
+ *   residual_add: a += b.  Replaces vtb_metal_segment_residual_add
+ *                 (bridge.h:145-149); math.addInto. */
+void vtb_hip_segment_rmsnorm(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *in_buf, VtbHipBuf *weight_buf,
+                             size_t weight_offset, size_t n, float eps);
+void vtb_hip_segment_swiglu(VtbHipSeg *seg, VtbHipBuf *gate_buf, VtbHipBuf *up_buf, size_t n);
+void vtb_hip_segment_gelu_approx(VtbHipSeg *seg, VtbHipBuf *gate_buf, VtbHipBuf *up_buf, size_t n);
+void vtb_hip_segment_residual_add(VtbHipSeg *seg, VtbHipBuf *a_buf, VtbHipBuf *b_buf, size_t n);
+
 /* f32 copy, dst[dst_off + i] = src[src_off + i] for i < n_floats.
  * Replaces vtb_metal_segment_copy (bridge.h:148-155). */
 void vtb_hip_segment_copy(VtbHipSeg *seg, VtbHipBuf *dst_buf, size_t dst_offset_bytes,

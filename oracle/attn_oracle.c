@@ -27,6 +27,10 @@
  *                              formula, window invariants
  *   vtb_oracle_attention_f64   independent numpy f64 formula
  *   vtb_oracle_pool_*          pool.zig:196-259 "sums chunks" KAT
+ *   vtb_oracle_rmsnorm         constant-row closed form, scale invariance,
+ *                              f64 formula (tests/test_layer_oracle.py)
+ *   vtb_oracle_swiglu / _geglu_approx  f(0) = 0, f(z) - f(-z) = z (odd
+ *                              sigmoid / tanh parts), f64 formula
  * The one thing no check pins is the ULP-level rounding of Zig's @exp
  * lowering versus glibc expf; the parity tolerances (1e-5 / 2e-3) absorb it.
  */
@@ -138,6 +142,47 @@ void vtb_oracle_rope_half(float *x, size_t head_dim, size_t pos, float base) {
 void vtb_oracle_rope_inv_freq(float *out, size_t head_dim, float base) {
     for (size_t j = 0; j < head_dim / 2; j++)
         out[j] = 1.0f / powf(base, (float)(2 * j) / (float)head_dim);
+}
+
+/* math.zig:11-32 -- math.rmsNorm, in place: the sum of squares in 8 lane
+ * accumulators (Vec) reduced in lane order, then the scalar tail; inv =
+ * 1/sqrt(ss/n + eps); the vector part scales as v*w*inv, the tail as
+ * x*inv*w.  Lane width 8 stands for std.simd.suggestVectorLength(f32) on an
+ * AVX2 host; other widths change only the summation order. */
+void vtb_oracle_rmsnorm(float *x, const float *w, size_t n, float eps) {
+    enum { LANE = 8 };
+    float acc[LANE] = {0};
+    size_t i = 0;
+    for (; i + LANE <= n; i += LANE)
+        for (int l = 0; l < LANE; l++) acc[l] += x[i + l] * x[i + l];
+    float ss = 0.0f;
+    for (int l = 0; l < LANE; l++) ss += acc[l];
+    for (; i < n; i++) ss += x[i] * x[i];
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    i = 0;
+    for (; i + LANE <= n; i += LANE)
+        for (int l = 0; l < LANE; l++) x[i + l] = x[i + l] * w[i + l] * inv;
+    for (; i < n; i++) x[i] = x[i] * inv * w[i];
+}
+
+/* math.zig:154-161 -- math.swiglu: gate = z / (1 + exp(-z)) * up. */
+void vtb_oracle_swiglu(float *gate, const float *up, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        const float z = gate[i];
+        const float silu = z / (1.0f + expf(-z));
+        gate[i] = silu * up[i];
+    }
+}
+
+/* math.zig:166-175 -- math.gegluApprox (tanh-approximate GELU). */
+void vtb_oracle_geglu_approx(float *gate, const float *up, size_t n) {
+    const float sqrt_2_over_pi = 0.7978845608028654f;
+    for (size_t i = 0; i < n; i++) {
+        const float z = gate[i];
+        const float inner = sqrt_2_over_pi * (z + 0.044715f * z * z * z);
+        const float gelu = 0.5f * z * (1.0f + tanhf(inner));
+        gate[i] = gelu * up[i];
+    }
 }
 
 /* math.zig:136-150 -- in-place softmax: max, exp(x-max) with a sequential

@@ -63,6 +63,9 @@ def lib():
         L = ctypes.CDLL(_LIB_PATH)
         P, S, F = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float
         L.vtb_oracle_softmax.argtypes = [P, S]
+        L.vtb_oracle_rmsnorm.argtypes = [P, P, S, F]
+        L.vtb_oracle_swiglu.argtypes = [P, P, S]
+        L.vtb_oracle_geglu_approx.argtypes = [P, P, S]
         L.vtb_oracle_rope.argtypes = [P, S, S, F]
         L.vtb_oracle_quant_block_bytes.argtypes = [ctypes.c_int]
         L.vtb_oracle_quant_block_bytes.restype = S
@@ -196,6 +199,30 @@ def softmax(x: np.ndarray) -> np.ndarray:
     y = np.ascontiguousarray(x, dtype=np.float32).copy()
     lib().vtb_oracle_softmax(_ptr(y), y.size)
     return y
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """math.rmsNorm (src/kernels/math.zig:11-32) of a copy of x."""
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    wf = np.ascontiguousarray(w, dtype=np.float32)
+    lib().vtb_oracle_rmsnorm(_ptr(y), _ptr(wf), y.size, eps)
+    return y
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """math.swiglu (math.zig:154-161): silu(gate) * up, as a new array."""
+    g = np.ascontiguousarray(gate, dtype=np.float32).copy()
+    u = np.ascontiguousarray(up, dtype=np.float32)
+    lib().vtb_oracle_swiglu(_ptr(g), _ptr(u), g.size)
+    return g
+
+
+def geglu_approx(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """math.gegluApprox (math.zig:166-175), as a new array."""
+    g = np.ascontiguousarray(gate, dtype=np.float32).copy()
+    u = np.ascontiguousarray(up, dtype=np.float32)
+    lib().vtb_oracle_geglu_approx(_ptr(g), _ptr(u), g.size)
+    return g
 
 
 def rope(x: np.ndarray, pos: int, base: float, half: bool = False) -> np.ndarray:
@@ -414,3 +441,40 @@ class Pool:
             self.close()
         except Exception:
             pass
+
+
+class LayerWeights:
+    """One decode layer's weights as the layer step uses them: f32 norm
+    weights and GGUF-quantised projection blocks (raw bytes) of one kind."""
+
+    def __init__(self, kind, attn_norm, wq, wk, wv, wo, ffn_norm, wgate, wup, wdown):
+        self.kind = kind
+        self.attn_norm, self.ffn_norm = attn_norm, ffn_norm
+        self.wq, self.wk, self.wv, self.wo = wq, wk, wv, wo
+        self.wgate, self.wup, self.wdown = wgate, wup, wdown
+
+
+def cpu_layer_step(x: np.ndarray, lw: LayerWeights, cache: OracleKvCache, c: ConfigC, layer: int, dim: int,
+                   ffn_dim: int, rms_eps: float, rope_base: float, rope_half: bool = False,
+                   activation: str = "silu") -> np.ndarray:
+    """forward.cpuLayerStep (src/runtime/forward.zig:230-288) for one token at
+    cache.pos, composed from the restatements above; returns the new x (f32)
+    and writes this token's K/V rows into the cache slot."""
+    n_heads, n_kv, hd = c.n_heads, c.n_kv_heads, c.head_dim
+    kv_dim = n_kv * hd
+    xb = rms_norm(x, lw.attn_norm, rms_eps)
+    q = matmul_quant(lw.kind, lw.wq, xb, dim, dim)
+    k = matmul_quant(lw.kind, lw.wk, xb, kv_dim, dim)
+    v = matmul_quant(lw.kind, lw.wv, xb, kv_dim, dim)
+    q = rope(q.reshape(n_heads, hd), cache.pos, rope_base, rope_half).reshape(-1)
+    k = rope(k.reshape(n_kv, hd), cache.pos, rope_base, rope_half).reshape(-1)
+    cache.key_slot(layer)[:] = k
+    cache.value_slot(layer)[:] = v
+    attn = cpu_attention(q, cache, c, layer)
+    x = (x + matmul_quant(lw.kind, lw.wo, attn, dim, dim)).astype(np.float32)
+    xb = rms_norm(x, lw.ffn_norm, rms_eps)
+    gate = matmul_quant(lw.kind, lw.wgate, xb, ffn_dim, dim)
+    up = matmul_quant(lw.kind, lw.wup, xb, ffn_dim, dim)
+    h = swiglu(gate, up) if activation == "silu" else geglu_approx(gate, up)
+    return (x + matmul_quant(lw.kind, lw.wdown, h, dim, ffn_dim)).astype(np.float32)
+

@@ -1,0 +1,196 @@
+"""Full-GPU decode layer through the C ABI: the four layer ops
+(vtb_hip_segment_rmsnorm / swiglu / gelu_approx / residual_add) against the
+oracle's restatements of math.zig, then a small quantised model decoded token
+by token with vantablack_amd.layer (the host side of gpuLayerStep,
+forward.zig:419-503, and gpuFinalStep, :505-511) against oracle.cpu_layer_step
+(cpuLayerStep, forward.zig:230-288), down to the argmax of the logits.
+
+Bars: the ops hold 2e-6 of the largest reference value (residual_add exact);
+the model's residual stream and logits hold 1e-4 of their largest value
+after the layers (f32 throughout, summation orders differ), and the logits'
+argmax agrees unless the reference's top two are within that bar.
+"""
+import numpy as np
+import pytest
+
+from tests.quant import random_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _views(ctx, arr, unaligned):
+    """arr on the device as a Buffer whose base is 16-byte aligned, or 4 bytes
+    past that (a view into a larger allocation); returns (view, backing)."""
+    back = ctx.to_device(np.concatenate([np.zeros(1, np.float32), arr]) if unaligned else arr)
+    if not unaligned:
+        return back, back
+    return ctx.wrap(back.ptr + 4, arr.nbytes, keepalive=back), back
+
+
+@pytest.mark.parametrize("unaligned", [False, True])
+@pytest.mark.parametrize("n", [1, 5, 4096, 5003])
+def test_rmsnorm(ctx, orc, n, unaligned):
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    w = (1 + 0.2 * rng.standard_normal(n)).astype(np.float32)
+    xb, _ = _views(ctx, x, unaligned)
+    wpad = np.concatenate([np.zeros(1 if unaligned else 4, np.float32), w])
+    wb = ctx.to_device(wpad)
+    ob, oback = _views(ctx, np.zeros(n, np.float32), unaligned)
+    with ctx.segment() as seg:
+        seg.rmsnorm(ob, xb, wb, (1 if unaligned else 4) * 4, n, 1e-5)
+    ctx.wait_idle()
+    got = ctx.download(oback, np.float32, n, offset=4 if unaligned else 0)
+    ref = orc.rms_norm(x, w, 1e-5)
+    assert np.max(np.abs(got - ref)) <= 2e-6 * np.max(np.abs(ref))
+
+
+def test_rmsnorm_in_place(ctx, orc):
+    # gpuFinalStep normalises x into itself (forward.zig:507).
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal(4096).astype(np.float32)
+    w = rng.random(4096).astype(np.float32)
+    xb, wb = ctx.to_device(x), ctx.to_device(w)
+    with ctx.segment() as seg:
+        seg.rmsnorm(xb, xb, wb, 0, 4096, 1e-6)
+    got = ctx.download(xb, np.float32, 4096)
+    ref = orc.rms_norm(x, w, 1e-6)
+    assert np.max(np.abs(got - ref)) <= 2e-6 * np.max(np.abs(ref))
+
+
+@pytest.mark.parametrize("unaligned", [False, True])
+@pytest.mark.parametrize("n", [1, 3, 1000, 4099])
+@pytest.mark.parametrize("op", ["swiglu", "gelu_approx", "residual_add"])
+def test_elementwise_ops(ctx, orc, op, n, unaligned):
+    rng = np.random.default_rng(n + len(op))
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    gb, gback = _views(ctx, g, unaligned)
+    ub, _ = _views(ctx, u, unaligned)
+    with ctx.segment() as seg:
+        getattr(seg, op)(gb, ub, n)
+    ctx.wait_idle()
+    got = ctx.download(gback, np.float32, n, offset=4 if unaligned else 0)
+    if op == "residual_add":
+        assert np.array_equal(got, g + u)
+        return
+    ref = orc.swiglu(g, u) if op == "swiglu" else orc.geglu_approx(g, u)
+    assert np.max(np.abs(got - ref)) <= 2e-6 * np.max(np.abs(ref))
+
+
+def test_ops_reject_ranges_beyond_the_buffer(ctx):
+    import vantablack_amd as vb
+    a, b = ctx.alloc(64), ctx.alloc(1024)
+    for call in (lambda s: s.rmsnorm(a, b, b, 0, 32, 1e-5), lambda s: s.rmsnorm(b, b, a, 0, 32, 1e-5),
+                 lambda s: s.swiglu(a, b, 32), lambda s: s.residual_add(b, a, 32)):
+        with pytest.raises(vb.HipError):
+            with ctx.segment() as seg:
+                call(seg)
+
+
+# ---------------------------------------------------------------- model
+
+class TinyModel:
+    """n_layers decode layers, an output norm and a vocab projection, every
+    tensor in one weights buffer at 32-byte aligned offsets (GGUF's default
+    alignment); norm weights f32, projections GGUF blocks."""
+
+    def __init__(self, orc, c, n_layers, vocab, kinds, seed):
+        from vantablack_amd.layer import LayerOffsets
+        rng = np.random.default_rng(seed)
+        parts, pos = [], 0
+
+        def put(arr):
+            nonlocal pos
+            b = np.ascontiguousarray(arr).view(np.uint8).reshape(-1)
+            off = pos
+            parts.append(b)
+            pos += b.size
+            pad = (-pos) % 32
+            if pad:
+                parts.append(np.zeros(pad, np.uint8))
+                pos += pad
+            return off
+
+        kv_dim = c.n_kv_heads * c.head_dim
+        shapes = {"q": (c.dim, c.dim), "k": (kv_dim, c.dim), "v": (kv_dim, c.dim), "o": (c.dim, c.dim),
+                  "gate": (c.ffn_dim, c.dim), "up": (c.ffn_dim, c.dim), "down": (c.dim, c.ffn_dim)}
+        self.offsets, self.oracle_layers = [], []
+        for l in range(n_layers):
+            an = (1 + 0.1 * rng.standard_normal(c.dim)).astype(np.float32)
+            fn = (1 + 0.1 * rng.standard_normal(c.dim)).astype(np.float32)
+            w = {n: random_weights(kinds[n], m, k, seed=seed * 100 + 10 * l + i)
+                 for i, (n, (m, k)) in enumerate(shapes.items())}
+            o = {n: put(w[n]) for n in shapes}
+            self.offsets.append(LayerOffsets(put(an), o["q"], o["k"], o["v"], o["o"], put(fn), o["gate"], o["up"],
+                                             o["down"], kinds["q"], kinds["k"], kinds["v"], kinds["o"],
+                                             kinds["gate"], kinds["up"], kinds["down"]))
+            # One kind per oracle layer (its matmuls take one): the model
+            # uses one kind per layer for the oracle's sake.
+            assert len({kinds[n] for n in shapes}) == 1
+            self.oracle_layers.append(orc.LayerWeights(kinds["q"], an, w["q"], w["k"], w["v"], w["o"], fn,
+                                                       w["gate"], w["up"], w["down"]))
+        self.out_norm = (1 + 0.1 * rng.standard_normal(c.dim)).astype(np.float32)
+        self.out_norm_off = put(self.out_norm)
+        self.out_kind = kinds["out"]
+        self.w_out = random_weights(self.out_kind, vocab, c.dim, seed=seed + 7)
+        self.out_off = put(self.w_out)
+        self.blob = np.concatenate(parts)
+
+
+@pytest.mark.parametrize("variant", ["llama_q4_k", "gemma_like_q6_k_window", "mistral_q8_0_gqa_window"])
+def test_model_decode_matches_cpu_layer_steps(ctx, orc, variant):
+    import vantablack_amd as vb
+    from vantablack_amd.layer import LayerConfig, LayerScratch, gpu_final_step, gpu_layer_step
+    if variant == "llama_q4_k":
+        c = LayerConfig(dim=256, n_heads=4, n_kv_heads=4, head_dim=64, ffn_dim=512, max_seq=16, kv_dtype=vb.F32)
+        kind, n_tok = "q4_k", 5
+    elif variant == "gemma_like_q6_k_window":
+        c = LayerConfig(dim=512, n_heads=2, n_kv_heads=1, head_dim=256, ffn_dim=768, max_seq=16, rms_eps=1e-6,
+                        rope_half=True, activation="gelu_approx", sliding_window=3, kv_dtype=vb.F32)
+        kind, n_tok = "q6_k", 6
+    else:
+        c = LayerConfig(dim=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn_dim=768, max_seq=16,
+                        sliding_window=4, kv_dtype=vb.F32)
+        kind, n_tok = "q8_0", 7
+    n_layers, vocab = 2, 777 if kind != "q4_k" else 768
+    kinds = {n: kind for n in ("q", "k", "v", "o", "gate", "up", "down")}
+    kinds["out"] = "q8_0"
+    m = TinyModel(orc, c, n_layers, vocab, kinds, seed=len(variant))
+    wbuf = ctx.to_device(m.blob)
+    kv_bytes = n_layers * c.max_seq * c.n_kv_heads * c.head_dim * 4
+    kk, kvv = ctx.alloc(kv_bytes), ctx.alloc(kv_bytes)
+    s = LayerScratch(ctx, c, vocab)
+    cache = orc.OracleKvCache(n_layers, c.n_kv_heads, c.head_dim, c.max_seq)
+    oc = orc.config(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq, c.sliding_window)
+    rng = np.random.default_rng(11)
+    try:
+        for pos in range(n_tok):
+            x = rng.standard_normal(c.dim).astype(np.float32)
+            ctx.upload(s.x, x)
+            with ctx.segment() as seg:
+                for l in range(n_layers):
+                    gpu_layer_step(seg, s, wbuf, m.offsets[l], kk, kvv, c, l, pos)
+                gpu_final_step(seg, s, wbuf, m.out_norm_off, m.out_off, m.out_kind, c, vocab)
+            ctx.wait_idle()
+            got_x = ctx.download(s.x, np.float32, c.dim)
+            got_logits = ctx.download(s.logits, np.float32, vocab)
+
+            cache.pos = pos
+            xr = x
+            for l in range(n_layers):
+                xr = orc.cpu_layer_step(xr, m.oracle_layers[l], cache, oc, l, c.dim, c.ffn_dim, c.rms_eps,
+                                        c.rope_base, c.rope_half, c.activation)
+            xr = orc.rms_norm(xr, m.out_norm, c.rms_eps)
+            logits = orc.matmul_quant(m.out_kind, m.w_out, xr, vocab, c.dim)
+
+            assert np.max(np.abs(got_x - xr)) <= 1e-4 * np.max(np.abs(xr)), f"{variant} pos {pos}: x"
+            bar = 1e-4 * np.max(np.abs(logits))
+            assert np.max(np.abs(got_logits - logits)) <= bar, f"{variant} pos {pos}: logits"
+            top2 = np.sort(logits)[-2:]
+            if top2[1] - top2[0] > bar:
+                assert orc.argmax(got_logits) == orc.argmax(logits), f"{variant} pos {pos}: argmax"
+    finally:
+        s.release()
+        for b in (wbuf, kk, kvv):
+            b.release()

@@ -1,0 +1,99 @@
+// The small ops of a decode layer around the projections and attention, as
+// vantablack's full-GPU layer encodes them (gpuLayerStep,
+// src/runtime/forward.zig:419-503; Metal kernels src/metal/bridge.m:88-194):
+//   vtb_rmsnorm_f32       out = in * w * inv, inv = 1 / sqrt(sum(in^2)/n + eps)
+//                         (math.rmsNorm, src/kernels/math.zig:11-32)
+//   vtb_swiglu_f32        gate = gate / (1 + exp(-gate)) * up   (math.zig:154-161)
+//   vtb_gelu_approx_f32   gate = 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3))) * up
+//                         (math.zig:166-175)
+//   vtb_residual_add_f32  a += b                              (math.addInto)
+//
+// rmsnorm is one workgroup: a model row is a few tens of KB (the CPU path
+// stops at dim 8192, forward.zig:646-648), so the launch is latency-bound and
+// a single workgroup avoids a second pass.  Each thread sums the squares of its
+// float4 chunks, the waves reduce by DPP and the 16 wave sums meet in LDS in a
+// fixed order.  The scale is an IEEE square root and division (not the
+// hardware reciprocal square root), as the CPU path computes it.  The
+// elementwise kernels take float4s and finish a ragged tail element by
+// element.
+#include "common.h"
+
+namespace vtb {
+
+struct RmsNormArgs {
+  float* out;
+  const float* in;
+  const float* w;
+  int n;
+  int n4;     // float4 chunks (n / 4 when all three arrays are 16-byte aligned, else 0)
+  float eps;
+  int pad;
+};
+
+struct EltArgs {
+  float* a;        // gate (activations) or the residual target
+  const float* b;  // up, or the residual addend
+  int n;
+  int n4;          // as RmsNormArgs::n4
+};
+
+__device__ inline float silu_mul(float z, float u) { return z / (1.0f + expf(-z)) * u; }
+
+__device__ inline float gelu_approx_mul(float z, float u) {
+  const float inner = 0.7978845608028654f * (z + 0.044715f * z * z * z);
+  return 0.5f * z * (1.0f + tanhf(inner)) * u;
+}
+
+}  // namespace vtb
+
+extern "C" __global__ __launch_bounds__(1024) void vtb_rmsnorm_f32(vtb::RmsNormArgs a) {
+  __shared__ float s_part[16];
+  const int tid = (int)threadIdx.x;
+  const int n4 = a.n4;
+  float ss = 0.0f;
+  for (int c = tid; c < n4; c += 1024) {
+    const float4 v = reinterpret_cast<const float4*>(a.in)[c];
+    ss = fmaf(v.x, v.x, ss);
+    ss = fmaf(v.y, v.y, ss);
+    ss = fmaf(v.z, v.z, ss);
+    ss = fmaf(v.w, v.w, ss);
+  }
+  for (int i = 4 * n4 + tid; i < a.n; i += 1024) ss = fmaf(a.in[i], a.in[i], ss);
+  ss = vtb::group_sum<64>(ss);
+  if ((tid & 63) == 0) s_part[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) tot += s_part[w];
+  const float inv = 1.0f / __builtin_sqrtf(tot / (float)a.n + a.eps);
+  for (int c = tid; c < n4; c += 1024) {
+    const float4 v = reinterpret_cast<const float4*>(a.in)[c];
+    const float4 w = reinterpret_cast<const float4*>(a.w)[c];
+    reinterpret_cast<float4*>(a.out)[c] = make_float4(v.x * w.x * inv, v.y * w.y * inv, v.z * w.z * inv, v.w * w.w * inv);
+  }
+  for (int i = 4 * n4 + tid; i < a.n; i += 1024) a.out[i] = a.in[i] * a.w[i] * inv;
+}
+
+// Elementwise kernels: thread i takes float4 i; the elements past the float4
+// chunks go to the first threads.
+#define VTB_ELT(NAME, EXPR)                                                                  \
+  extern "C" __global__ __launch_bounds__(256) void NAME(vtb::EltArgs a) {                  \
+    const int i = (int)(blockIdx.x * 256 + threadIdx.x);                                     \
+    const int n4 = a.n4;                                                                     \
+    if (i < n4) {                                                                            \
+      float4 x = reinterpret_cast<float4*>(a.a)[i];                                          \
+      const float4 y = reinterpret_cast<const float4*>(a.b)[i];                              \
+      x.x = EXPR(x.x, y.x);                                                                  \
+      x.y = EXPR(x.y, y.y);                                                                  \
+      x.z = EXPR(x.z, y.z);                                                                  \
+      x.w = EXPR(x.w, y.w);                                                                  \
+      reinterpret_cast<float4*>(a.a)[i] = x;                                                 \
+    }                                                                                        \
+    const int t = 4 * n4 + i;                                                                \
+    if (t < a.n) a.a[t] = EXPR(a.a[t], a.b[t]);                                              \
+  }
+
+#define VTB_ADD(x, y) ((x) + (y))
+VTB_ELT(vtb_swiglu_f32, vtb::silu_mul)
+VTB_ELT(vtb_gelu_approx_f32, vtb::gelu_approx_mul)
+VTB_ELT(vtb_residual_add_f32, VTB_ADD)

@@ -27,6 +27,7 @@ extern const unsigned char vtb_blob_prefill[];
 extern const unsigned char vtb_blob_kvcopy[];
 extern const unsigned char vtb_blob_gemv[];
 extern const unsigned char vtb_blob_qgemm[];
+extern const unsigned char vtb_blob_layer[];
 }
 
 namespace {
@@ -168,6 +169,8 @@ struct VtbHipCtx {
   hipFunction_t f_copy = nullptr;
   hipFunction_t f_gemv[kNumQuant][kNumGemvR] = {};  // vtb_gemv_<kind>_r<1|2|4>
   hipFunction_t f_xsplit = nullptr;
+  hipModule_t mod_layer = nullptr;  // rmsnorm, swiglu, gelu_approx, residual_add
+  hipFunction_t f_rmsnorm = nullptr, f_swiglu = nullptr, f_gelu = nullptr, f_resadd = nullptr;
   hipFunction_t f_qgemm[kNumQuant] = {};  // vtb_qgemm_<kind>
   // Split-K workspace and arrival counters (counters are zero between launches).
   void* ws = nullptr;
@@ -616,6 +619,7 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
   ok = ok && hipModuleLoadData(&ctx->mod_kvcopy, vtb_blob_kvcopy) == hipSuccess;
   ok = ok && hipModuleLoadData(&ctx->mod_gemv, vtb_blob_gemv) == hipSuccess;
   ok = ok && hipModuleLoadData(&ctx->mod_qgemm, vtb_blob_qgemm) == hipSuccess;
+  ok = ok && hipModuleLoadData(&ctx->mod_layer, vtb_blob_layer) == hipSuccess;
   char name[96];
   for (int kv = 0; ok && kv < kNumKv; ++kv) {
     for (int di = 0; ok && di < kNumD; ++di) {
@@ -648,6 +652,10 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
       ok = hipModuleGetFunction(&ctx->f_gemv[qk][ri], ctx->mod_gemv, name) == hipSuccess;
     }
   ok = ok && hipModuleGetFunction(&ctx->f_xsplit, ctx->mod_qgemm, "vtb_xsplit") == hipSuccess;
+  ok = ok && hipModuleGetFunction(&ctx->f_rmsnorm, ctx->mod_layer, "vtb_rmsnorm_f32") == hipSuccess;
+  ok = ok && hipModuleGetFunction(&ctx->f_swiglu, ctx->mod_layer, "vtb_swiglu_f32") == hipSuccess;
+  ok = ok && hipModuleGetFunction(&ctx->f_gelu, ctx->mod_layer, "vtb_gelu_approx_f32") == hipSuccess;
+  ok = ok && hipModuleGetFunction(&ctx->f_resadd, ctx->mod_layer, "vtb_residual_add_f32") == hipSuccess;
   for (int qk = 0; ok && qk < kNumQuant; ++qk) {
     snprintf(name, sizeof name, "vtb_qgemm_%s", kQuantNames[qk]);
     ok = hipModuleGetFunction(&ctx->f_qgemm[qk], ctx->mod_qgemm, name) == hipSuccess;
@@ -674,6 +682,7 @@ extern "C" void vtb_hip_destroy(VtbHipCtx* ctx) {
   if (ctx->mod_kvcopy) (void)hipModuleUnload(ctx->mod_kvcopy);
   if (ctx->mod_gemv) (void)hipModuleUnload(ctx->mod_gemv);
   if (ctx->mod_qgemm) (void)hipModuleUnload(ctx->mod_qgemm);
+  if (ctx->mod_layer) (void)hipModuleUnload(ctx->mod_layer);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -770,6 +779,71 @@ extern "C" void vtb_hip_segment_copy(VtbHipSeg* seg, VtbHipBuf* dst_buf, size_t 
   CopyArgs a{(float*)bptr(dst_buf, dst_offset_bytes), (const float*)bptr(src_buf, src_offset_bytes),
              (long long)n_floats};
   seg_note(seg, launch(ctx, ctx->f_copy, (unsigned)((n_floats + 255) / 256), 1, 1, 256, &a));
+}
+
+// Layer ops around the projections (kernels/layer.hip): the Metal bridge's
+// segment encoders rmsnorm / swiglu / gelu_approx / residual_add
+// (src/metal/bridge.h:115-150), which gpuLayerStep (forward.zig:419-503)
+// chains between its matmuls.  f32 arrays of n elements; float4 access when
+// every array is 16-byte aligned, element access otherwise.
+struct RmsNormArgs {
+  float* out;
+  const float* in;
+  const float* w;
+  int n;
+  int n4;
+  float eps;
+  int pad;
+};
+struct EltArgs {
+  float* a;
+  const float* b;
+  int n;
+  int n4;
+};
+
+extern "C" void vtb_hip_segment_rmsnorm(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* in_buf, VtbHipBuf* weight_buf,
+                                        size_t weight_offset, size_t n, float eps) {
+  if (!seg) return;
+  VtbHipCtx* ctx = seg->ctx;
+  if (n == 0) return;
+  if (n > 0x7fffffff / 4 || weight_offset % 4 || !buf_ok(out_buf, 0, n * 4) || !buf_ok(in_buf, 0, n * 4) ||
+      !buf_ok(weight_buf, weight_offset, n * 4))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "rmsnorm: bad range"));
+  RmsNormArgs a;
+  memset(&a, 0, sizeof a);
+  a.out = (float*)bptr(out_buf, 0);
+  a.in = (const float*)bptr(in_buf, 0);
+  a.w = (const float*)bptr(weight_buf, weight_offset);
+  a.n = (int)n;
+  a.n4 = (aligned16(a.out) && aligned16(a.in) && aligned16(a.w)) ? (int)(n / 4) : 0;
+  a.eps = eps;
+  seg_note(seg, launch(ctx, ctx->f_rmsnorm, 1, 1, 1, 1024, &a));
+}
+
+static void seg_elementwise(VtbHipSeg* seg, hipFunction_t f, const char* what, VtbHipBuf* a_buf, VtbHipBuf* b_buf,
+                            size_t n) {
+  if (!seg) return;
+  VtbHipCtx* ctx = seg->ctx;
+  if (n == 0) return;
+  if (n > 0x7fffffff / 4 || !buf_ok(a_buf, 0, n * 4) || !buf_ok(b_buf, 0, n * 4))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, what));
+  EltArgs a{(float*)bptr(a_buf, 0), (const float*)bptr(b_buf, 0), (int)n, 0};
+  a.n4 = (aligned16(a.a) && aligned16(a.b)) ? (int)(n / 4) : 0;
+  const size_t threads = std::max((size_t)a.n4, n - 4 * (size_t)a.n4);
+  seg_note(seg, launch(ctx, f, (unsigned)((threads + 255) / 256), 1, 1, 256, &a));
+}
+
+extern "C" void vtb_hip_segment_swiglu(VtbHipSeg* seg, VtbHipBuf* gate_buf, VtbHipBuf* up_buf, size_t n) {
+  seg_elementwise(seg, seg ? seg->ctx->f_swiglu : nullptr, "swiglu: bad range", gate_buf, up_buf, n);
+}
+
+extern "C" void vtb_hip_segment_gelu_approx(VtbHipSeg* seg, VtbHipBuf* gate_buf, VtbHipBuf* up_buf, size_t n) {
+  seg_elementwise(seg, seg ? seg->ctx->f_gelu : nullptr, "gelu_approx: bad range", gate_buf, up_buf, n);
+}
+
+extern "C" void vtb_hip_segment_residual_add(VtbHipSeg* seg, VtbHipBuf* a_buf, VtbHipBuf* b_buf, size_t n) {
+  seg_elementwise(seg, seg ? seg->ctx->f_resadd : nullptr, "residual_add: bad range", a_buf, b_buf, n);
 }
 
 extern "C" void vtb_hip_segment_kv_append(VtbHipSeg* seg, VtbHipBuf* kv_buf, size_t slot_offset_bytes,

@@ -82,6 +82,10 @@ SIGNATURES = {
     "vtb_hip_segment_commit": ([_P], _I),
     "vtb_hip_wait_idle": ([_P], _I),
     "vtb_hip_segment_copy": ([_P, _P, _S, _P, _S, _S], None),
+    "vtb_hip_segment_rmsnorm": ([_P, _P, _P, _P, _S, _S, _F], None),
+    "vtb_hip_segment_swiglu": ([_P, _P, _P, _S], None),
+    "vtb_hip_segment_gelu_approx": ([_P, _P, _P, _S], None),
+    "vtb_hip_segment_residual_add": ([_P, _P, _P, _S], None),
     "vtb_hip_segment_kv_append": ([_P, _P, _S, _I, _P, _S, _S], None),
     "vtb_hip_segment_attn_decode": ([_P, _P, _P, _P, _S, _P, _S, _S, _S, _S, _S, _F, _I], None),
     "vtb_hip_segment_attn_decode_append": ([_P, _P, _P, _P, _S, _P, _S, _P, _P, _S, _S, _S, _S, _F, _I], None),
@@ -210,6 +214,20 @@ class Segment:
 
     def copy(self, dst: Buffer, dst_off: int, src: Buffer, src_off: int, n_floats: int):
         lib().vtb_hip_segment_copy(self.h, dst.h, dst_off, src.h, src_off, n_floats)
+
+    def rmsnorm(self, out: Buffer, inp: Buffer, weight: Buffer, weight_off: int, n: int, eps: float):
+        """out = rmsnorm(inp) * weight (f32 weights at byte offset weight_off);
+        seg.rmsnorm of gpuLayerStep (forward.zig:440)."""
+        lib().vtb_hip_segment_rmsnorm(self.h, out.h, inp.h, weight.h, weight_off, n, eps)
+
+    def swiglu(self, gate: Buffer, up: Buffer, n: int):
+        lib().vtb_hip_segment_swiglu(self.h, gate.h, up.h, n)
+
+    def gelu_approx(self, gate: Buffer, up: Buffer, n: int):
+        lib().vtb_hip_segment_gelu_approx(self.h, gate.h, up.h, n)
+
+    def residual_add(self, a: Buffer, b: Buffer, n: int):
+        lib().vtb_hip_segment_residual_add(self.h, a.h, b.h, n)
 
     def kv_append(self, kv: Buffer, slot_off_bytes: int, kv_dtype: int, src: Buffer, src_off: int, n: int):
         lib().vtb_hip_segment_kv_append(self.h, kv.h, slot_off_bytes, kv_dtype, src.h, src_off, n)

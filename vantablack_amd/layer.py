@@ -1,0 +1,144 @@
+"""Full-GPU decode layer: the host side of vantablack's gpuLayerStep
+(src/runtime/forward.zig:419-503) and gpuFinalStep (:505-511), composed from
+this library's segment ops.  Per layer and token, on one segment:
+
+  rmsnorm(xb <- x)                          vtb_hip_segment_rmsnorm
+  q, k_cur, v_cur = Wq xb, Wk xb, Wv xb     vtb_hip_segment_matmul_<kind>
+  RoPE(q, k_cur) + K/V slot write +         vtb_hip_segment_attn_decode_rope_append
+    decode attention (one launch)           (the reference's rope x2, copy x2
+                                            and three attention kernels)
+  xb2 = Wo attn_out; x += xb2               matmul, vtb_hip_segment_residual_add
+  rmsnorm(xb <- x); gate, up = Wg xb, Wu xb
+  gate = swiglu(gate, up) | gelu_approx     vtb_hip_segment_swiglu / _gelu_approx
+  ffn_out = Wd gate; x += ffn_out
+
+The sliding window is the reference's caller-side offset shift
+(forward.zig:470-480): the K/V base moves to the window's first row and the
+attended length shrinks, and the append lands at row pos either way.  The
+weights live in one device buffer at per-tensor byte offsets, as the
+reference's weightsBuf()/weightOffset() addresses them (norm weights f32,
+projections GGUF-quantised).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+from . import hip
+
+NO_WINDOW = hip.NO_WINDOW
+KV_BYTES = {hip.F32: 4, hip.F16: 2, hip.BF16: 2}
+
+
+@dataclass
+class LayerConfig:
+    """The LlamaConfig fields a decode layer reads (src/runtime/model.zig:40-70)."""
+    dim: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    ffn_dim: int
+    max_seq: int
+    rms_eps: float = 1e-5
+    rope_base: float = 10000.0
+    rope_half: bool = False
+    activation: str = "silu"          # or "gelu_approx" (Gemma)
+    sliding_window: int = NO_WINDOW
+    kv_dtype: int = hip.F16
+
+
+@dataclass
+class LayerOffsets:
+    """Byte offsets of one layer's tensors in the weights buffer and the
+    quant kind of each projection."""
+    attn_norm: int
+    wq: int
+    wk: int
+    wv: int
+    wo: int
+    ffn_norm: int
+    wgate: int
+    wup: int
+    wdown: int
+    kind_q: str
+    kind_k: str
+    kind_v: str
+    kind_o: str
+    kind_gate: str
+    kind_up: str
+    kind_down: str
+
+
+class LayerScratch:
+    """The device activations the layer steps through (MetalBackend's x, xb,
+    xb2, q, k_cur, v_cur, attn_out, gate, up, ffn_out, logits)."""
+
+    def __init__(self, ctx, c: LayerConfig, vocab_size: int = 0):
+        kv_dim = c.n_kv_heads * c.head_dim
+        q_dim = c.n_heads * c.head_dim
+        self.x = ctx.alloc(c.dim * 4)
+        self.xb = ctx.alloc(max(c.dim, q_dim) * 4)
+        self.xb2 = ctx.alloc(c.dim * 4)
+        self.q = ctx.alloc(q_dim * 4)
+        self.k_cur = ctx.alloc(kv_dim * 4)
+        self.v_cur = ctx.alloc(kv_dim * 4)
+        self.attn_out = ctx.alloc(q_dim * 4)
+        self.gate = ctx.alloc(c.ffn_dim * 4)
+        self.up = ctx.alloc(c.ffn_dim * 4)
+        self.ffn_out = ctx.alloc(c.dim * 4)
+        self.logits = ctx.alloc(vocab_size * 4) if vocab_size else None
+
+    def release(self):
+        for b in (self.x, self.xb, self.xb2, self.q, self.k_cur, self.v_cur, self.attn_out, self.gate, self.up,
+                  self.ffn_out, self.logits):
+            if b is not None:
+                b.release()
+
+
+def gpu_layer_step(seg, s: LayerScratch, weights, off: LayerOffsets, kv_k, kv_v, c: LayerConfig, layer: int,
+                   pos: int):
+    """One decode layer for the token at position pos (cache rows [0, pos)
+    already hold the earlier tokens); updates s.x in place and writes row pos
+    of this layer's K/V slab.  kv_k / kv_v are layer-major caches of
+    c.kv_dtype, [n_layers][max_seq][n_kv_heads][head_dim]."""
+    if c.n_heads * c.head_dim != c.dim:
+        raise ValueError("gpu_layer_step: n_heads * head_dim must equal dim (as forward.zig:440-502 assumes)")
+    if pos >= c.max_seq:
+        raise ValueError("gpu_layer_step: position beyond max_seq")
+    kv_dim = c.n_kv_heads * c.head_dim
+    eb = KV_BYTES[c.kv_dtype]
+    row_bytes = kv_dim * eb
+    layer_off = layer * c.max_seq * row_bytes
+    wstart = 0 if (c.sliding_window == NO_WINDOW or pos < c.sliding_window) else pos - c.sliding_window + 1
+    attended = pos + 1 - wstart
+    win_off = layer_off + wstart * row_bytes
+
+    seg.rmsnorm(s.xb, s.x, weights, off.attn_norm, c.dim, c.rms_eps)
+    seg.matmul_quant(off.kind_q, s.q, weights, off.wq, s.xb, c.dim, c.dim)
+    seg.matmul_quant(off.kind_k, s.k_cur, weights, off.wk, s.xb, kv_dim, c.dim)
+    seg.matmul_quant(off.kind_v, s.v_cur, weights, off.wv, s.xb, kv_dim, c.dim)
+    seg.attn_decode_rope_append(s.attn_out, s.q, kv_k, win_off, kv_v, win_off, s.k_cur, s.v_cur, c.n_heads,
+                                c.n_kv_heads, c.head_dim, attended, 1.0 / math.sqrt(c.head_dim), c.kv_dtype, pos,
+                                c.rope_base, c.rope_half)
+    seg.matmul_quant(off.kind_o, s.xb2, weights, off.wo, s.attn_out, c.dim, c.dim)
+    seg.residual_add(s.x, s.xb2, c.dim)
+
+    seg.rmsnorm(s.xb, s.x, weights, off.ffn_norm, c.dim, c.rms_eps)
+    seg.matmul_quant(off.kind_gate, s.gate, weights, off.wgate, s.xb, c.ffn_dim, c.dim)
+    seg.matmul_quant(off.kind_up, s.up, weights, off.wup, s.xb, c.ffn_dim, c.dim)
+    if c.activation == "silu":
+        seg.swiglu(s.gate, s.up, c.ffn_dim)
+    elif c.activation == "gelu_approx":
+        seg.gelu_approx(s.gate, s.up, c.ffn_dim)
+    else:
+        raise ValueError(f"unknown activation {c.activation!r}")
+    seg.matmul_quant(off.kind_down, s.ffn_out, weights, off.wdown, s.gate, c.dim, c.ffn_dim)
+    seg.residual_add(s.x, s.ffn_out, c.dim)
+
+
+def gpu_final_step(seg, s: LayerScratch, weights, output_norm_off: int, output_off: int, output_kind: str,
+                   c: LayerConfig, vocab_size: int):
+    """gpuFinalStep (forward.zig:505-511): x = rmsnorm(x) in place, then the
+    logits projection into s.logits."""
+    seg.rmsnorm(s.x, s.x, weights, output_norm_off, c.dim, c.rms_eps)
+    seg.matmul_quant(output_kind, s.logits, weights, output_off, s.x, vocab_size, c.dim)
