@@ -389,6 +389,99 @@ def bench_qgemm_layer(ctx, torch, kind, n_tokens, reps=3):
     return res
 
 
+def bench_full_decode(ctx, torch, ctx_rows=8192, steps=6, warmup=2):
+    """Whole-token decode of a Llama-2-7B-shaped model on the GPU, as
+    vantablack's gpuLayerStep x 32 + gpuFinalStep encode it
+    (forward.zig:419-511), through vantablack_amd.layer: per layer rmsnorm,
+    Q/K/V GEMVs, RoPE + K/V append + attention (one launch), O GEMV, residual,
+    rmsnorm, gate/up GEMVs, SwiGLU, down GEMV, residual; then the output norm
+    and the 32000-row logits GEMV.  Q4_K projections (random blocks with small
+    f16 scales), f32 norm weights, f16 KV cache holding ctx_rows rows.
+    Returns ms per token from HIP events on the context stream."""
+    import numpy as np
+    from vantablack_amd import layer as ly
+    dim, nh, nkv, hd, ffn, n_layers, vocab = 4096, 32, 32, 128, 11008, 32, 32000
+    c = ly.LayerConfig(dim=dim, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn_dim=ffn,
+                       max_seq=ctx_rows + warmup + steps, kv_dtype=1)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(77)
+    qb, qe = QUANT_BLOCK["q4_k"]
+    scale = torch.tensor([0.01], dtype=torch.float16, device=dev).view(torch.uint8)
+
+    def q4k(m, k):
+        w = torch.randint(0, 256, (m * k // qe, qb), generator=g, dtype=torch.uint8, device=dev)
+        w[:, 0:2] = scale
+        w[:, 2:4] = scale
+        return w.reshape(-1)
+
+    shapes = [("q", dim, dim), ("k", nkv * hd, dim), ("v", nkv * hd, dim), ("o", dim, dim),
+              ("gate", ffn, dim), ("up", ffn, dim), ("down", dim, ffn)]
+    tensors, offs, pos = [], [], 0
+
+    def put(t):
+        nonlocal pos
+        off = pos
+        tensors.append(t)
+        pos += t.numel()
+        return off
+
+    norm = torch.ones(dim, dtype=torch.float32, device=dev).view(torch.uint8)
+    for _ in range(n_layers):
+        an = put(norm)
+        o = {n: put(q4k(m, k)) for n, m, k in shapes}
+        fn = put(norm)
+        offs.append(ly.LayerOffsets(an, o["q"], o["k"], o["v"], o["o"], fn, o["gate"], o["up"], o["down"],
+                                    *(["q4_k"] * 7)))
+    out_norm_off = put(norm)
+    out_off = put(q4k(vocab, dim))
+    blob = torch.cat(tensors)
+    del tensors
+    weight_bytes = blob.numel()
+    kc = torch.empty((n_layers, c.max_seq, nkv, hd), dtype=torch.float16, device=dev)
+    vc = torch.empty_like(kc)
+    kc.normal_(generator=g)
+    vc.normal_(generator=g)
+    torch.cuda.synchronize()
+    wb, kb, vb_ = ctx.wrap_tensor(blob), ctx.wrap_tensor(kc), ctx.wrap_tensor(vc)
+    s = ly.LayerScratch(ctx, c, vocab)
+    ctx.upload(s.x, np.zeros(dim, np.float32) + np.float32(0.1))
+
+    def token(seg, p):
+        for l in range(n_layers):
+            ly.gpu_layer_step(seg, s, wb, offs[l], kb, vb_, c, l, p)
+        ly.gpu_final_step(seg, s, wb, out_norm_off, out_off, "q4_k", c, vocab)
+
+    with ctx.segment() as seg:
+        for t in range(warmup):
+            token(seg, ctx_rows + t)
+    ctx.wait_idle()
+    stream = torch.cuda.ExternalStream(ctx.stream)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    with ctx.segment() as seg:
+        for t in range(steps):
+            token(seg, ctx_rows + warmup + t)
+    e1.record(stream)
+    ctx.wait_idle()
+    torch.cuda.synchronize()
+    t_tok = e0.elapsed_time(e1) * 1e-3 / steps
+    L_mid = ctx_rows + warmup + steps // 2
+    kv_bytes = n_layers * decode_bytes(L_mid, nh, nkv, hd, 2)
+    s.release()
+    for b in (wb, kb, vb_):
+        b.release()
+    del blob, kc, vc
+    torch.cuda.empty_cache()
+    log(f"full decode: {t_tok * 1e3:.3f} ms/token ({1 / t_tok:.1f} tok/s), "
+        f"{(weight_bytes + kv_bytes) / t_tok / 1e9:.0f} GB/s over weights + KV")
+    return {"ms_per_token": round(t_tok * 1e3, 3), "tok_per_s": round(1 / t_tok, 1),
+            "launches_per_token": n_layers * 13 + 2, "weight_bytes": weight_bytes,
+            "kv_bytes_per_token": kv_bytes,
+            "hbm_gbs": round((weight_bytes + kv_bytes) / t_tok / 1e9, 1),
+            "pct_of_hbm_peak": round(100.0 * (weight_bytes + kv_bytes) / t_tok / 1e9 / HBM_PEAK_GBS, 1)}
+
+
 def cpu_baseline(seconds_budget=18.0):
     """Time the CPU oracle on a bounded sample of the decode workload: one
     C2 layer at L=8192 (f32 values of the f16 cache, as vantablack's f32
@@ -565,6 +658,8 @@ def main():
                                        for kind in ("q4_k", "q5_k", "q6_k", "q8_0")}
     # matmulBatched (the prefill projections) at the C4 prompt length.
     qgemm = None if args.no_gemv else bench_qgemm_layer(ctx, torch, "q4_k", 8192)
+    # The whole token: every layer on the GPU (gpuLayerStep x 32 + gpuFinalStep).
+    full = None if args.no_gemv else bench_full_decode(ctx, torch, ctx_rows=args.ctx)
     cpu = None if args.no_cpu else cpu_baseline()
     ctx.close()
     traffic = load_traffic()
@@ -611,6 +706,11 @@ def main():
                         "f32 activations; weights cycled over >= 512 MB so each launch reads HBM",
             **gemv,
         }
+    if full:
+        line["full_decode"] = dict(
+            workload="Llama-2-7B shapes, 32 layers + output norm and 32000-row logits, Q4_K projections, "
+                     f"f16 KV at ctx {args.ctx}, one token per step; every op on the GPU",
+            **full)
     if qgemm:
         line["prefill_projections"] = {
             "workload": "Llama-3-8B layer projections (q,o 4096x4096; k,v 1024x4096; gate,up 14336x4096; "
