@@ -114,6 +114,14 @@ void vtb_hip_segment_rmsnorm(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *in_b
 void vtb_hip_segment_swiglu(VtbHipSeg *seg, VtbHipBuf *gate_buf, VtbHipBuf *up_buf, size_t n);
 void vtb_hip_segment_gelu_approx(VtbHipSeg *seg, VtbHipBuf *gate_buf, VtbHipBuf *up_buf, size_t n);
 void vtb_hip_segment_residual_add(VtbHipSeg *seg, VtbHipBuf *a_buf, VtbHipBuf *b_buf, size_t n);
+/* x += b, then out = rmsnorm(x) * w (out may be x): the residual add and the
+ * rmsnorm that follows it in gpuLayerStep (forward.zig:488-489 and 502, each
+ * followed by an rmsnorm of x at :489 / the next layer's :440, or
+ * gpuFinalStep's :507) in one launch, with the same arithmetic as the two
+ * encoders above.  No counterpart in the Metal bridge: a fusion of
+ * vtb_metal_segment_residual_add and vtb_metal_segment_rmsnorm. */
+void vtb_hip_segment_residual_add_rmsnorm(VtbHipSeg *seg, VtbHipBuf *x_buf, VtbHipBuf *b_buf, VtbHipBuf *out_buf,
+                                          VtbHipBuf *weight_buf, size_t weight_offset, size_t n, float eps);
 
 /* f32 copy, dst[dst_off + i] = src[src_off + i] for i < n_floats.
  * Replaces vtb_metal_segment_copy (bridge.h:148-155). */

@@ -78,6 +78,30 @@ def test_elementwise_ops(ctx, orc, op, n, unaligned):
     assert np.max(np.abs(got - ref)) <= 2e-6 * np.max(np.abs(ref))
 
 
+@pytest.mark.parametrize("in_place", [False, True])
+@pytest.mark.parametrize("unaligned", [False, True])
+@pytest.mark.parametrize("n", [3, 4096, 5003])
+def test_residual_add_rmsnorm(ctx, orc, n, unaligned, in_place):
+    # x += b, then out = rmsnorm(x) * w: the two ops back to back, in one launch.
+    rng = np.random.default_rng(n + 17)
+    x = rng.standard_normal(n).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    w = (1 + 0.2 * rng.standard_normal(n)).astype(np.float32)
+    xv, xback = _views(ctx, x, unaligned)
+    bv, _ = _views(ctx, b, unaligned)
+    wb = ctx.to_device(w)
+    ov, oback = (xv, xback) if in_place else _views(ctx, np.zeros(n, np.float32), unaligned)
+    with ctx.segment() as seg:
+        seg.residual_add_rmsnorm(xv, bv, ov, wb, 0, n, 1e-5)
+    ctx.wait_idle()
+    off = 4 if unaligned else 0
+    ref = orc.rms_norm(x + b, w, 1e-5)
+    got = ctx.download(oback, np.float32, n, offset=off)
+    assert np.max(np.abs(got - ref)) <= 2e-6 * np.max(np.abs(ref))
+    if not in_place:
+        assert np.array_equal(ctx.download(xback, np.float32, n, offset=off), x + b)
+
+
 def test_ops_reject_ranges_beyond_the_buffer(ctx):
     import vantablack_amd as vb
     a, b = ctx.alloc(64), ctx.alloc(1024)
@@ -138,10 +162,14 @@ class TinyModel:
         self.blob = np.concatenate(parts)
 
 
+@pytest.mark.parametrize("path", ["layer_steps", "token_step"])
 @pytest.mark.parametrize("variant", ["llama_q4_k", "gemma_like_q6_k_window", "mistral_q8_0_gqa_window"])
-def test_model_decode_matches_cpu_layer_steps(ctx, orc, variant):
+def test_model_decode_matches_cpu_layer_steps(ctx, orc, variant, path):
+    """path layer_steps: gpu_layer_step per layer + gpu_final_step (the
+    reference's encoder sequence); token_step: gpu_token_step (residual adds
+    fused into the following rmsnorm)."""
     import vantablack_amd as vb
-    from vantablack_amd.layer import LayerConfig, LayerScratch, gpu_final_step, gpu_layer_step
+    from vantablack_amd.layer import LayerConfig, LayerScratch, gpu_final_step, gpu_layer_step, gpu_token_step
     if variant == "llama_q4_k":
         c = LayerConfig(dim=256, n_heads=4, n_kv_heads=4, head_dim=64, ffn_dim=512, max_seq=16, kv_dtype=vb.F32)
         kind, n_tok = "q4_k", 5
@@ -169,9 +197,13 @@ def test_model_decode_matches_cpu_layer_steps(ctx, orc, variant):
             x = rng.standard_normal(c.dim).astype(np.float32)
             ctx.upload(s.x, x)
             with ctx.segment() as seg:
-                for l in range(n_layers):
-                    gpu_layer_step(seg, s, wbuf, m.offsets[l], kk, kvv, c, l, pos)
-                gpu_final_step(seg, s, wbuf, m.out_norm_off, m.out_off, m.out_kind, c, vocab)
+                if path == "token_step":
+                    gpu_token_step(seg, s, wbuf, m.offsets, kk, kvv, c, pos, m.out_norm_off, m.out_off, m.out_kind,
+                                   vocab)
+                else:
+                    for l in range(n_layers):
+                        gpu_layer_step(seg, s, wbuf, m.offsets[l], kk, kvv, c, l, pos)
+                    gpu_final_step(seg, s, wbuf, m.out_norm_off, m.out_off, m.out_kind, c, vocab)
             ctx.wait_idle()
             got_x = ctx.download(s.x, np.float32, c.dim)
             got_logits = ctx.download(s.logits, np.float32, vocab)

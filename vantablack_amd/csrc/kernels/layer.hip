@@ -7,6 +7,10 @@
 //   vtb_gelu_approx_f32   gate = 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3))) * up
 //                         (math.zig:166-175)
 //   vtb_residual_add_f32  a += b                              (math.addInto)
+//   vtb_add_rmsnorm_f32   x += b, then out = rmsnorm(x) * w: the residual add
+//                         and the rmsnorm that follows it in the layer
+//                         (forward.zig:488-489, 502 then the next layer's 440),
+//                         one launch instead of two, same arithmetic
 //
 // rmsnorm is one workgroup: a model row is a few tens of KB (the CPU path
 // stops at dim 8192, forward.zig:646-648), so the launch is latency-bound and
@@ -26,6 +30,17 @@ struct RmsNormArgs {
   const float* w;
   int n;
   int n4;     // float4 chunks (n / 4 when all three arrays are 16-byte aligned, else 0)
+  float eps;
+  int pad;
+};
+
+struct AddNormArgs {
+  float* x;        // residual stream, updated in place
+  const float* b;  // addend
+  float* out;      // normalised output (may be x)
+  const float* w;
+  int n;
+  int n4;          // float4 chunks when all four arrays are 16-byte aligned, else 0
   float eps;
   int pad;
 };
@@ -72,6 +87,43 @@ extern "C" __global__ __launch_bounds__(1024) void vtb_rmsnorm_f32(vtb::RmsNormA
     reinterpret_cast<float4*>(a.out)[c] = make_float4(v.x * w.x * inv, v.y * w.y * inv, v.z * w.z * inv, v.w * w.w * inv);
   }
   for (int i = 4 * n4 + tid; i < a.n; i += 1024) a.out[i] = a.in[i] * a.w[i] * inv;
+}
+
+// x += b (stored), then the rmsnorm of the new x into out.  Each thread
+// re-reads in the second pass exactly the elements it wrote in the first.
+extern "C" __global__ __launch_bounds__(1024) void vtb_add_rmsnorm_f32(vtb::AddNormArgs a) {
+  __shared__ float s_part[16];
+  const int tid = (int)threadIdx.x;
+  const int n4 = a.n4;
+  float ss = 0.0f;
+  for (int c = tid; c < n4; c += 1024) {
+    float4 v = reinterpret_cast<const float4*>(a.x)[c];
+    const float4 d = reinterpret_cast<const float4*>(a.b)[c];
+    v = make_float4(v.x + d.x, v.y + d.y, v.z + d.z, v.w + d.w);
+    reinterpret_cast<float4*>(a.x)[c] = v;
+    ss = fmaf(v.x, v.x, ss);
+    ss = fmaf(v.y, v.y, ss);
+    ss = fmaf(v.z, v.z, ss);
+    ss = fmaf(v.w, v.w, ss);
+  }
+  for (int i = 4 * n4 + tid; i < a.n; i += 1024) {
+    const float v = a.x[i] + a.b[i];
+    a.x[i] = v;
+    ss = fmaf(v, v, ss);
+  }
+  ss = vtb::group_sum<64>(ss);
+  if ((tid & 63) == 0) s_part[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) tot += s_part[w];
+  const float inv = 1.0f / __builtin_sqrtf(tot / (float)a.n + a.eps);
+  for (int c = tid; c < n4; c += 1024) {
+    const float4 v = reinterpret_cast<const float4*>(a.x)[c];
+    const float4 w = reinterpret_cast<const float4*>(a.w)[c];
+    reinterpret_cast<float4*>(a.out)[c] = make_float4(v.x * w.x * inv, v.y * w.y * inv, v.z * w.z * inv, v.w * w.w * inv);
+  }
+  for (int i = 4 * n4 + tid; i < a.n; i += 1024) a.out[i] = a.x[i] * a.w[i] * inv;
 }
 
 // Elementwise kernels: thread i takes float4 i; the elements past the float4

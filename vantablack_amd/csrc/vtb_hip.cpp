@@ -170,7 +170,7 @@ struct VtbHipCtx {
   hipFunction_t f_gemv[kNumQuant][kNumGemvR] = {};  // vtb_gemv_<kind>_r<1|2|4>
   hipFunction_t f_xsplit = nullptr;
   hipModule_t mod_layer = nullptr;  // rmsnorm, swiglu, gelu_approx, residual_add
-  hipFunction_t f_rmsnorm = nullptr, f_swiglu = nullptr, f_gelu = nullptr, f_resadd = nullptr;
+  hipFunction_t f_rmsnorm = nullptr, f_swiglu = nullptr, f_gelu = nullptr, f_resadd = nullptr, f_addnorm = nullptr;
   hipFunction_t f_qgemm[kNumQuant] = {};  // vtb_qgemm_<kind>
   // Split-K workspace and arrival counters (counters are zero between launches).
   void* ws = nullptr;
@@ -656,6 +656,7 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
   ok = ok && hipModuleGetFunction(&ctx->f_swiglu, ctx->mod_layer, "vtb_swiglu_f32") == hipSuccess;
   ok = ok && hipModuleGetFunction(&ctx->f_gelu, ctx->mod_layer, "vtb_gelu_approx_f32") == hipSuccess;
   ok = ok && hipModuleGetFunction(&ctx->f_resadd, ctx->mod_layer, "vtb_residual_add_f32") == hipSuccess;
+  ok = ok && hipModuleGetFunction(&ctx->f_addnorm, ctx->mod_layer, "vtb_add_rmsnorm_f32") == hipSuccess;
   for (int qk = 0; ok && qk < kNumQuant; ++qk) {
     snprintf(name, sizeof name, "vtb_qgemm_%s", kQuantNames[qk]);
     ok = hipModuleGetFunction(&ctx->f_qgemm[qk], ctx->mod_qgemm, name) == hipSuccess;
@@ -819,6 +820,38 @@ extern "C" void vtb_hip_segment_rmsnorm(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbH
   a.n4 = (aligned16(a.out) && aligned16(a.in) && aligned16(a.w)) ? (int)(n / 4) : 0;
   a.eps = eps;
   seg_note(seg, launch(ctx, ctx->f_rmsnorm, 1, 1, 1, 1024, &a));
+}
+
+struct AddNormArgs {
+  float* x;
+  const float* b;
+  float* out;
+  const float* w;
+  int n;
+  int n4;
+  float eps;
+  int pad;
+};
+
+extern "C" void vtb_hip_segment_residual_add_rmsnorm(VtbHipSeg* seg, VtbHipBuf* x_buf, VtbHipBuf* b_buf,
+                                                     VtbHipBuf* out_buf, VtbHipBuf* weight_buf,
+                                                     size_t weight_offset, size_t n, float eps) {
+  if (!seg) return;
+  VtbHipCtx* ctx = seg->ctx;
+  if (n == 0) return;
+  if (n > 0x7fffffff / 4 || weight_offset % 4 || !buf_ok(x_buf, 0, n * 4) || !buf_ok(b_buf, 0, n * 4) ||
+      !buf_ok(out_buf, 0, n * 4) || !buf_ok(weight_buf, weight_offset, n * 4))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "residual_add_rmsnorm: bad range"));
+  AddNormArgs a;
+  memset(&a, 0, sizeof a);
+  a.x = (float*)bptr(x_buf, 0);
+  a.b = (const float*)bptr(b_buf, 0);
+  a.out = (float*)bptr(out_buf, 0);
+  a.w = (const float*)bptr(weight_buf, weight_offset);
+  a.n = (int)n;
+  a.n4 = (aligned16(a.x) && aligned16(a.b) && aligned16(a.out) && aligned16(a.w)) ? (int)(n / 4) : 0;
+  a.eps = eps;
+  seg_note(seg, launch(ctx, ctx->f_addnorm, 1, 1, 1, 1024, &a));
 }
 
 static void seg_elementwise(VtbHipSeg* seg, hipFunction_t f, const char* what, VtbHipBuf* a_buf, VtbHipBuf* b_buf,

@@ -86,6 +86,7 @@ SIGNATURES = {
     "vtb_hip_segment_swiglu": ([_P, _P, _P, _S], None),
     "vtb_hip_segment_gelu_approx": ([_P, _P, _P, _S], None),
     "vtb_hip_segment_residual_add": ([_P, _P, _P, _S], None),
+    "vtb_hip_segment_residual_add_rmsnorm": ([_P, _P, _P, _P, _P, _S, _S, _F], None),
     "vtb_hip_segment_kv_append": ([_P, _P, _S, _I, _P, _S, _S], None),
     "vtb_hip_segment_attn_decode": ([_P, _P, _P, _P, _S, _P, _S, _S, _S, _S, _S, _F, _I], None),
     "vtb_hip_segment_attn_decode_append": ([_P, _P, _P, _P, _S, _P, _S, _P, _P, _S, _S, _S, _S, _F, _I], None),
@@ -228,6 +229,11 @@ class Segment:
 
     def residual_add(self, a: Buffer, b: Buffer, n: int):
         lib().vtb_hip_segment_residual_add(self.h, a.h, b.h, n)
+
+    def residual_add_rmsnorm(self, x: Buffer, b: Buffer, out: Buffer, weight: Buffer, weight_off: int, n: int,
+                             eps: float):
+        """x += b, then out = rmsnorm(x) * weight, in one launch."""
+        lib().vtb_hip_segment_residual_add_rmsnorm(self.h, x.h, b.h, out.h, weight.h, weight_off, n, eps)
 
     def kv_append(self, kv: Buffer, slot_off_bytes: int, kv_dtype: int, src: Buffer, src_off: int, n: int):
         lib().vtb_hip_segment_kv_append(self.h, kv.h, slot_off_bytes, kv_dtype, src.h, src_off, n)

@@ -12,6 +12,11 @@ this library's segment ops.  Per layer and token, on one segment:
   gate = swiglu(gate, up) | gelu_approx     vtb_hip_segment_swiglu / _gelu_approx
   ffn_out = Wd gate; x += ffn_out
 
+gpu_token_step runs a whole token (every layer, then the final step) with
+each residual add fused into the rmsnorm that follows it
+(vtb_hip_segment_residual_add_rmsnorm): 11 launches per layer instead of 13,
+the same arithmetic.
+
 The sliding window is the reference's caller-side offset shift
 (forward.zig:470-480): the K/V base moves to the window's first row and the
 attended length shrinks, and the append lands at row pos either way.  The
@@ -95,35 +100,30 @@ class LayerScratch:
                 b.release()
 
 
-def gpu_layer_step(seg, s: LayerScratch, weights, off: LayerOffsets, kv_k, kv_v, c: LayerConfig, layer: int,
-                   pos: int):
-    """One decode layer for the token at position pos (cache rows [0, pos)
-    already hold the earlier tokens); updates s.x in place and writes row pos
-    of this layer's K/V slab.  kv_k / kv_v are layer-major caches of
-    c.kv_dtype, [n_layers][max_seq][n_kv_heads][head_dim]."""
+def _check(c: LayerConfig, pos: int):
     if c.n_heads * c.head_dim != c.dim:
-        raise ValueError("gpu_layer_step: n_heads * head_dim must equal dim (as forward.zig:440-502 assumes)")
+        raise ValueError("n_heads * head_dim must equal dim (as forward.zig:440-502 assumes)")
     if pos >= c.max_seq:
-        raise ValueError("gpu_layer_step: position beyond max_seq")
+        raise ValueError("position beyond max_seq")
+
+
+def _attention(seg, s, weights, off, kv_k, kv_v, c, layer, pos):
+    """Q/K/V GEMVs, then RoPE + K/V slot write + attention in one launch."""
     kv_dim = c.n_kv_heads * c.head_dim
-    eb = KV_BYTES[c.kv_dtype]
-    row_bytes = kv_dim * eb
+    row_bytes = kv_dim * KV_BYTES[c.kv_dtype]
     layer_off = layer * c.max_seq * row_bytes
     wstart = 0 if (c.sliding_window == NO_WINDOW or pos < c.sliding_window) else pos - c.sliding_window + 1
-    attended = pos + 1 - wstart
     win_off = layer_off + wstart * row_bytes
-
-    seg.rmsnorm(s.xb, s.x, weights, off.attn_norm, c.dim, c.rms_eps)
     seg.matmul_quant(off.kind_q, s.q, weights, off.wq, s.xb, c.dim, c.dim)
     seg.matmul_quant(off.kind_k, s.k_cur, weights, off.wk, s.xb, kv_dim, c.dim)
     seg.matmul_quant(off.kind_v, s.v_cur, weights, off.wv, s.xb, kv_dim, c.dim)
     seg.attn_decode_rope_append(s.attn_out, s.q, kv_k, win_off, kv_v, win_off, s.k_cur, s.v_cur, c.n_heads,
-                                c.n_kv_heads, c.head_dim, attended, 1.0 / math.sqrt(c.head_dim), c.kv_dtype, pos,
-                                c.rope_base, c.rope_half)
-    seg.matmul_quant(off.kind_o, s.xb2, weights, off.wo, s.attn_out, c.dim, c.dim)
-    seg.residual_add(s.x, s.xb2, c.dim)
+                                c.n_kv_heads, c.head_dim, pos + 1 - wstart, 1.0 / math.sqrt(c.head_dim),
+                                c.kv_dtype, pos, c.rope_base, c.rope_half)
 
-    seg.rmsnorm(s.xb, s.x, weights, off.ffn_norm, c.dim, c.rms_eps)
+
+def _ffn(seg, s, weights, off, c):
+    """gate/up GEMVs, the gated activation, the down GEMV into s.ffn_out."""
     seg.matmul_quant(off.kind_gate, s.gate, weights, off.wgate, s.xb, c.ffn_dim, c.dim)
     seg.matmul_quant(off.kind_up, s.up, weights, off.wup, s.xb, c.ffn_dim, c.dim)
     if c.activation == "silu":
@@ -133,6 +133,43 @@ def gpu_layer_step(seg, s: LayerScratch, weights, off: LayerOffsets, kv_k, kv_v,
     else:
         raise ValueError(f"unknown activation {c.activation!r}")
     seg.matmul_quant(off.kind_down, s.ffn_out, weights, off.wdown, s.gate, c.dim, c.ffn_dim)
+
+
+def gpu_token_step(seg, s: LayerScratch, weights, offs, kv_k, kv_v, c: LayerConfig, pos: int,
+                   output_norm_off: int, output_off: int, output_kind: str, vocab_size: int):
+    """Every layer in offs, then gpuFinalStep, for the token at pos (s.x holds
+    its embedding); leaves the normalised x in s.x and the logits in s.logits.
+    Each residual add runs fused with the rmsnorm after it."""
+    _check(c, pos)
+    for layer, off in enumerate(offs):
+        if layer == 0:
+            seg.rmsnorm(s.xb, s.x, weights, off.attn_norm, c.dim, c.rms_eps)
+        else:
+            seg.residual_add_rmsnorm(s.x, s.ffn_out, s.xb, weights, off.attn_norm, c.dim, c.rms_eps)
+        _attention(seg, s, weights, off, kv_k, kv_v, c, layer, pos)
+        seg.matmul_quant(off.kind_o, s.xb2, weights, off.wo, s.attn_out, c.dim, c.dim)
+        seg.residual_add_rmsnorm(s.x, s.xb2, s.xb, weights, off.ffn_norm, c.dim, c.rms_eps)
+        _ffn(seg, s, weights, off, c)
+    if offs:
+        seg.residual_add_rmsnorm(s.x, s.ffn_out, s.x, weights, output_norm_off, c.dim, c.rms_eps)
+    else:
+        seg.rmsnorm(s.x, s.x, weights, output_norm_off, c.dim, c.rms_eps)
+    seg.matmul_quant(output_kind, s.logits, weights, output_off, s.x, vocab_size, c.dim)
+
+
+def gpu_layer_step(seg, s: LayerScratch, weights, off: LayerOffsets, kv_k, kv_v, c: LayerConfig, layer: int,
+                   pos: int):
+    """One decode layer for the token at position pos (cache rows [0, pos)
+    already hold the earlier tokens); updates s.x in place and writes row pos
+    of this layer's K/V slab.  kv_k / kv_v are layer-major caches of
+    c.kv_dtype, [n_layers][max_seq][n_kv_heads][head_dim]."""
+    _check(c, pos)
+    seg.rmsnorm(s.xb, s.x, weights, off.attn_norm, c.dim, c.rms_eps)
+    _attention(seg, s, weights, off, kv_k, kv_v, c, layer, pos)
+    seg.matmul_quant(off.kind_o, s.xb2, weights, off.wo, s.attn_out, c.dim, c.dim)
+    seg.residual_add(s.x, s.xb2, c.dim)
+    seg.rmsnorm(s.xb, s.x, weights, off.ffn_norm, c.dim, c.rms_eps)
+    _ffn(seg, s, weights, off, c)
     seg.residual_add(s.x, s.ffn_out, c.dim)
 
 
