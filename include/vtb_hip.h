@@ -94,8 +94,28 @@ int vtb_hip_segment_commit(VtbHipSeg *seg);
 /* Blocks until all work enqueued on ctx has finished (bridge.h:84-87). */
 int vtb_hip_wait_idle(VtbHipCtx *ctx);
 
+/* Two or three quantised GEMVs of one format over the same activations in one
+ * launch: out_b[i] = W_b[i,:] . acts for the m_b rows of W_b at w_off_b in
+ * w_buf (b = 0, 1, 2; m2 = 0 for two).  For the Q/K/V and gate/up
+ * projections, which the reference encodes as separate segMatmulQuant calls
+ * on one input (forward.zig:459-461, 502-503) or as one call on a fused
+ * [Q|K|V] / [gate|up] tensor followed by copies (:443-457, :492-500).  No
+ * Metal counterpart: each block is exactly vtb_hip_segment_matmul_<kind>. */
+void vtb_hip_segment_matmul3_q8_0(VtbHipSeg *seg, VtbHipBuf *out0, size_t w_off0, size_t m0, VtbHipBuf *out1,
+                                  size_t w_off1, size_t m1, VtbHipBuf *out2, size_t w_off2, size_t m2,
+                                  VtbHipBuf *w_buf, VtbHipBuf *acts_buf, size_t k);
+void vtb_hip_segment_matmul3_q4_k(VtbHipSeg *seg, VtbHipBuf *out0, size_t w_off0, size_t m0, VtbHipBuf *out1,
+                                  size_t w_off1, size_t m1, VtbHipBuf *out2, size_t w_off2, size_t m2,
+                                  VtbHipBuf *w_buf, VtbHipBuf *acts_buf, size_t k);
+void vtb_hip_segment_matmul3_q5_k(VtbHipSeg *seg, VtbHipBuf *out0, size_t w_off0, size_t m0, VtbHipBuf *out1,
+                                  size_t w_off1, size_t m1, VtbHipBuf *out2, size_t w_off2, size_t m2,
+                                  VtbHipBuf *w_buf, VtbHipBuf *acts_buf, size_t k);
+void vtb_hip_segment_matmul3_q6_k(VtbHipSeg *seg, VtbHipBuf *out0, size_t w_off0, size_t m0, VtbHipBuf *out1,
+                                  size_t w_off1, size_t m1, VtbHipBuf *out2, size_t w_off2, size_t m2,
+                                  VtbHipBuf *w_buf, VtbHipBuf *acts_buf, size_t k);
+
 /* The small ops a full-GPU decode layer chains between its matmuls
- * (gpuLayerStep, src/runtime/forward.zig:419-503), over f32 arrays of n
+ * (gpuLayerStep, src/runtime/forward.zig:419-513), over f32 arrays of n
  * elements.  Bad ranges are recorded on the segment (commit reports them).
  *   rmsnorm:      out = in * w * inv, inv = 1/sqrt(sum(in^2)/n + eps), w the
  *                 f32 weights at weight_offset bytes (out may be in).  Replaces
@@ -115,9 +135,9 @@ void vtb_hip_segment_swiglu(VtbHipSeg *seg, VtbHipBuf *gate_buf, VtbHipBuf *up_b
 void vtb_hip_segment_gelu_approx(VtbHipSeg *seg, VtbHipBuf *gate_buf, VtbHipBuf *up_buf, size_t n);
 void vtb_hip_segment_residual_add(VtbHipSeg *seg, VtbHipBuf *a_buf, VtbHipBuf *b_buf, size_t n);
 /* x += b, then out = rmsnorm(x) * w (out may be x): the residual add and the
- * rmsnorm that follows it in gpuLayerStep (forward.zig:488-489 and 502, each
- * followed by an rmsnorm of x at :489 / the next layer's :440, or
- * gpuFinalStep's :507) in one launch, with the same arithmetic as the two
+ * rmsnorm that follows it in gpuLayerStep (forward.zig:487 and 510, each
+ * followed by an rmsnorm of x at :490 / the next layer's :441, or
+ * gpuFinalStep's :517) in one launch, with the same arithmetic as the two
  * encoders above.  No counterpart in the Metal bridge: a fusion of
  * vtb_metal_segment_residual_add and vtb_metal_segment_rmsnorm. */
 void vtb_hip_segment_residual_add_rmsnorm(VtbHipSeg *seg, VtbHipBuf *x_buf, VtbHipBuf *b_buf, VtbHipBuf *out_buf,

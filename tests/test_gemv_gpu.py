@@ -90,3 +90,32 @@ def test_synchronous_entry(ctx, orc):
     got = ctx.download(ob, np.float32, m)
     ref = orc.matmul_quant(kind, w, x, m, k)
     assert np.max(np.abs(got - ref)) <= 1e-4 * np.max(np.abs(ref))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("ms", [(4096, 1024, 1024), (11008, 11008), (13, 1000, 257)])
+def test_grouped_row_blocks_match_single_gemvs(ctx, orc, kind, ms):
+    """vtb_hip_segment_matmul3_<kind>: two or three row blocks (their own
+    weights and outputs, one activation vector) in one launch, each to the
+    per-row bar of the single GEMV; block sizes not multiples of the rows per
+    workgroup included."""
+    k = 1024 if kind == "q8_0" else 2048
+    rng = np.random.default_rng(sum(ms))
+    x = ((rng.random(k, dtype=np.float32) - 0.5) * 2.0).astype(np.float32)
+    ws = [random_weights(kind, m, k, seed=m + i) for i, m in enumerate(ms)]
+    offs, pos = [], 0
+    for w in ws:
+        offs.append(pos)
+        pos += (w.size + 31) // 32 * 32
+    blob = np.zeros(pos, np.uint8)
+    for w, o in zip(ws, offs):
+        blob[o:o + w.size] = w
+    wb, xb = ctx.to_device(blob), ctx.to_device(x)
+    outs = [ctx.alloc(m * 4) for m in ms]
+    with ctx.segment() as seg:
+        seg.matmul3(kind, wb, xb, k, [(o, off, m) for o, off, m in zip(outs, offs, ms)])
+    for w, o, m in zip(ws, outs, ms):
+        got = ctx.download(o, np.float32, m).astype(np.float64)
+        ref = orc.matmul_quant(kind, w, x, m, k).astype(np.float64)
+        cond = np.abs(np_dequant(kind, w).astype(np.float64).reshape(m, k)) @ np.abs(x.astype(np.float64))
+        assert np.all(np.abs(got - ref) <= 1e-5 * cond), f"{kind} block m{m}"

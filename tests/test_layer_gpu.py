@@ -2,7 +2,7 @@
 (vtb_hip_segment_rmsnorm / swiglu / gelu_approx / residual_add) against the
 oracle's restatements of math.zig, then a small quantised model decoded token
 by token with vantablack_amd.layer (the host side of gpuLayerStep,
-forward.zig:419-503, and gpuFinalStep, :505-511) against oracle.cpu_layer_step
+forward.zig:419-513, and gpuFinalStep, :515-520) against oracle.cpu_layer_step
 (cpuLayerStep, forward.zig:230-288), down to the argmax of the logits.
 
 Bars: the ops hold 2e-6 of the largest reference value (residual_add exact);
@@ -46,7 +46,7 @@ def test_rmsnorm(ctx, orc, n, unaligned):
 
 
 def test_rmsnorm_in_place(ctx, orc):
-    # gpuFinalStep normalises x into itself (forward.zig:507).
+    # gpuFinalStep normalises x into itself (forward.zig:517).
     rng = np.random.default_rng(9)
     x = rng.standard_normal(4096).astype(np.float32)
     w = rng.random(4096).astype(np.float32)

@@ -58,6 +58,19 @@ struct GemvArgs {
   int m;
   int k;
   int row_bytes;
+  // Up to two more row blocks of the same format sharing x (the Q/K/V or
+  // gate/up projections of one layer): workgroups [wg1, wg2) compute block 1
+  // and [wg2, grid) block 2, each with its own weights, output and rows.
+  int nblk;           // 1, 2 or 3
+  int wg1, wg2;
+  const uint8_t* w1;
+  float* out1;
+  unsigned w_bytes1;
+  int m1;
+  const uint8_t* w2;
+  float* out2;
+  unsigned w_bytes2;
+  int m2;
 };
 
 // Activation staging: 8 rows of 64 lanes + kGemvXPad float4 per wave, in
@@ -335,10 +348,21 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nw = (int)(blockDim.x >> 6);
-  const int row0 = (int)blockIdx.x * R;
+  // This workgroup's row block (wave-uniform selects).
+  int wg = (int)blockIdx.x;
+  const uint8_t* wp = a.w;
+  float* outp = a.out;
+  unsigned wbytes = a.w_bytes;
+  int m = a.m;
+  if (a.nblk > 2 && wg >= a.wg2) {
+    wp = a.w2, outp = a.out2, wbytes = a.w_bytes2, m = a.m2, wg -= a.wg2;
+  } else if (a.nblk > 1 && wg >= a.wg1) {
+    wp = a.w1, outp = a.out1, wbytes = a.w_bytes1, m = a.m1, wg -= a.wg1;
+  }
+  const int row0 = wg * R;
   const int c0 = wave * 2048;  // the wave's slice
   const int c = lane & 7;      // lane within its block (K-quants)
-  const auto rsrc = buffer_rsrc(a.w, a.w_bytes);
+  const auto rsrc = buffer_rsrc(wp, wbytes);
   const auto xrsrc = buffer_rsrc(a.x, 4u * (unsigned)a.k);
   const bool active = c0 + F::first(lane) < a.k;
 
@@ -359,7 +383,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
   const int boff = F::block(lane, c0) * F::BB;
 #pragma unroll
   for (int i = 0; i < R; ++i)
-    F::load(rsrc, active && row0 + i < a.m ? (row0 + i) * a.row_bytes + boff : (int)a.w_bytes, c, raw[i]);
+    F::load(rsrc, active && row0 + i < m ? (row0 + i) * a.row_bytes + boff : (int)wbytes, c, raw[i]);
 
   // Hand each float4 to its owner lane through this wave's LDS rows.  LDS
   // operations of one wave execute in order, so the reads below see every
@@ -396,10 +420,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
     if (lane == 0) s_part[wave][i] = t;
   }
   __syncthreads();
-  if ((int)threadIdx.x < R && row0 + (int)threadIdx.x < a.m) {
+  if ((int)threadIdx.x < R && row0 + (int)threadIdx.x < m) {
     float t = 0.0f;
     for (int w = 0; w < nw; ++w) t += s_part[w][threadIdx.x];
-    a.out[row0 + threadIdx.x] = t;
+    outp[row0 + threadIdx.x] = t;
   }
 }
 

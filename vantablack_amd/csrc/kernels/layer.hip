@@ -1,6 +1,6 @@
 // The small ops of a decode layer around the projections and attention, as
 // vantablack's full-GPU layer encodes them (gpuLayerStep,
-// src/runtime/forward.zig:419-503; Metal kernels src/metal/bridge.m:88-194):
+// src/runtime/forward.zig:419-513; Metal kernels src/metal/bridge.m:88-194):
 //   vtb_rmsnorm_f32       out = in * w * inv, inv = 1 / sqrt(sum(in^2)/n + eps)
 //                         (math.rmsNorm, src/kernels/math.zig:11-32)
 //   vtb_swiglu_f32        gate = gate / (1 + exp(-gate)) * up   (math.zig:154-161)
@@ -9,7 +9,7 @@
 //   vtb_residual_add_f32  a += b                              (math.addInto)
 //   vtb_add_rmsnorm_f32   x += b, then out = rmsnorm(x) * w: the residual add
 //                         and the rmsnorm that follows it in the layer
-//                         (forward.zig:488-489, 502 then the next layer's 440),
+//                         (forward.zig:487 and 490, 510 then the next layer's 441),
 //                         one launch instead of two, same arithmetic
 //
 // rmsnorm is one workgroup: a model row is a few tens of KB (the CPU path

@@ -126,6 +126,16 @@ struct GemvArgs {
   int m;
   int k;
   int row_bytes;
+  int nblk;
+  int wg1, wg2;
+  const void* w1;
+  float* out1;
+  unsigned w_bytes1;
+  int m1;
+  const void* w2;
+  float* out2;
+  unsigned w_bytes2;
+  int m2;
 };
 
 // Mirrors vtb::XSplitArgs / vtb::QGemmArgs (kernels/qgemm.hip).
@@ -468,16 +478,25 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const void* q, const void* k
 // 4 where it still gives two workgroups per CU, except for Q6_K with k above
 // 8192 (R = 4: 15.3 us, R = 2: 14.4 us for 4096 x 11008), else 2, else 1;
 // VTB_GEMV_R overrides.
-int launch_gemv(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* x, size_t m, size_t k) {
+// Up to three row blocks of one format sharing x go in one launch
+// (launch_gemv_blocks); R is chosen on the total rows.
+int launch_gemv_blocks(VtbHipCtx* ctx, int qk, int nblk, float* const outs[], const void* const ws[],
+                       const size_t ms[], const float* x, size_t k) {
   if (qk < 0 || qk >= kNumQuant) return set_err(ctx, VTB_HIP_EINVAL, "bad quant kind");
-  if (m == 0 || k == 0 || k % kQuantBlockElems[qk] != 0)
+  if (nblk < 1 || nblk > 3) return set_err(ctx, VTB_HIP_EINVAL, "matmul: 1 to 3 row blocks");
+  if (k == 0 || k % kQuantBlockElems[qk] != 0)
     return set_err(ctx, VTB_HIP_EINVAL, "matmul: k must be a positive multiple of the block size");
   if (k > 16 * 2048) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul: k above 32768");
   const size_t row_bytes = k / kQuantBlockElems[qk] * kQuantBlockBytes[qk];
-  // Offsets stay below 2^31 with room for one block past the end, where
-  // the kernel points the loads of rows past m.
-  if (m > 0x7fff0000 / row_bytes) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul: weights beyond 2 GiB");
-  if ((uintptr_t)w % 4 != 0) return set_err(ctx, VTB_HIP_EINVAL, "matmul: weights not 4-byte aligned");
+  size_t m = 0;
+  for (int b = 0; b < nblk; ++b) {
+    if (ms[b] == 0) return set_err(ctx, VTB_HIP_EINVAL, "matmul: empty row block");
+    // Offsets stay below 2^31 with room for one block past the end, where
+    // the kernel points the loads of rows past m.
+    if (ms[b] > 0x7fff0000 / row_bytes) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul: weights beyond 2 GiB");
+    if ((uintptr_t)ws[b] % 4 != 0) return set_err(ctx, VTB_HIP_EINVAL, "matmul: weights not 4-byte aligned");
+    m += ms[b];
+  }
   if (!aligned16(x)) return set_err(ctx, VTB_HIP_EINVAL, "matmul: activations not 16-byte aligned");
   int ri = 0;
   const long long forced = env_int("VTB_GEMV_R", 0);
@@ -490,25 +509,45 @@ int launch_gemv(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* 
       break;
     }
   }
-  GemvArgs a;
-  memset(&a, 0, sizeof a);
-  a.w = w;
-  a.x = x;
-  a.out = out;
+  const size_t R = (size_t)kGemvRs[ri];
   // The range is rounded up to whole dwords: a raw buffer load returns zero
   // for a dword only partly in range, and the last field of a 34- or
   // 210-byte block can end two bytes into one.  With the base 4-byte
   // aligned that dword lies in the page holding the tensor's last bytes.
-  a.w_bytes = (unsigned)((m * row_bytes + 3) & ~(size_t)3);
-  a.m = (int)m;
+  auto wbytes = [&](size_t rows) { return (unsigned)((rows * row_bytes + 3) & ~(size_t)3); };
+  GemvArgs a;
+  memset(&a, 0, sizeof a);
+  a.w = ws[0];
+  a.x = x;
+  a.out = outs[0];
+  a.w_bytes = wbytes(ms[0]);
+  a.m = (int)ms[0];
   a.k = (int)k;
   a.row_bytes = (int)row_bytes;
+  a.nblk = nblk;
+  size_t grid = (ms[0] + R - 1) / R;
+  if (nblk > 1) {
+    a.wg1 = (int)grid;
+    a.w1 = ws[1], a.out1 = outs[1], a.w_bytes1 = wbytes(ms[1]), a.m1 = (int)ms[1];
+    grid += (ms[1] + R - 1) / R;
+  }
+  if (nblk > 2) {
+    a.wg2 = (int)grid;
+    a.w2 = ws[2], a.out2 = outs[2], a.w_bytes2 = wbytes(ms[2]), a.m2 = (int)ms[2];
+    grid += (ms[2] + R - 1) / R;
+  }
   const unsigned waves = (unsigned)((k + 2047) / 2048);
-  const size_t R = (size_t)kGemvRs[ri];
   // Per wave the kernel stages its 2048 activations as 8 rows of (64 + 4)
   // float4 in dynamic LDS.
   const unsigned lds = waves * 8u * (64u + 4u) * 16u;
-  return launch(ctx, ctx->f_gemv[qk][ri], (unsigned)((m + R - 1) / R), 1, 1, 64 * waves, &a, lds);
+  return launch(ctx, ctx->f_gemv[qk][ri], (unsigned)grid, 1, 1, 64 * waves, &a, lds);
+}
+
+int launch_gemv(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* x, size_t m, size_t k) {
+  float* const outs[1] = {out};
+  const void* const ws[1] = {w};
+  const size_t ms[1] = {m};
+  return launch_gemv_blocks(ctx, qk, 1, outs, ws, ms, x, k);
 }
 
 // Batched quantised matmul launcher: out[B][m] = acts[B][k] . W^T.  The
@@ -784,7 +823,7 @@ extern "C" void vtb_hip_segment_copy(VtbHipSeg* seg, VtbHipBuf* dst_buf, size_t 
 
 // Layer ops around the projections (kernels/layer.hip): the Metal bridge's
 // segment encoders rmsnorm / swiglu / gelu_approx / residual_add
-// (src/metal/bridge.h:115-150), which gpuLayerStep (forward.zig:419-503)
+// (src/metal/bridge.h:115-150), which gpuLayerStep (forward.zig:419-513)
 // chains between its matmuls.  f32 arrays of n elements; float4 access when
 // every array is 16-byte aligned, element access otherwise.
 struct RmsNormArgs {
@@ -1054,6 +1093,46 @@ VTB_MATMUL_ENTRIES(q8_0, 0)
 VTB_MATMUL_ENTRIES(q4_k, 1)
 VTB_MATMUL_ENTRIES(q5_k, 2)
 VTB_MATMUL_ENTRIES(q6_k, 3)
+
+// Two or three GEMVs of one format over the same activations in one launch
+// (m2 = 0: two).
+static int matmul3_entry(VtbHipCtx* ctx, int qk, VtbHipBuf* out0, size_t w_off0, size_t m0, VtbHipBuf* out1,
+                         size_t w_off1, size_t m1, VtbHipBuf* out2, size_t w_off2, size_t m2, VtbHipBuf* w_buf,
+                         VtbHipBuf* acts_buf, size_t k) {
+  if (!ctx || !out0 || !out1 || !w_buf || !acts_buf || (m2 && !out2)) return VTB_HIP_EINVAL;
+  if (m0 == 0 || m1 == 0 || k == 0 || k % kQuantBlockElems[qk] != 0 || m0 > ((size_t)1 << 31) ||
+      m1 > ((size_t)1 << 31) || m2 > ((size_t)1 << 31) || k > ((size_t)1 << 31))
+    return set_err(ctx, VTB_HIP_EINVAL, "matmul3: bad shape");
+  const size_t row_bytes = k / kQuantBlockElems[qk] * kQuantBlockBytes[qk];
+  VtbHipBuf* outs_b[3] = {out0, out1, out2};
+  const size_t offs[3] = {w_off0, w_off1, w_off2}, ms[3] = {m0, m1, m2};
+  const int nblk = m2 ? 3 : 2;
+  float* outs[3] = {nullptr, nullptr, nullptr};
+  const void* ws[3] = {nullptr, nullptr, nullptr};
+  if (!buf_ok(acts_buf, 0, k * 4)) return set_err(ctx, VTB_HIP_EINVAL, "matmul3: buffer too small");
+  for (int b = 0; b < nblk; ++b) {
+    if (!buf_ok(w_buf, offs[b], ms[b] * row_bytes) || !buf_ok(outs_b[b], 0, ms[b] * 4))
+      return set_err(ctx, VTB_HIP_EINVAL, "matmul3: buffer too small");
+    outs[b] = (float*)outs_b[b]->ptr;
+    ws[b] = bptr(w_buf, offs[b]);
+  }
+  return launch_gemv_blocks(ctx, qk, nblk, outs, ws, ms, (const float*)acts_buf->ptr, k);
+}
+
+#define VTB_MATMUL3_ENTRY(NAME, QK)                                                                        \
+  extern "C" void vtb_hip_segment_matmul3_##NAME(VtbHipSeg* seg, VtbHipBuf* out0, size_t w_off0, size_t m0, \
+                                                 VtbHipBuf* out1, size_t w_off1, size_t m1, VtbHipBuf* out2, \
+                                                 size_t w_off2, size_t m2, VtbHipBuf* w_buf,                 \
+                                                 VtbHipBuf* acts_buf, size_t k) {                            \
+    if (!seg) return;                                                                                     \
+    seg_note(seg, matmul3_entry(seg->ctx, QK, out0, w_off0, m0, out1, w_off1, m1, out2, w_off2, m2, w_buf,  \
+                                acts_buf, k));                                                            \
+  }
+
+VTB_MATMUL3_ENTRY(q8_0, 0)
+VTB_MATMUL3_ENTRY(q4_k, 1)
+VTB_MATMUL3_ENTRY(q5_k, 2)
+VTB_MATMUL3_ENTRY(q6_k, 3)
 
 static int matmul_batched_entry(VtbHipCtx* ctx, int qk, VtbHipBuf* out_buf, VtbHipBuf* w_buf, size_t w_offset,
                                 VtbHipBuf* acts_buf, size_t m, size_t k, size_t B) {

@@ -87,6 +87,10 @@ SIGNATURES = {
     "vtb_hip_segment_gelu_approx": ([_P, _P, _P, _S], None),
     "vtb_hip_segment_residual_add": ([_P, _P, _P, _S], None),
     "vtb_hip_segment_residual_add_rmsnorm": ([_P, _P, _P, _P, _P, _S, _S, _F], None),
+    "vtb_hip_segment_matmul3_q8_0": ([_P, _P, _S, _S, _P, _S, _S, _P, _S, _S, _P, _P, _S], None),
+    "vtb_hip_segment_matmul3_q4_k": ([_P, _P, _S, _S, _P, _S, _S, _P, _S, _S, _P, _P, _S], None),
+    "vtb_hip_segment_matmul3_q5_k": ([_P, _P, _S, _S, _P, _S, _S, _P, _S, _S, _P, _P, _S], None),
+    "vtb_hip_segment_matmul3_q6_k": ([_P, _P, _S, _S, _P, _S, _S, _P, _S, _S, _P, _P, _S], None),
     "vtb_hip_segment_kv_append": ([_P, _P, _S, _I, _P, _S, _S], None),
     "vtb_hip_segment_attn_decode": ([_P, _P, _P, _P, _S, _P, _S, _S, _S, _S, _S, _F, _I], None),
     "vtb_hip_segment_attn_decode_append": ([_P, _P, _P, _P, _S, _P, _S, _P, _P, _S, _S, _S, _S, _F, _I], None),
@@ -218,7 +222,7 @@ class Segment:
 
     def rmsnorm(self, out: Buffer, inp: Buffer, weight: Buffer, weight_off: int, n: int, eps: float):
         """out = rmsnorm(inp) * weight (f32 weights at byte offset weight_off);
-        seg.rmsnorm of gpuLayerStep (forward.zig:440)."""
+        seg.rmsnorm of gpuLayerStep (forward.zig:441)."""
         lib().vtb_hip_segment_rmsnorm(self.h, out.h, inp.h, weight.h, weight_off, n, eps)
 
     def swiglu(self, gate: Buffer, up: Buffer, n: int):
@@ -267,6 +271,19 @@ class Segment:
         if kind not in QUANT_KINDS:
             raise ValueError(f"unknown quant kind {kind!r}")
         getattr(lib(), f"vtb_hip_segment_matmul_{kind}")(self.h, out.h, w.h, w_offset, acts.h, m, k)
+
+    def matmul3(self, kind: str, w: Buffer, acts: Buffer, k: int, blocks):
+        """Two or three GEMVs of one format over the same acts in one launch:
+        blocks = [(out, w_offset, m), ...]."""
+        if kind not in QUANT_KINDS:
+            raise ValueError(f"unknown quant kind {kind!r}")
+        if len(blocks) not in (2, 3):
+            raise ValueError("matmul3 takes two or three row blocks")
+        b = list(blocks) + ([(None, 0, 0)] if len(blocks) == 2 else [])
+        args = []
+        for out, off, m in b:
+            args += [out.h if out is not None else None, off, m]
+        getattr(lib(), f"vtb_hip_segment_matmul3_{kind}")(self.h, *args, w.h, acts.h, k)
 
     def matmul_batched(self, kind: str, out: Buffer, w: Buffer, w_offset: int, acts: Buffer, m: int, k: int,
                        n_tokens: int):

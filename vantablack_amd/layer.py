@@ -1,5 +1,5 @@
 """Full-GPU decode layer: the host side of vantablack's gpuLayerStep
-(src/runtime/forward.zig:419-503) and gpuFinalStep (:505-511), composed from
+(src/runtime/forward.zig:419-513) and gpuFinalStep (:515-520), composed from
 this library's segment ops.  Per layer and token, on one segment:
 
   rmsnorm(xb <- x)                          vtb_hip_segment_rmsnorm
@@ -14,8 +14,10 @@ this library's segment ops.  Per layer and token, on one segment:
 
 gpu_token_step runs a whole token (every layer, then the final step) with
 each residual add fused into the rmsnorm that follows it
-(vtb_hip_segment_residual_add_rmsnorm): 11 launches per layer instead of 13,
-the same arithmetic.
+(vtb_hip_segment_residual_add_rmsnorm) and the Q/K/V and gate/up GEMVs
+grouped into one launch each when they share a format
+(vtb_hip_segment_matmul3_<kind>): 8 launches per layer instead of 13, the
+same arithmetic per output.
 
 The sliding window is the reference's caller-side offset shift
 (forward.zig:470-480): the K/V base moves to the window's first row and the
@@ -102,30 +104,39 @@ class LayerScratch:
 
 def _check(c: LayerConfig, pos: int):
     if c.n_heads * c.head_dim != c.dim:
-        raise ValueError("n_heads * head_dim must equal dim (as forward.zig:440-502 assumes)")
+        raise ValueError("n_heads * head_dim must equal dim (as forward.zig:441-510 assumes)")
     if pos >= c.max_seq:
         raise ValueError("position beyond max_seq")
 
 
-def _attention(seg, s, weights, off, kv_k, kv_v, c, layer, pos):
-    """Q/K/V GEMVs, then RoPE + K/V slot write + attention in one launch."""
+def _attention(seg, s, weights, off, kv_k, kv_v, c, layer, pos, grouped=False):
+    """Q/K/V GEMVs (one grouped launch when grouped and the three share a
+    format), then RoPE + K/V slot write + attention in one launch."""
     kv_dim = c.n_kv_heads * c.head_dim
     row_bytes = kv_dim * KV_BYTES[c.kv_dtype]
     layer_off = layer * c.max_seq * row_bytes
     wstart = 0 if (c.sliding_window == NO_WINDOW or pos < c.sliding_window) else pos - c.sliding_window + 1
     win_off = layer_off + wstart * row_bytes
-    seg.matmul_quant(off.kind_q, s.q, weights, off.wq, s.xb, c.dim, c.dim)
-    seg.matmul_quant(off.kind_k, s.k_cur, weights, off.wk, s.xb, kv_dim, c.dim)
-    seg.matmul_quant(off.kind_v, s.v_cur, weights, off.wv, s.xb, kv_dim, c.dim)
+    if grouped and off.kind_q == off.kind_k == off.kind_v:
+        seg.matmul3(off.kind_q, weights, s.xb, c.dim,
+                    [(s.q, off.wq, c.dim), (s.k_cur, off.wk, kv_dim), (s.v_cur, off.wv, kv_dim)])
+    else:
+        seg.matmul_quant(off.kind_q, s.q, weights, off.wq, s.xb, c.dim, c.dim)
+        seg.matmul_quant(off.kind_k, s.k_cur, weights, off.wk, s.xb, kv_dim, c.dim)
+        seg.matmul_quant(off.kind_v, s.v_cur, weights, off.wv, s.xb, kv_dim, c.dim)
     seg.attn_decode_rope_append(s.attn_out, s.q, kv_k, win_off, kv_v, win_off, s.k_cur, s.v_cur, c.n_heads,
                                 c.n_kv_heads, c.head_dim, pos + 1 - wstart, 1.0 / math.sqrt(c.head_dim),
                                 c.kv_dtype, pos, c.rope_base, c.rope_half)
 
 
-def _ffn(seg, s, weights, off, c):
-    """gate/up GEMVs, the gated activation, the down GEMV into s.ffn_out."""
-    seg.matmul_quant(off.kind_gate, s.gate, weights, off.wgate, s.xb, c.ffn_dim, c.dim)
-    seg.matmul_quant(off.kind_up, s.up, weights, off.wup, s.xb, c.ffn_dim, c.dim)
+def _ffn(seg, s, weights, off, c, grouped=False):
+    """gate/up GEMVs (one grouped launch when grouped and they share a
+    format), the gated activation, the down GEMV into s.ffn_out."""
+    if grouped and off.kind_gate == off.kind_up:
+        seg.matmul3(off.kind_gate, weights, s.xb, c.dim, [(s.gate, off.wgate, c.ffn_dim), (s.up, off.wup, c.ffn_dim)])
+    else:
+        seg.matmul_quant(off.kind_gate, s.gate, weights, off.wgate, s.xb, c.ffn_dim, c.dim)
+        seg.matmul_quant(off.kind_up, s.up, weights, off.wup, s.xb, c.ffn_dim, c.dim)
     if c.activation == "silu":
         seg.swiglu(s.gate, s.up, c.ffn_dim)
     elif c.activation == "gelu_approx":
@@ -146,10 +157,10 @@ def gpu_token_step(seg, s: LayerScratch, weights, offs, kv_k, kv_v, c: LayerConf
             seg.rmsnorm(s.xb, s.x, weights, off.attn_norm, c.dim, c.rms_eps)
         else:
             seg.residual_add_rmsnorm(s.x, s.ffn_out, s.xb, weights, off.attn_norm, c.dim, c.rms_eps)
-        _attention(seg, s, weights, off, kv_k, kv_v, c, layer, pos)
+        _attention(seg, s, weights, off, kv_k, kv_v, c, layer, pos, grouped=True)
         seg.matmul_quant(off.kind_o, s.xb2, weights, off.wo, s.attn_out, c.dim, c.dim)
         seg.residual_add_rmsnorm(s.x, s.xb2, s.xb, weights, off.ffn_norm, c.dim, c.rms_eps)
-        _ffn(seg, s, weights, off, c)
+        _ffn(seg, s, weights, off, c, grouped=True)
     if offs:
         seg.residual_add_rmsnorm(s.x, s.ffn_out, s.x, weights, output_norm_off, c.dim, c.rms_eps)
     else:
@@ -175,7 +186,7 @@ def gpu_layer_step(seg, s: LayerScratch, weights, off: LayerOffsets, kv_k, kv_v,
 
 def gpu_final_step(seg, s: LayerScratch, weights, output_norm_off: int, output_off: int, output_kind: str,
                    c: LayerConfig, vocab_size: int):
-    """gpuFinalStep (forward.zig:505-511): x = rmsnorm(x) in place, then the
+    """gpuFinalStep (forward.zig:515-520): x = rmsnorm(x) in place, then the
     logits projection into s.logits."""
     seg.rmsnorm(s.x, s.x, weights, output_norm_off, c.dim, c.rms_eps)
     seg.matmul_quant(output_kind, s.logits, weights, output_off, s.x, vocab_size, c.dim)
