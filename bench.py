@@ -395,8 +395,8 @@ def bench_full_decode(ctx, torch, ctx_rows=8192, steps=6, warmup=2):
     (forward.zig:419-520), through vantablack_amd.layer.gpu_token_step: per
     layer (residual add +) rmsnorm, the Q/K/V GEMVs (one grouped launch), RoPE +
     K/V append + attention (one launch), O GEMV, residual add + rmsnorm (one
-    launch), gate/up GEMVs (one grouped launch), SwiGLU, down GEMV; then the
-    last residual add + output norm and the 32000-row logits GEMV.  Q4_K projections (random blocks with small
+    launch), gate/up GEMVs + SwiGLU (one gated launch), down GEMV; then the last
+    residual add + output norm and the 32000-row logits GEMV.  Q4_K projections (random blocks with small
     f16 scales), f32 norm weights, f16 KV cache holding ctx_rows rows.
     Returns ms per token from HIP events on the context stream."""
     import numpy as np
@@ -475,7 +475,7 @@ def bench_full_decode(ctx, torch, ctx_rows=8192, steps=6, warmup=2):
     log(f"full decode: {t_tok * 1e3:.3f} ms/token ({1 / t_tok:.1f} tok/s), "
         f"{(weight_bytes + kv_bytes) / t_tok / 1e9:.0f} GB/s over weights + KV")
     return {"ms_per_token": round(t_tok * 1e3, 3), "tok_per_s": round(1 / t_tok, 1),
-            "launches_per_token": n_layers * 8 + 2, "weight_bytes": weight_bytes,
+            "launches_per_token": n_layers * 7 + 2, "weight_bytes": weight_bytes,
             "kv_bytes_per_token": kv_bytes,
             "hbm_gbs": round((weight_bytes + kv_bytes) / t_tok / 1e9, 1),
             "pct_of_hbm_peak": round(100.0 * (weight_bytes + kv_bytes) / t_tok / 1e9 / HBM_PEAK_GBS, 1)}

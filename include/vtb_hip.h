@@ -114,6 +114,22 @@ void vtb_hip_segment_matmul3_q6_k(VtbHipSeg *seg, VtbHipBuf *out0, size_t w_off0
                                   size_t w_off1, size_t m1, VtbHipBuf *out2, size_t w_off2, size_t m2,
                                   VtbHipBuf *w_buf, VtbHipBuf *acts_buf, size_t k);
 
+/* The FFN's gate and up GEMVs and its activation in one launch:
+ * out[i] = act(W_gate[i,:] . acts) * (W_up[i,:] . acts) for the m rows of the
+ * two matrices at w_off_gate / w_off_up in w_buf; activation 0 = silu
+ * (math.swiglu, math.zig:154-161), 1 = tanh-approximate gelu
+ * (math.gegluApprox, :166-175).  Replaces the gate/up segMatmulQuant calls
+ * and the swiglu / gegluApprox encoder of gpuLayerStep
+ * (forward.zig:502-507); no Metal counterpart (a fusion of those three). */
+void vtb_hip_segment_matmul_gated_q8_0(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_off_gate,
+                                       size_t w_off_up, VtbHipBuf *acts_buf, size_t m, size_t k, int activation);
+void vtb_hip_segment_matmul_gated_q4_k(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_off_gate,
+                                       size_t w_off_up, VtbHipBuf *acts_buf, size_t m, size_t k, int activation);
+void vtb_hip_segment_matmul_gated_q5_k(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_off_gate,
+                                       size_t w_off_up, VtbHipBuf *acts_buf, size_t m, size_t k, int activation);
+void vtb_hip_segment_matmul_gated_q6_k(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *w_buf, size_t w_off_gate,
+                                       size_t w_off_up, VtbHipBuf *acts_buf, size_t m, size_t k, int activation);
+
 /* The small ops a full-GPU decode layer chains between its matmuls
  * (gpuLayerStep, src/runtime/forward.zig:419-513), over f32 arrays of n
  * elements.  Bad ranges are recorded on the segment (commit reports them).

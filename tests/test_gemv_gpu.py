@@ -119,3 +119,33 @@ def test_grouped_row_blocks_match_single_gemvs(ctx, orc, kind, ms):
         ref = orc.matmul_quant(kind, w, x, m, k).astype(np.float64)
         cond = np.abs(np_dequant(kind, w).astype(np.float64).reshape(m, k)) @ np.abs(x.astype(np.float64))
         assert np.all(np.abs(got - ref) <= 1e-5 * cond), f"{kind} block m{m}"
+
+
+@pytest.mark.parametrize("activation", ["silu", "gelu_approx"])
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("m", [11008, 13])
+def test_gated_pair_matches_gemvs_and_activation(ctx, orc, kind, m, activation):
+    """vtb_hip_segment_matmul_gated_<kind>: act(W_gate x) * (W_up x) in one
+    launch against the oracle's GEMVs and math.swiglu / gegluApprox.  Bar:
+    the GEMV bar carried through the activation, |d act*u| <= 1.1 |u| dg +
+    |act| du with dg, du <= 1e-5 * cond, plus 1e-6 of the output's scale for
+    the activation's own rounding."""
+    k = 1024 if kind == "q8_0" else 2048
+    rng = np.random.default_rng(m + len(kind))
+    x = ((rng.random(k, dtype=np.float32) - 0.5) * 2.0).astype(np.float32)
+    wg, wu = random_weights(kind, m, k, seed=m), random_weights(kind, m, k, seed=m + 1)
+    off_up = (wg.size + 31) // 32 * 32
+    blob = np.zeros(off_up + wu.size, np.uint8)
+    blob[:wg.size], blob[off_up:] = wg, wu
+    wb, xb, ob = ctx.to_device(blob), ctx.to_device(x), ctx.alloc(m * 4)
+    with ctx.segment() as seg:
+        seg.matmul_gated(kind, ob, wb, 0, off_up, xb, m, k, activation)
+    got = ctx.download(ob, np.float32, m).astype(np.float64)
+    g = orc.matmul_quant(kind, wg, x, m, k)
+    u = orc.matmul_quant(kind, wu, x, m, k)
+    ref = (orc.swiglu(g, u) if activation == "silu" else orc.geglu_approx(g, u)).astype(np.float64)
+    xa = np.abs(x.astype(np.float64))
+    cg = np.abs(np_dequant(kind, wg).astype(np.float64).reshape(m, k)) @ xa
+    cu = np.abs(np_dequant(kind, wu).astype(np.float64).reshape(m, k)) @ xa
+    bar = 1e-5 * (1.1 * np.abs(u) * cg + (np.abs(g) + 1.0) * cu) + 1e-6 * np.max(np.abs(ref))
+    assert np.all(np.abs(got - ref) <= bar), f"{kind} m{m} {activation}"

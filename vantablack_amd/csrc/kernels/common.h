@@ -208,4 +208,12 @@ __device__ inline void buffer_load8_coherent(__amdgpu_buffer_rsrc_t r, int off, 
 // transfers (their LDS writes have landed when vmcnt reaches zero).
 __device__ inline void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Gated activations of the FFN (math.zig:154-175): silu(z) * u and the
+// tanh-approximate gelu(z) * u, in the reference's operation order.
+__device__ inline float silu_mul(float z, float u) { return z / (1.0f + expf(-z)) * u; }
+__device__ inline float gelu_approx_mul(float z, float u) {
+  const float inner = 0.7978845608028654f * (z + 0.044715f * z * z * z);
+  return 0.5f * z * (1.0f + tanhf(inner)) * u;
+}
+
 }  // namespace vtb

@@ -71,6 +71,11 @@ struct GemvArgs {
   float* out2;
   unsigned w_bytes2;
   int m2;
+  // Gated pair (the FFN's gate and up with its activation, nblk 1): a
+  // workgroup takes rows [R/2 wg, +R/2) of both W_gate (w) and W_up (w1) and
+  // writes act(gate) * up to out; 1 = silu (swiglu), 2 = gelu_approx.
+  int gated;
+  int pad;
 };
 
 // Activation staging: 8 rows of 64 lanes + kGemvXPad float4 per wave, in
@@ -359,10 +364,13 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
   } else if (a.nblk > 1 && wg >= a.wg1) {
     wp = a.w1, outp = a.out1, wbytes = a.w_bytes1, m = a.m1, wg -= a.wg1;
   }
-  const int row0 = wg * R;
+  constexpr int RH = R > 1 ? R / 2 : 1;
+  const bool gated = R > 1 && a.gated != 0;
+  const int row0 = gated ? wg * RH : wg * R;
   const int c0 = wave * 2048;  // the wave's slice
   const int c = lane & 7;      // lane within its block (K-quants)
   const auto rsrc = buffer_rsrc(wp, wbytes);
+  const auto rsrc_up = buffer_rsrc(a.w1, a.w_bytes1);
   const auto xrsrc = buffer_rsrc(a.x, 4u * (unsigned)a.k);
   const bool active = c0 + F::first(lane) < a.k;
 
@@ -382,8 +390,14 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
   typename F::Raw raw[R];
   const int boff = F::block(lane, c0) * F::BB;
 #pragma unroll
-  for (int i = 0; i < R; ++i)
-    F::load(rsrc, active && row0 + i < m ? (row0 + i) * a.row_bytes + boff : (int)wbytes, c, raw[i]);
+  for (int i = 0; i < R; ++i) {
+    // Gated: rows 0 .. RH-1 of the workgroup are gate rows, RH .. R-1 the
+    // same rows of up.
+    const bool up = gated && i >= RH;
+    const int row = row0 + (gated ? i % RH : i);
+    F::load(up ? rsrc_up : rsrc, active && row < m ? row * a.row_bytes + boff : (int)(up ? a.w_bytes1 : wbytes), c,
+            raw[i]);
+  }
 
   // Hand each float4 to its owner lane through this wave's LDS rows.  LDS
   // operations of one wave execute in order, so the reads below see every
@@ -420,7 +434,16 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
     if (lane == 0) s_part[wave][i] = t;
   }
   __syncthreads();
-  if ((int)threadIdx.x < R && row0 + (int)threadIdx.x < m) {
+  if (gated) {
+    if ((int)threadIdx.x < RH && row0 + (int)threadIdx.x < m) {
+      float g = 0.0f, u = 0.0f;
+      for (int w = 0; w < nw; ++w) {
+        g += s_part[w][threadIdx.x];
+        u += s_part[w][threadIdx.x + RH];
+      }
+      outp[row0 + threadIdx.x] = a.gated == 1 ? silu_mul(g, u) : gelu_approx_mul(g, u);
+    }
+  } else if ((int)threadIdx.x < R && row0 + (int)threadIdx.x < m) {
     float t = 0.0f;
     for (int w = 0; w < nw; ++w) t += s_part[w][threadIdx.x];
     outp[row0 + threadIdx.x] = t;

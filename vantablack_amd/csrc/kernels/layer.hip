@@ -52,13 +52,6 @@ struct EltArgs {
   int n4;          // as RmsNormArgs::n4
 };
 
-__device__ inline float silu_mul(float z, float u) { return z / (1.0f + expf(-z)) * u; }
-
-__device__ inline float gelu_approx_mul(float z, float u) {
-  const float inner = 0.7978845608028654f * (z + 0.044715f * z * z * z);
-  return 0.5f * z * (1.0f + tanhf(inner)) * u;
-}
-
 }  // namespace vtb
 
 extern "C" __global__ __launch_bounds__(1024) void vtb_rmsnorm_f32(vtb::RmsNormArgs a) {

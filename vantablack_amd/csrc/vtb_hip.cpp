@@ -136,6 +136,8 @@ struct GemvArgs {
   float* out2;
   unsigned w_bytes2;
   int m2;
+  int gated;
+  int pad;
 };
 
 // Mirrors vtb::XSplitArgs / vtb::QGemmArgs (kernels/qgemm.hip).
@@ -541,6 +543,52 @@ int launch_gemv_blocks(VtbHipCtx* ctx, int qk, int nblk, float* const outs[], co
   // float4 in dynamic LDS.
   const unsigned lds = waves * 8u * (64u + 4u) * 16u;
   return launch(ctx, ctx->f_gemv[qk][ri], (unsigned)grid, 1, 1, 64 * waves, &a, lds);
+}
+
+// Gated pair: out[i] = act(W_gate[i,:] . x) * (W_up[i,:] . x), the FFN's
+// gate/up GEMVs and its activation in one launch (act 1 = silu, 2 =
+// gelu_approx).  R/2 rows of each matrix per workgroup, R = 4 or 2.
+int launch_gemv_gated(VtbHipCtx* ctx, int qk, int act, float* out, const void* w_gate, const void* w_up,
+                      const float* x, size_t m, size_t k) {
+  if (qk < 0 || qk >= kNumQuant) return set_err(ctx, VTB_HIP_EINVAL, "bad quant kind");
+  if (act != 1 && act != 2) return set_err(ctx, VTB_HIP_EINVAL, "matmul_gated: bad activation");
+  if (m == 0 || k == 0 || k % kQuantBlockElems[qk] != 0)
+    return set_err(ctx, VTB_HIP_EINVAL, "matmul_gated: k must be a positive multiple of the block size");
+  if (k > 16 * 2048) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul_gated: k above 32768");
+  const size_t row_bytes = k / kQuantBlockElems[qk] * kQuantBlockBytes[qk];
+  if (m > 0x7fff0000 / row_bytes) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul_gated: weights beyond 2 GiB");
+  if ((uintptr_t)w_gate % 4 != 0 || (uintptr_t)w_up % 4 != 0)
+    return set_err(ctx, VTB_HIP_EINVAL, "matmul_gated: weights not 4-byte aligned");
+  if (!aligned16(x)) return set_err(ctx, VTB_HIP_EINVAL, "matmul_gated: activations not 16-byte aligned");
+  // R = 4 (two rows of each matrix) while that keeps two workgroups per CU
+  // and k fits its 8 waves, else R = 2.
+  int ri = -1;
+  for (int i = 0; i < kNumGemvR; ++i) {
+    if (kGemvRs[i] == 2) ri = i;
+    if (kGemvRs[i] == 4 && k <= 8 * 2048 && (long long)((m + 1) / 2) >= 2LL * std::max(ctx->cu_count, 1)) {
+      ri = i;
+      break;
+    }
+  }
+  if (ri < 0) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul_gated: no 2- or 4-row kernel");
+  const size_t RH = (size_t)kGemvRs[ri] / 2;
+  GemvArgs a;
+  memset(&a, 0, sizeof a);
+  a.w = w_gate;
+  a.x = x;
+  a.out = out;
+  a.w_bytes = (unsigned)((m * row_bytes + 3) & ~(size_t)3);
+  a.m = (int)m;
+  a.k = (int)k;
+  a.row_bytes = (int)row_bytes;
+  a.nblk = 1;
+  a.w1 = w_up;
+  a.w_bytes1 = a.w_bytes;
+  a.m1 = (int)m;
+  a.gated = act;
+  const unsigned waves = (unsigned)((k + 2047) / 2048);
+  const unsigned lds = waves * 8u * (64u + 4u) * 16u;
+  return launch(ctx, ctx->f_gemv[qk][ri], (unsigned)((m + RH - 1) / RH), 1, 1, 64 * waves, &a, lds);
 }
 
 int launch_gemv(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* x, size_t m, size_t k) {
@@ -1128,6 +1176,29 @@ static int matmul3_entry(VtbHipCtx* ctx, int qk, VtbHipBuf* out0, size_t w_off0,
     seg_note(seg, matmul3_entry(seg->ctx, QK, out0, w_off0, m0, out1, w_off1, m1, out2, w_off2, m2, w_buf,  \
                                 acts_buf, k));                                                            \
   }
+
+#define VTB_MATMUL_GATED_ENTRY(NAME, QK)                                                                  \
+  extern "C" void vtb_hip_segment_matmul_gated_##NAME(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* w_buf,    \
+                                                      size_t w_off_gate, size_t w_off_up, VtbHipBuf* acts_buf, \
+                                                      size_t m, size_t k, int activation) {                    \
+    if (!seg) return;                                                                                      \
+    VtbHipCtx* ctx = seg->ctx;                                                                             \
+    if (!out_buf || !w_buf || !acts_buf || m == 0 || k == 0 || k % kQuantBlockElems[QK] != 0 ||            \
+        m > ((size_t)1 << 31) || k > ((size_t)1 << 31))                                                    \
+      return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "matmul_gated: bad shape"));                       \
+    const size_t rb = k / kQuantBlockElems[QK] * kQuantBlockBytes[QK];                                     \
+    if (!buf_ok(w_buf, w_off_gate, m * rb) || !buf_ok(w_buf, w_off_up, m * rb) || !buf_ok(acts_buf, 0, k * 4) || \
+        !buf_ok(out_buf, 0, m * 4))                                                                        \
+      return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "matmul_gated: buffer too small"));                \
+    seg_note(seg, launch_gemv_gated(ctx, QK, activation == 0 ? 1 : (activation == 1 ? 2 : 0),             \
+                                    (float*)out_buf->ptr, bptr(w_buf, w_off_gate), bptr(w_buf, w_off_up),  \
+                                    (const float*)acts_buf->ptr, m, k));                                   \
+  }
+
+VTB_MATMUL_GATED_ENTRY(q8_0, 0)
+VTB_MATMUL_GATED_ENTRY(q4_k, 1)
+VTB_MATMUL_GATED_ENTRY(q5_k, 2)
+VTB_MATMUL_GATED_ENTRY(q6_k, 3)
 
 VTB_MATMUL3_ENTRY(q8_0, 0)
 VTB_MATMUL3_ENTRY(q4_k, 1)

@@ -87,6 +87,10 @@ SIGNATURES = {
     "vtb_hip_segment_gelu_approx": ([_P, _P, _P, _S], None),
     "vtb_hip_segment_residual_add": ([_P, _P, _P, _S], None),
     "vtb_hip_segment_residual_add_rmsnorm": ([_P, _P, _P, _P, _P, _S, _S, _F], None),
+    "vtb_hip_segment_matmul_gated_q8_0": ([_P, _P, _P, _S, _S, _P, _S, _S, _I], None),
+    "vtb_hip_segment_matmul_gated_q4_k": ([_P, _P, _P, _S, _S, _P, _S, _S, _I], None),
+    "vtb_hip_segment_matmul_gated_q5_k": ([_P, _P, _P, _S, _S, _P, _S, _S, _I], None),
+    "vtb_hip_segment_matmul_gated_q6_k": ([_P, _P, _P, _S, _S, _P, _S, _S, _I], None),
     "vtb_hip_segment_matmul3_q8_0": ([_P, _P, _S, _S, _P, _S, _S, _P, _S, _S, _P, _P, _S], None),
     "vtb_hip_segment_matmul3_q4_k": ([_P, _P, _S, _S, _P, _S, _S, _P, _S, _S, _P, _P, _S], None),
     "vtb_hip_segment_matmul3_q5_k": ([_P, _P, _S, _S, _P, _S, _S, _P, _S, _S, _P, _P, _S], None),
@@ -271,6 +275,16 @@ class Segment:
         if kind not in QUANT_KINDS:
             raise ValueError(f"unknown quant kind {kind!r}")
         getattr(lib(), f"vtb_hip_segment_matmul_{kind}")(self.h, out.h, w.h, w_offset, acts.h, m, k)
+
+    def matmul_gated(self, kind: str, out: Buffer, w: Buffer, w_off_gate: int, w_off_up: int, acts: Buffer, m: int,
+                     k: int, activation: str = "silu"):
+        """out = act(W_gate @ acts) * (W_up @ acts): the FFN's gate/up GEMVs and
+        swiglu (activation "silu") or gegluApprox ("gelu_approx") in one launch."""
+        if kind not in QUANT_KINDS:
+            raise ValueError(f"unknown quant kind {kind!r}")
+        act = {"silu": 0, "gelu_approx": 1}[activation]
+        getattr(lib(), f"vtb_hip_segment_matmul_gated_{kind}")(self.h, out.h, w.h, w_off_gate, w_off_up, acts.h, m, k,
+                                                               act)
 
     def matmul3(self, kind: str, w: Buffer, acts: Buffer, k: int, blocks):
         """Two or three GEMVs of one format over the same acts in one launch:

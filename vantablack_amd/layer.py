@@ -14,10 +14,11 @@ this library's segment ops.  Per layer and token, on one segment:
 
 gpu_token_step runs a whole token (every layer, then the final step) with
 each residual add fused into the rmsnorm that follows it
-(vtb_hip_segment_residual_add_rmsnorm) and the Q/K/V and gate/up GEMVs
-grouped into one launch each when they share a format
-(vtb_hip_segment_matmul3_<kind>): 8 launches per layer instead of 13, the
-same arithmetic per output.
+(vtb_hip_segment_residual_add_rmsnorm), the Q/K/V GEMVs grouped into one
+launch (vtb_hip_segment_matmul3_<kind>) and the gate/up GEMVs with the
+activation in one launch (vtb_hip_segment_matmul_gated_<kind>) when the
+projections share a format: 7 launches per layer instead of 13, the same
+arithmetic per output.
 
 The sliding window is the reference's caller-side offset shift
 (forward.zig:470-480): the K/V base moves to the window's first row and the
@@ -132,11 +133,15 @@ def _attention(seg, s, weights, off, kv_k, kv_v, c, layer, pos, grouped=False):
 def _ffn(seg, s, weights, off, c, grouped=False):
     """gate/up GEMVs (one grouped launch when grouped and they share a
     format), the gated activation, the down GEMV into s.ffn_out."""
+    if c.activation not in ("silu", "gelu_approx"):
+        raise ValueError(f"unknown activation {c.activation!r}")
     if grouped and off.kind_gate == off.kind_up:
-        seg.matmul3(off.kind_gate, weights, s.xb, c.dim, [(s.gate, off.wgate, c.ffn_dim), (s.up, off.wup, c.ffn_dim)])
-    else:
-        seg.matmul_quant(off.kind_gate, s.gate, weights, off.wgate, s.xb, c.ffn_dim, c.dim)
-        seg.matmul_quant(off.kind_up, s.up, weights, off.wup, s.xb, c.ffn_dim, c.dim)
+        # gate/up GEMVs and the activation in one launch, into s.gate
+        seg.matmul_gated(off.kind_gate, s.gate, weights, off.wgate, off.wup, s.xb, c.ffn_dim, c.dim, c.activation)
+        seg.matmul_quant(off.kind_down, s.ffn_out, weights, off.wdown, s.gate, c.dim, c.ffn_dim)
+        return
+    seg.matmul_quant(off.kind_gate, s.gate, weights, off.wgate, s.xb, c.ffn_dim, c.dim)
+    seg.matmul_quant(off.kind_up, s.up, weights, off.wup, s.xb, c.ffn_dim, c.dim)
     if c.activation == "silu":
         seg.swiglu(s.gate, s.up, c.ffn_dim)
     elif c.activation == "gelu_approx":
