@@ -131,8 +131,8 @@ def _attention(seg, s, weights, off, kv_k, kv_v, c, layer, pos, grouped=False):
 
 
 def _ffn(seg, s, weights, off, c, grouped=False):
-    """gate/up GEMVs (one grouped launch when grouped and they share a
-    format), the gated activation, the down GEMV into s.ffn_out."""
+    """gate/up GEMVs and the gated activation (one gated launch when grouped
+    and the two share a format), then the down GEMV into s.ffn_out."""
     if c.activation not in ("silu", "gelu_approx"):
         raise ValueError(f"unknown activation {c.activation!r}")
     if grouped and off.kind_gate == off.kind_up:
@@ -144,10 +144,8 @@ def _ffn(seg, s, weights, off, c, grouped=False):
     seg.matmul_quant(off.kind_up, s.up, weights, off.wup, s.xb, c.ffn_dim, c.dim)
     if c.activation == "silu":
         seg.swiglu(s.gate, s.up, c.ffn_dim)
-    elif c.activation == "gelu_approx":
-        seg.gelu_approx(s.gate, s.up, c.ffn_dim)
     else:
-        raise ValueError(f"unknown activation {c.activation!r}")
+        seg.gelu_approx(s.gate, s.up, c.ffn_dim)
     seg.matmul_quant(off.kind_down, s.ffn_out, weights, off.wdown, s.gate, c.dim, c.ffn_dim)
 
 
@@ -155,7 +153,8 @@ def gpu_token_step(seg, s: LayerScratch, weights, offs, kv_k, kv_v, c: LayerConf
                    output_norm_off: int, output_off: int, output_kind: str, vocab_size: int):
     """Every layer in offs, then gpuFinalStep, for the token at pos (s.x holds
     its embedding); leaves the normalised x in s.x and the logits in s.logits.
-    Each residual add runs fused with the rmsnorm after it."""
+    Each residual add runs fused with the rmsnorm after it, and Q/K/V and
+    gate/up (+ activation) run grouped when their formats match."""
     _check(c, pos)
     for layer, off in enumerate(offs):
         if layer == 0:
