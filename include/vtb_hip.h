@@ -147,6 +147,16 @@ void vtb_hip_segment_matmul_gated_q6_k(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHi
  *                 (bridge.h:145-149); math.addInto. */
 void vtb_hip_segment_rmsnorm(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *in_buf, VtbHipBuf *weight_buf,
                              size_t weight_offset, size_t n, float eps);
+/* rmsnorm of each of `rows` consecutive rows of n (the prefill's per-token
+ * norm, prefill.zig:159-164 and 207-212), same weights for every row. */
+void vtb_hip_segment_rmsnorm_rows(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *in_buf, VtbHipBuf *weight_buf,
+                                  size_t weight_offset, size_t n, size_t rows, float eps);
+/* RoPE in place of x = f32 [rows][n_heads][head_dim], row t at position
+ * pos0 + t: math.rope (half = 0) or math.ropeHalf (half = 1) per (token,
+ * head), as prefillLayer applies them (prefill.zig:177-189).  The same
+ * angles, sin/cos and operation order as the decode kernel's fused RoPE. */
+void vtb_hip_segment_rope_rows(VtbHipSeg *seg, VtbHipBuf *x_buf, size_t rows, size_t n_heads, size_t head_dim,
+                               size_t pos0, float base, int half);
 void vtb_hip_segment_swiglu(VtbHipSeg *seg, VtbHipBuf *gate_buf, VtbHipBuf *up_buf, size_t n);
 void vtb_hip_segment_gelu_approx(VtbHipSeg *seg, VtbHipBuf *gate_buf, VtbHipBuf *up_buf, size_t n);
 void vtb_hip_segment_residual_add(VtbHipSeg *seg, VtbHipBuf *a_buf, VtbHipBuf *b_buf, size_t n);

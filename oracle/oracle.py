@@ -478,3 +478,38 @@ def cpu_layer_step(x: np.ndarray, lw: LayerWeights, cache: OracleKvCache, c: Con
     h = swiglu(gate, up) if activation == "silu" else geglu_approx(gate, up)
     return (x + matmul_quant(lw.kind, lw.wdown, h, dim, ffn_dim)).astype(np.float32)
 
+
+def cpu_prefill_layer(x: np.ndarray, lw: LayerWeights, cache: OracleKvCache, c: ConfigC, layer: int, dim: int,
+                      ffn_dim: int, rms_eps: float, rope_base: float, rope_half: bool = False,
+                      activation: str = "silu", kv_round=None) -> np.ndarray:
+    """prefill.prefillLayer (src/runtime/prefill.zig:151-231) for the B tokens
+    of x ([B][dim]) at positions cache.pos .. cache.pos+B-1; returns the new
+    x and writes the B K/V rows into the cache.  kv_round, when given, maps
+    the f32 K/V rows (and the queries) to the values a lower-precision cache
+    holds, as the GPU path stores them."""
+    B = x.shape[0]
+    n_heads, n_kv, hd = c.n_heads, c.n_kv_heads, c.head_dim
+    kv_dim = n_kv * hd
+    pos0 = cache.pos
+    xb = np.stack([rms_norm(x[b], lw.attn_norm, rms_eps) for b in range(B)])
+    q = matmul_batched(lw.kind, lw.wq, xb, dim, dim, B).reshape(B, n_heads, hd)
+    k = matmul_batched(lw.kind, lw.wk, xb, kv_dim, dim, B).reshape(B, n_kv, hd)
+    v = matmul_batched(lw.kind, lw.wv, xb, kv_dim, dim, B).reshape(B, n_kv, hd)
+    for b in range(B):
+        q[b] = rope(q[b], pos0 + b, rope_base, rope_half)
+        k[b] = rope(k[b], pos0 + b, rope_base, rope_half)
+    if kv_round is not None:
+        k, v, q = kv_round(k), kv_round(v), kv_round(q)
+    for b in range(B):
+        cache.pos = pos0 + b
+        cache.key_slot(layer)[:] = k[b].reshape(-1)
+        cache.value_slot(layer)[:] = v[b].reshape(-1)
+    cache.pos = pos0
+    attn = attention_causal(q.reshape(B, -1), cache, c, layer, range(B))
+    x = (x + matmul_batched(lw.kind, lw.wo, attn, dim, dim, B).reshape(B, dim)).astype(np.float32)
+    xb = np.stack([rms_norm(x[b], lw.ffn_norm, rms_eps) for b in range(B)])
+    gate = matmul_batched(lw.kind, lw.wgate, xb, ffn_dim, dim, B)
+    up = matmul_batched(lw.kind, lw.wup, xb, ffn_dim, dim, B)
+    h = (swiglu(gate, up) if activation == "silu" else geglu_approx(gate, up)).reshape(B, ffn_dim)
+    return (x + matmul_batched(lw.kind, lw.wdown, h, dim, ffn_dim, B).reshape(B, dim)).astype(np.float32)
+

@@ -226,3 +226,106 @@ def test_model_decode_matches_cpu_layer_steps(ctx, orc, variant, path):
         s.release()
         for b in (wbuf, kk, kvv):
             b.release()
+
+
+# ---------------------------------------------------------------- prefill
+
+@pytest.mark.parametrize("n", [4096, 1003])
+def test_rmsnorm_rows(ctx, orc, n):
+    rows = 5
+    rng = np.random.default_rng(n + 3)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    w = (1 + 0.2 * rng.standard_normal(n)).astype(np.float32)
+    xb, wb, ob = ctx.to_device(x), ctx.to_device(w), ctx.alloc(rows * n * 4)
+    with ctx.segment() as seg:
+        seg.rmsnorm_rows(ob, xb, wb, 0, n, rows, 1e-5)
+    got = ctx.download(ob, np.float32, rows * n).reshape(rows, n)
+    for r in range(rows):
+        ref = orc.rms_norm(x[r], w, 1e-5)
+        assert np.max(np.abs(got[r] - ref)) <= 2e-6 * np.max(np.abs(ref)), f"row {r}"
+
+
+@pytest.mark.parametrize("half", [False, True])
+@pytest.mark.parametrize("heads,hd,pos0", [(8, 128, 0), (3, 256, 70000), (5, 64, 12)])
+def test_rope_rows(ctx, orc, heads, hd, pos0, half):
+    # Bar: 2e-6 of each head's largest value, as the decode path's fused RoPE
+    # is held to the oracle's math.rope / ropeHalf.
+    rows = 9
+    rng = np.random.default_rng(hd + heads)
+    x = rng.standard_normal((rows, heads, hd)).astype(np.float32)
+    xb = ctx.to_device(x)
+    with ctx.segment() as seg:
+        seg.rope_rows(xb, rows, heads, hd, pos0, 10000.0, half)
+    got = ctx.download(xb, np.float32, x.size).reshape(rows, heads, hd)
+    for t in range(rows):
+        ref = orc.rope(x[t], pos0 + t, 10000.0, half)
+        assert np.all(np.max(np.abs(got[t] - ref), axis=1) <= 2e-6 * np.max(np.abs(ref), axis=1)), f"row {t}"
+
+
+def _bf16_round(a):
+    from oracle import oracle as o
+    return o.bf16_bits_to_f32(o.f32_to_bf16_bits(np.ascontiguousarray(a, np.float32))).reshape(a.shape)
+
+
+@pytest.mark.parametrize("variant", ["llama_q4_k_f32cache", "mistral_q8_0_bf16_window_pos7"])
+def test_model_prefill_matches_cpu_prefill_layers(ctx, orc, variant):
+    """Two layers of prefill on the GPU (gpu_prefill_layer: MFMA projections
+    and attention, batched RoPE, per-token norms) against
+    oracle.cpu_prefill_layer (prefillLayer, prefill.zig:151-231).  Bars: 1e-4 of
+    the residual stream's largest value with an f32 cache; 2e-3 with a bf16
+    cache (queries, keys and values rounded to bf16 on both sides; P in f16
+    inside the MFMA attention)."""
+    import vantablack_amd as vb
+    from vantablack_amd.layer import LayerConfig, PrefillScratch, gpu_prefill_layer
+    if variant == "llama_q4_k_f32cache":
+        c = LayerConfig(dim=256, n_heads=4, n_kv_heads=4, head_dim=64, ffn_dim=512, max_seq=64, kv_dtype=vb.F32)
+        kind, B, pos0, bar, rnd = "q4_k", 37, 0, 1e-4, None
+    else:
+        c = LayerConfig(dim=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn_dim=768, max_seq=80, sliding_window=20,
+                        kv_dtype=vb.BF16)
+        kind, B, pos0, bar, rnd = "q8_0", 50, 7, 2e-3, _bf16_round
+    n_layers = 2
+    kinds = dict({n: kind for n in ("q", "k", "v", "o", "gate", "up", "down")}, out="q8_0")
+    m = TinyModel(orc, c, n_layers, 64, kinds, seed=len(variant))
+    wbuf = ctx.to_device(m.blob)
+    kv_dim = c.n_kv_heads * c.head_dim
+    rng = np.random.default_rng(23)
+    cache = orc.OracleKvCache(n_layers, c.n_kv_heads, c.head_dim, c.max_seq)
+    # Rows before pos0 (an earlier prompt): random, in the cache's precision.
+    prior_k = rng.standard_normal((n_layers, pos0, kv_dim)).astype(np.float32)
+    prior_v = rng.standard_normal((n_layers, pos0, kv_dim)).astype(np.float32)
+    if rnd is not None:
+        prior_k, prior_v = rnd(prior_k), rnd(prior_v)
+    for l in range(n_layers):
+        cache.layer_rows("k", l)[:pos0] = prior_k[l].reshape(pos0, c.n_kv_heads, c.head_dim)
+        cache.layer_rows("v", l)[:pos0] = prior_v[l].reshape(pos0, c.n_kv_heads, c.head_dim)
+    if c.kv_dtype == vb.F32:
+        kfull = np.zeros((n_layers, c.max_seq, kv_dim), np.float32)
+        vfull = np.zeros_like(kfull)
+    else:
+        kfull = np.zeros((n_layers, c.max_seq, kv_dim), np.uint16)
+        vfull = np.zeros_like(kfull)
+    kfull[:, :pos0] = prior_k if c.kv_dtype == vb.F32 else orc.f32_to_bf16_bits(prior_k).reshape(prior_k.shape)
+    vfull[:, :pos0] = prior_v if c.kv_dtype == vb.F32 else orc.f32_to_bf16_bits(prior_v).reshape(prior_v.shape)
+    kk, kvv = ctx.to_device(kfull), ctx.to_device(vfull)
+    s = PrefillScratch(ctx, c, B)
+    x = rng.standard_normal((B, c.dim)).astype(np.float32)
+    oc = orc.config(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq, c.sliding_window)
+    try:
+        ctx.upload(s.x, x)
+        with ctx.segment() as seg:
+            for l in range(n_layers):
+                gpu_prefill_layer(seg, s, wbuf, m.offsets[l], kk, kvv, c, l, pos0)
+        ctx.wait_idle()
+        got = ctx.download(s.x, np.float32, B * c.dim).reshape(B, c.dim)
+        cache.pos = pos0
+        xr = x
+        for l in range(n_layers):
+            xr = orc.cpu_prefill_layer(xr, m.oracle_layers[l], cache, oc, l, c.dim, c.ffn_dim, c.rms_eps,
+                                       c.rope_base, c.rope_half, c.activation, kv_round=rnd)
+        assert np.max(np.abs(got - xr)) <= bar * np.max(np.abs(xr)), f"{variant}: max err " \
+            f"{np.max(np.abs(got - xr)) / np.max(np.abs(xr)):.2e}"
+    finally:
+        s.release()
+        for b in (wbuf, kk, kvv):
+            b.release()

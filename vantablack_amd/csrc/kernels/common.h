@@ -216,4 +216,17 @@ __device__ inline float gelu_approx_mul(float z, float u) {
   return 0.5f * z * (1.0f + tanhf(inner)) * u;
 }
 
+// sin and cos of an f32 RoPE angle.  The angle (up to ~2^24 rad) is
+// reduced in f64: theta / (2 pi) in revolutions, keeping the signed fraction
+// (absolute error < 1e-9 rev), then rounded to f32 (< 3e-8 rev) and fed to
+// the hardware v_sin / v_cos, which take revolutions.  About ten
+// instructions against the library sincosf's large-argument reduction; the
+// GPU RoPE tests hold the result to the host libm at 2e-6 of the row.
+__device__ inline void rope_sincos(float theta, float* sn, float* cs) {
+  const double rev = (double)theta * 0.15915494309189533577;  // 1 / (2 pi)
+  const float r = (float)(rev - __builtin_rint(rev));
+  *sn = __builtin_amdgcn_sinf(r);
+  *cs = __builtin_amdgcn_cosf(r);
+}
+
 }  // namespace vtb

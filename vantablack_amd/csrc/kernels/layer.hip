@@ -7,6 +7,10 @@
 //   vtb_gelu_approx_f32   gate = 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3))) * up
 //                         (math.zig:166-175)
 //   vtb_residual_add_f32  a += b                              (math.addInto)
+//   vtb_rope_rows_f32     RoPE of rows tokens x heads in place, token t at
+//                         position pos0 + t (prefill.zig:180-189: math.rope /
+//                         ropeHalf per (batch, head)), with the decode
+//                         kernel's angle, sin/cos and operation order
 //   vtb_add_rmsnorm_f32   x += b, then out = rmsnorm(x) * w: the residual add
 //                         and the rmsnorm that follows it in the layer
 //                         (forward.zig:487 and 490, 510 then the next layer's 441),
@@ -29,9 +33,19 @@ struct RmsNormArgs {
   const float* in;
   const float* w;
   int n;
-  int n4;     // float4 chunks (n / 4 when all three arrays are 16-byte aligned, else 0)
+  int n4;     // float4 chunks per row (n / 4 when every row of the three arrays is 16-byte aligned, else 0)
   float eps;
-  int pad;
+  int pad;    // rows: one workgroup per row of n (gridDim.x)
+};
+
+struct RopeRowsArgs {
+  float* x;               // [rows][heads][head_dim] f32
+  const float* inv_freq;  // [head_dim / 2]
+  long long pos0;         // position of row 0
+  int rows;
+  int heads;
+  int head_dim;
+  int half;               // ropeHalf pairing (i, i + d/2) instead of (2i, 2i+1)
 };
 
 struct AddNormArgs {
@@ -57,6 +71,9 @@ struct EltArgs {
 extern "C" __global__ __launch_bounds__(1024) void vtb_rmsnorm_f32(vtb::RmsNormArgs a) {
   __shared__ float s_part[16];
   const int tid = (int)threadIdx.x;
+  // Row blockIdx.x of a batch (the prefill's per-token norm).
+  a.in += (size_t)blockIdx.x * a.n;
+  a.out += (size_t)blockIdx.x * a.n;
   const int n4 = a.n4;
   float ss = 0.0f;
   for (int c = tid; c < n4; c += 1024) {
@@ -117,6 +134,24 @@ extern "C" __global__ __launch_bounds__(1024) void vtb_add_rmsnorm_f32(vtb::AddN
     reinterpret_cast<float4*>(a.out)[c] = make_float4(v.x * w.x * inv, v.y * w.y * inv, v.z * w.z * inv, v.w * w.w * inv);
   }
   for (int i = 4 * n4 + tid; i < a.n; i += 1024) a.out[i] = a.x[i] * a.w[i] * inv;
+}
+
+// One thread per rotated pair.
+extern "C" __global__ __launch_bounds__(256) void vtb_rope_rows_f32(vtb::RopeRowsArgs a) {
+#pragma clang fp contract(off)
+  const int hd2 = a.head_dim >> 1;
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long long)a.rows * a.heads * hd2) return;
+  const int j = (int)(i % hd2);
+  const long long rh = i / hd2;  // row * heads + head
+  const long long row = rh / a.heads;
+  float* base = a.x + rh * a.head_dim;
+  const int i0 = a.half ? j : 2 * j, i1 = a.half ? j + hd2 : 2 * j + 1;
+  float sn, cs;
+  vtb::rope_sincos((float)(a.pos0 + row) * a.inv_freq[j], &sn, &cs);
+  const float x0 = base[i0], x1 = base[i1];
+  base[i0] = x0 * cs - x1 * sn;
+  base[i1] = x0 * sn + x1 * cs;
 }
 
 // Elementwise kernels: thread i takes float4 i; the elements past the float4

@@ -183,6 +183,7 @@ struct VtbHipCtx {
   hipFunction_t f_xsplit = nullptr;
   hipModule_t mod_layer = nullptr;  // rmsnorm, swiglu, gelu_approx, residual_add
   hipFunction_t f_rmsnorm = nullptr, f_swiglu = nullptr, f_gelu = nullptr, f_resadd = nullptr, f_addnorm = nullptr;
+  hipFunction_t f_rope_rows = nullptr;
   hipFunction_t f_qgemm[kNumQuant] = {};  // vtb_qgemm_<kind>
   // Split-K workspace and arrival counters (counters are zero between launches).
   void* ws = nullptr;
@@ -744,6 +745,7 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
   ok = ok && hipModuleGetFunction(&ctx->f_gelu, ctx->mod_layer, "vtb_gelu_approx_f32") == hipSuccess;
   ok = ok && hipModuleGetFunction(&ctx->f_resadd, ctx->mod_layer, "vtb_residual_add_f32") == hipSuccess;
   ok = ok && hipModuleGetFunction(&ctx->f_addnorm, ctx->mod_layer, "vtb_add_rmsnorm_f32") == hipSuccess;
+  ok = ok && hipModuleGetFunction(&ctx->f_rope_rows, ctx->mod_layer, "vtb_rope_rows_f32") == hipSuccess;
   for (int qk = 0; ok && qk < kNumQuant; ++qk) {
     snprintf(name, sizeof name, "vtb_qgemm_%s", kQuantNames[qk]);
     ok = hipModuleGetFunction(&ctx->f_qgemm[qk], ctx->mod_qgemm, name) == hipSuccess;
@@ -890,13 +892,14 @@ struct EltArgs {
   int n4;
 };
 
-extern "C" void vtb_hip_segment_rmsnorm(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* in_buf, VtbHipBuf* weight_buf,
-                                        size_t weight_offset, size_t n, float eps) {
+extern "C" void vtb_hip_segment_rmsnorm_rows(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* in_buf,
+                                             VtbHipBuf* weight_buf, size_t weight_offset, size_t n, size_t rows,
+                                             float eps) {
   if (!seg) return;
   VtbHipCtx* ctx = seg->ctx;
-  if (n == 0) return;
-  if (n > 0x7fffffff / 4 || weight_offset % 4 || !buf_ok(out_buf, 0, n * 4) || !buf_ok(in_buf, 0, n * 4) ||
-      !buf_ok(weight_buf, weight_offset, n * 4))
+  if (n == 0 || rows == 0) return;
+  if (n > 0x7fffffff / 4 || rows > 0x7fffffff || weight_offset % 4 || !buf_ok(out_buf, 0, rows * n * 4) ||
+      !buf_ok(in_buf, 0, rows * n * 4) || !buf_ok(weight_buf, weight_offset, n * 4))
     return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "rmsnorm: bad range"));
   RmsNormArgs a;
   memset(&a, 0, sizeof a);
@@ -904,9 +907,39 @@ extern "C" void vtb_hip_segment_rmsnorm(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbH
   a.in = (const float*)bptr(in_buf, 0);
   a.w = (const float*)bptr(weight_buf, weight_offset);
   a.n = (int)n;
-  a.n4 = (aligned16(a.out) && aligned16(a.in) && aligned16(a.w)) ? (int)(n / 4) : 0;
+  a.n4 = (aligned16(a.out) && aligned16(a.in) && aligned16(a.w) && (rows == 1 || n % 4 == 0)) ? (int)(n / 4) : 0;
   a.eps = eps;
-  seg_note(seg, launch(ctx, ctx->f_rmsnorm, 1, 1, 1, 1024, &a));
+  seg_note(seg, launch(ctx, ctx->f_rmsnorm, (unsigned)rows, 1, 1, 1024, &a));
+}
+
+extern "C" void vtb_hip_segment_rmsnorm(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* in_buf, VtbHipBuf* weight_buf,
+                                        size_t weight_offset, size_t n, float eps) {
+  vtb_hip_segment_rmsnorm_rows(seg, out_buf, in_buf, weight_buf, weight_offset, n, 1, eps);
+}
+
+struct RopeRowsArgs {
+  float* x;
+  const float* inv_freq;
+  long long pos0;
+  int rows;
+  int heads;
+  int head_dim;
+  int half;
+};
+
+extern "C" void vtb_hip_segment_rope_rows(VtbHipSeg* seg, VtbHipBuf* x_buf, size_t rows, size_t n_heads,
+                                          size_t head_dim, size_t pos0, float base, int half) {
+  if (!seg) return;
+  VtbHipCtx* ctx = seg->ctx;
+  if (rows == 0 || n_heads == 0) return;
+  if (head_dim == 0 || head_dim % 2 || head_dim > 4096 || rows > 0x7fffffff || n_heads > 65535 ||
+      pos0 > ((size_t)1 << 40) || !buf_ok(x_buf, 0, rows * n_heads * head_dim * 4))
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "rope_rows: bad shape"));
+  const float* inv = rope_table(ctx, base, head_dim);
+  if (!inv) return seg_note(seg, VTB_HIP_EDEVICE);  // rope_table recorded the cause
+  RopeRowsArgs a{(float*)bptr(x_buf, 0), inv, (long long)pos0, (int)rows, (int)n_heads, (int)head_dim, half ? 1 : 0};
+  const size_t pairs = rows * n_heads * (head_dim / 2);
+  seg_note(seg, launch(ctx, ctx->f_rope_rows, (unsigned)((pairs + 255) / 256), 1, 1, 256, &a));
 }
 
 struct AddNormArgs {

@@ -83,6 +83,8 @@ SIGNATURES = {
     "vtb_hip_wait_idle": ([_P], _I),
     "vtb_hip_segment_copy": ([_P, _P, _S, _P, _S, _S], None),
     "vtb_hip_segment_rmsnorm": ([_P, _P, _P, _P, _S, _S, _F], None),
+    "vtb_hip_segment_rmsnorm_rows": ([_P, _P, _P, _P, _S, _S, _S, _F], None),
+    "vtb_hip_segment_rope_rows": ([_P, _P, _S, _S, _S, _S, _F, _I], None),
     "vtb_hip_segment_swiglu": ([_P, _P, _P, _S], None),
     "vtb_hip_segment_gelu_approx": ([_P, _P, _P, _S], None),
     "vtb_hip_segment_residual_add": ([_P, _P, _P, _S], None),
@@ -228,6 +230,14 @@ class Segment:
         """out = rmsnorm(inp) * weight (f32 weights at byte offset weight_off);
         seg.rmsnorm of gpuLayerStep (forward.zig:441)."""
         lib().vtb_hip_segment_rmsnorm(self.h, out.h, inp.h, weight.h, weight_off, n, eps)
+
+    def rmsnorm_rows(self, out: Buffer, inp: Buffer, weight: Buffer, weight_off: int, n: int, rows: int,
+                     eps: float):
+        lib().vtb_hip_segment_rmsnorm_rows(self.h, out.h, inp.h, weight.h, weight_off, n, rows, eps)
+
+    def rope_rows(self, x: Buffer, rows: int, n_heads: int, head_dim: int, pos0: int, base: float,
+                  half: bool = False):
+        lib().vtb_hip_segment_rope_rows(self.h, x.h, rows, n_heads, head_dim, pos0, base, 1 if half else 0)
 
     def swiglu(self, gate: Buffer, up: Buffer, n: int):
         lib().vtb_hip_segment_swiglu(self.h, gate.h, up.h, n)

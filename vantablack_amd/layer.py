@@ -194,3 +194,77 @@ def gpu_final_step(seg, s: LayerScratch, weights, output_norm_off: int, output_o
     logits projection into s.logits."""
     seg.rmsnorm(s.x, s.x, weights, output_norm_off, c.dim, c.rms_eps)
     seg.matmul_quant(output_kind, s.logits, weights, output_off, s.x, vocab_size, c.dim)
+
+
+class PrefillScratch:
+    """Device activations of a B-token prefill (prefill.zig Scratch: x, xb,
+    xb2, q, k_cur, v_cur, attn_out, gate, up, ffn_out), plus the queries in
+    the cache dtype for the MFMA attention."""
+
+    def __init__(self, ctx, c: LayerConfig, B: int):
+        kv_dim = c.n_kv_heads * c.head_dim
+        q_dim = c.n_heads * c.head_dim
+        self.B = B
+        self.x = ctx.alloc(B * c.dim * 4)
+        self.xb = ctx.alloc(B * c.dim * 4)
+        self.xb2 = ctx.alloc(B * c.dim * 4)
+        self.q = ctx.alloc(B * q_dim * 4)
+        self.q_dt = ctx.alloc(B * q_dim * 2)
+        self.k_cur = ctx.alloc(B * kv_dim * 4)
+        self.v_cur = ctx.alloc(B * kv_dim * 4)
+        self.attn_out = ctx.alloc(B * q_dim * 4)
+        self.gate = ctx.alloc(B * c.ffn_dim * 4)
+        self.up = ctx.alloc(B * c.ffn_dim * 4)
+        self.ffn_out = ctx.alloc(B * c.dim * 4)
+
+    def release(self):
+        for b in (self.x, self.xb, self.xb2, self.q, self.q_dt, self.k_cur, self.v_cur, self.attn_out, self.gate,
+                  self.up, self.ffn_out):
+            b.release()
+
+
+def gpu_prefill_layer(seg, s: PrefillScratch, weights, off: LayerOffsets, kv_k, kv_v, c: LayerConfig, layer: int,
+                      pos0: int):
+    """prefillLayer (src/runtime/prefill.zig:151-231) on the GPU for the B
+    tokens at positions pos0 .. pos0+B-1 (s.x holds their embeddings, [B][dim]):
+    per-token rmsnorm, batched Q/K/V projections (MFMA), RoPE per (token,
+    head), the B K/V rows written at pos0, causal attention (MFMA for f16/bf16
+    caches), O projection + residual, per-token rmsnorm, batched gate/up, the
+    activation, batched down projection + residual.  Updates s.x in place."""
+    B = s.B
+    if c.n_heads * c.head_dim != c.dim:
+        raise ValueError("n_heads * head_dim must equal dim")
+    if pos0 + B > c.max_seq:
+        raise ValueError("prefill beyond max_seq (KvCacheFull)")
+    kv_dim = c.n_kv_heads * c.head_dim
+    q_dim = c.n_heads * c.head_dim
+    row_bytes = kv_dim * KV_BYTES[c.kv_dtype]
+    layer_off = layer * c.max_seq * row_bytes
+    seg.rmsnorm_rows(s.xb, s.x, weights, off.attn_norm, c.dim, B, c.rms_eps)
+    seg.matmul_batched(off.kind_q, s.q, weights, off.wq, s.xb, c.dim, c.dim, B)
+    seg.matmul_batched(off.kind_k, s.k_cur, weights, off.wk, s.xb, kv_dim, c.dim, B)
+    seg.matmul_batched(off.kind_v, s.v_cur, weights, off.wv, s.xb, kv_dim, c.dim, B)
+    seg.rope_rows(s.q, B, c.n_heads, c.head_dim, pos0, c.rope_base, c.rope_half)
+    seg.rope_rows(s.k_cur, B, c.n_kv_heads, c.head_dim, pos0, c.rope_base, c.rope_half)
+    seg.kv_append(kv_k, layer_off + pos0 * row_bytes, c.kv_dtype, s.k_cur, 0, B * kv_dim)
+    seg.kv_append(kv_v, layer_off + pos0 * row_bytes, c.kv_dtype, s.v_cur, 0, B * kv_dim)
+    if c.kv_dtype == hip.F32:
+        q = s.q
+    else:
+        seg.kv_append(s.q_dt, 0, c.kv_dtype, s.q, 0, B * q_dim)  # f32 -> cache dtype, nearest even
+        q = s.q_dt
+    seg.attn_prefill(s.attn_out, q, kv_k, kv_v, layer_off, B, pos0, c.sliding_window, c.n_heads, c.n_kv_heads,
+                     c.head_dim, 1.0 / math.sqrt(c.head_dim), c.kv_dtype)
+    seg.matmul_batched(off.kind_o, s.xb2, weights, off.wo, s.attn_out, c.dim, c.dim, B)
+    seg.residual_add(s.x, s.xb2, B * c.dim)
+    seg.rmsnorm_rows(s.xb, s.x, weights, off.ffn_norm, c.dim, B, c.rms_eps)
+    seg.matmul_batched(off.kind_gate, s.gate, weights, off.wgate, s.xb, c.ffn_dim, c.dim, B)
+    seg.matmul_batched(off.kind_up, s.up, weights, off.wup, s.xb, c.ffn_dim, c.dim, B)
+    if c.activation == "silu":
+        seg.swiglu(s.gate, s.up, B * c.ffn_dim)
+    elif c.activation == "gelu_approx":
+        seg.gelu_approx(s.gate, s.up, B * c.ffn_dim)
+    else:
+        raise ValueError(f"unknown activation {c.activation!r}")
+    seg.matmul_batched(off.kind_down, s.ffn_out, weights, off.wdown, s.gate, c.dim, c.ffn_dim, B)
+    seg.residual_add(s.x, s.ffn_out, B * c.dim)
