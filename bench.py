@@ -481,6 +481,91 @@ def bench_full_decode(ctx, torch, ctx_rows=8192, steps=6, warmup=2):
             "pct_of_hbm_peak": round(100.0 * (weight_bytes + kv_bytes) / t_tok / 1e9 / HBM_PEAK_GBS, 1)}
 
 
+def bench_full_prefill(ctx, torch, B=8192, reps=2):
+    """A whole-prompt prefill of B tokens through a Llama-3-8B-shaped model
+    on the GPU (prefillLayer x 32, prefill.zig:151-231, through
+    vantablack_amd.layer.gpu_prefill_layer): per layer per-token rmsnorm,
+    Q/K/V projections on MFMA, batched RoPE, the K/V rows into a bf16 cache,
+    MFMA causal attention, O projection + residual, rmsnorm, gate/up, SwiGLU,
+    down + residual.  Q4_K projections (random blocks, small f16 scales), a
+    distinct weight set per layer (3.9 GB).  Returns ms per prompt from HIP
+    events on the context stream."""
+    import numpy as np
+    from vantablack_amd import layer as ly
+    dim, nh, nkv, hd, ffn, n_layers = 4096, 32, 8, 128, 14336, 32
+    c = ly.LayerConfig(dim=dim, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn_dim=ffn, max_seq=B,
+                       rope_base=500000.0, kv_dtype=2)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(78)
+    qb, qe = QUANT_BLOCK["q4_k"]
+    scale = torch.tensor([0.002], dtype=torch.float16, device=dev).view(torch.uint8)
+    tensors, offs, pos = [], [], 0
+
+    def put(t):
+        nonlocal pos
+        off = pos
+        tensors.append(t)
+        pos += t.numel()
+        return off
+
+    def q4k(m, k):
+        w = torch.randint(0, 256, (m * k // qe, qb), generator=g, dtype=torch.uint8, device=dev)
+        w[:, 0:2] = scale
+        w[:, 2:4] = scale
+        return w.reshape(-1)
+
+    norm = torch.ones(dim, dtype=torch.float32, device=dev).view(torch.uint8)
+    shapes = [("q", dim, dim), ("k", nkv * hd, dim), ("v", nkv * hd, dim), ("o", dim, dim),
+              ("gate", ffn, dim), ("up", ffn, dim), ("down", dim, ffn)]
+    for _ in range(n_layers):
+        an = put(norm)
+        o = {n: put(q4k(m, k)) for n, m, k in shapes}
+        fn = put(norm)
+        offs.append(ly.LayerOffsets(an, o["q"], o["k"], o["v"], o["o"], fn, o["gate"], o["up"], o["down"],
+                                    *(["q4_k"] * 7)))
+    blob = torch.cat(tensors)
+    del tensors
+    kc = torch.zeros((n_layers, B, nkv, hd), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    x0 = (torch.randn((B, dim), generator=g, device=dev) * 0.1).contiguous()
+    torch.cuda.synchronize()
+    wb, kb, vb_ = ctx.wrap_tensor(blob), ctx.wrap_tensor(kc), ctx.wrap_tensor(vc)
+    xin = ctx.wrap_tensor(x0)
+    s = ly.PrefillScratch(ctx, c, B)
+
+    def prompt(seg):
+        seg.copy(s.x, 0, xin, 0, B * dim)
+        for l in range(n_layers):
+            ly.gpu_prefill_layer(seg, s, wb, offs[l], kb, vb_, c, l, 0)
+
+    with ctx.segment() as seg:
+        prompt(seg)
+    ctx.wait_idle()
+    stream = torch.cuda.ExternalStream(ctx.stream)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    with ctx.segment() as seg:
+        for _ in range(reps):
+            prompt(seg)
+    e1.record(stream)
+    ctx.wait_idle()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / reps
+    proj_flops = 2.0 * B * n_layers * sum(m * k for _, m, k in shapes)
+    attn_flops = n_layers * prefill_flops(B, nh, hd)
+    s.release()
+    for b in (wb, kb, vb_, xin):
+        b.release()
+    del blob, kc, vc, x0
+    torch.cuda.empty_cache()
+    log(f"full prefill: {t * 1e3:.1f} ms per {B}-token prompt ({B / t:.0f} tok/s), "
+        f"{(proj_flops + attn_flops) / t / 1e12:.0f} TFLOP/s (reference flops)")
+    return {"ms_per_prompt": round(t * 1e3, 2), "tok_per_s": round(B / t, 1),
+            "ms_per_layer": round(t * 1e3 / n_layers, 3),
+            "tflops_reference": round((proj_flops + attn_flops) / t / 1e12, 1)}
+
+
 def cpu_baseline(seconds_budget=18.0):
     """Time the CPU oracle on a bounded sample of the decode workload: one
     C2 layer at L=8192 (f32 values of the f16 cache, as vantablack's f32
@@ -659,6 +744,7 @@ def main():
     qgemm = None if args.no_gemv else bench_qgemm_layer(ctx, torch, "q4_k", 8192)
     # The whole token: every layer on the GPU (gpuLayerStep x 32 + gpuFinalStep).
     full = None if args.no_gemv else bench_full_decode(ctx, torch, ctx_rows=args.ctx)
+    fullp = None if (args.no_gemv or args.no_prefill) else bench_full_prefill(ctx, torch)
     cpu = None if args.no_cpu else cpu_baseline()
     ctx.close()
     traffic = load_traffic()
@@ -705,6 +791,11 @@ def main():
                         "f32 activations; weights cycled over >= 512 MB so each launch reads HBM",
             **gemv,
         }
+    if fullp:
+        line["full_prefill"] = dict(
+            workload="Llama-3-8B shapes (32 layers, 32q/8kv heads x d128, ffn 14336), 8192-token prompt, Q4_K "
+                     "projections on MFMA, bf16 KV, MFMA causal attention; every op on the GPU",
+            **fullp)
     if full:
         line["full_decode"] = dict(
             workload="Llama-2-7B shapes, 32 layers + output norm and 32000-row logits, Q4_K projections, "
