@@ -329,3 +329,23 @@ def test_model_prefill_matches_cpu_prefill_layers(ctx, orc, variant):
         s.release()
         for b in (wbuf, kk, kvv):
             b.release()
+
+
+def test_new_entries_reject_bad_shapes_and_ranges(ctx):
+    """Bad arguments to the batched and grouped entries are recorded on the
+    segment and reported by commit, never launched."""
+    import vantablack_amd as vb
+    from vantablack_amd import hip
+    small, big = ctx.alloc(256), ctx.alloc(1 << 20)
+    calls = [
+        lambda s: s.rmsnorm_rows(big, small, big, 0, 64, 4, 1e-5),        # rows beyond the input
+        lambda s: s.rope_rows(big, 2, 4, 63, 0, 10000.0),                 # odd head_dim
+        lambda s: s.rope_rows(small, 4, 4, 64, 0, 10000.0),               # rows beyond the buffer
+        lambda s: s.matmul3("q8_0", small, big, 64, [(big, 0, 64), (big, 0, 64)]),   # weights beyond the buffer
+        lambda s: s.matmul_gated("q4_k", big, big, 0, 0, big, 64, 100),   # k not a whole number of blocks
+        lambda s: hip.lib().vtb_hip_segment_matmul_gated_q8_0(s.h, big.h, big.h, 0, 0, big.h, 8, 64, 7),  # activation
+    ]
+    for i, call in enumerate(calls):
+        with pytest.raises(vb.HipError):
+            with ctx.segment() as seg:
+                call(seg)
