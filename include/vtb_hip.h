@@ -114,6 +114,25 @@ void vtb_hip_segment_matmul3_q6_k(VtbHipSeg *seg, VtbHipBuf *out0, size_t w_off0
                                   size_t w_off1, size_t m1, VtbHipBuf *out2, size_t w_off2, size_t m2,
                                   VtbHipBuf *w_buf, VtbHipBuf *acts_buf, size_t k);
 
+/* Two or three batched matmuls of one format over the same B tokens of
+ * activations (the Q/K/V or gate/up projections of prefillLayer,
+ * prefill.zig:167-169 and 216-217): out_b[B][m_b] = acts . W_b^T, each
+ * block exactly vtb_hip_segment_matmul_batched_<kind>, with the activation
+ * pre-pass run once for all blocks (m2 = 0 for two).  No reference
+ * counterpart: a launch-count reduction over matmulBatched's calls. */
+void vtb_hip_segment_matmul_batched3_q8_0(VtbHipSeg *seg, VtbHipBuf *out0, size_t w_off0, size_t m0,
+                                         VtbHipBuf *out1, size_t w_off1, size_t m1, VtbHipBuf *out2, size_t w_off2,
+                                         size_t m2, VtbHipBuf *w_buf, VtbHipBuf *acts_buf, size_t k, size_t B);
+void vtb_hip_segment_matmul_batched3_q4_k(VtbHipSeg *seg, VtbHipBuf *out0, size_t w_off0, size_t m0,
+                                         VtbHipBuf *out1, size_t w_off1, size_t m1, VtbHipBuf *out2, size_t w_off2,
+                                         size_t m2, VtbHipBuf *w_buf, VtbHipBuf *acts_buf, size_t k, size_t B);
+void vtb_hip_segment_matmul_batched3_q5_k(VtbHipSeg *seg, VtbHipBuf *out0, size_t w_off0, size_t m0,
+                                         VtbHipBuf *out1, size_t w_off1, size_t m1, VtbHipBuf *out2, size_t w_off2,
+                                         size_t m2, VtbHipBuf *w_buf, VtbHipBuf *acts_buf, size_t k, size_t B);
+void vtb_hip_segment_matmul_batched3_q6_k(VtbHipSeg *seg, VtbHipBuf *out0, size_t w_off0, size_t m0,
+                                         VtbHipBuf *out1, size_t w_off1, size_t m1, VtbHipBuf *out2, size_t w_off2,
+                                         size_t m2, VtbHipBuf *w_buf, VtbHipBuf *acts_buf, size_t k, size_t B);
+
 /* The FFN's gate and up GEMVs and its activation in one launch:
  * out[i] = act(W_gate[i,:] . acts) * (W_up[i,:] . acts) for the m rows of the
  * two matrices at w_off_gate / w_off_up in w_buf; activation 0 = silu

@@ -116,3 +116,30 @@ def test_synchronous_entry(ctx, orc):
     got = ctx.download(ob, np.float32, B * m).reshape(B, m)
     ref = orc.matmul_batched(kind, w, x, m, k, B)
     assert np.max(np.abs(got - ref)) <= 1e-4 * np.max(np.abs(ref))
+
+
+@pytest.mark.parametrize("kind", ["q8_0", "q4_k", "q5_k", "q6_k"])
+def test_shared_prepass_blocks_match_single_calls(ctx, kind):
+    """vtb_hip_segment_matmul_batched3_<kind>: three weight blocks over one
+    activation pre-pass give exactly what three single batched calls give
+    (same kernels, same split of the activations)."""
+    k, B, ms = 512, 37, (256, 64, 130)
+    rng = np.random.default_rng(len(kind))
+    acts = rng.standard_normal((B, k)).astype(np.float32)
+    ws = [random_weights(kind, m, k, seed=m) for m in ms]
+    offs, pos = [], 0
+    for w in ws:
+        offs.append(pos)
+        pos += (w.size + 31) // 32 * 32
+    blob = np.zeros(pos, np.uint8)
+    for w, o in zip(ws, offs):
+        blob[o:o + w.size] = w
+    wb, xb = ctx.to_device(blob), ctx.to_device(acts)
+    grouped = [ctx.alloc(B * m * 4) for m in ms]
+    single = [ctx.alloc(B * m * 4) for m in ms]
+    with ctx.segment() as seg:
+        seg.matmul_batched3(kind, wb, xb, k, B, [(o, off, m) for o, off, m in zip(grouped, offs, ms)])
+        for o, off, m in zip(single, offs, ms):
+            seg.matmul_batched(kind, o, wb, off, xb, m, k, B)
+    for g, s1, m in zip(grouped, single, ms):
+        assert np.array_equal(ctx.download(g, np.float32, B * m), ctx.download(s1, np.float32, B * m))

@@ -604,17 +604,24 @@ int launch_gemv(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* 
 // planes, 16-column sums and the token's inverse scale in the
 // context's scratch (grown on demand, after the stream drains); the GEMM
 // then runs one workgroup per 128 tokens x 128 rows.
-int launch_qgemm(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* acts, size_t m, size_t k,
-                 size_t B) {
+// Up to three weight matrices of one format over the same activations share
+// one pre-pass (the Q/K/V or gate/up projections of a prefill layer).
+int launch_qgemm_blocks(VtbHipCtx* ctx, int qk, int nblk, float* const outs[], const void* const ws[],
+                        const size_t ms[], const float* acts, size_t k, size_t B) {
   if (qk < 0 || qk >= kNumQuant) return set_err(ctx, VTB_HIP_EINVAL, "bad quant kind");
-  if (m == 0 || k == 0 || B == 0 || k % kQuantBlockElems[qk] != 0 || k % 32 != 0)
+  if (nblk < 1 || nblk > 3) return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: 1 to 3 weight blocks");
+  if (k == 0 || B == 0 || k % kQuantBlockElems[qk] != 0 || k % 32 != 0)
     return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: k must be a positive multiple of the block size");
   // prefill.zig MAX_K: the reference returns DimTooLarge above it.
   if (k > 32768) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul_batched: k above 32768");
   const size_t row_bytes = k / kQuantBlockElems[qk] * kQuantBlockBytes[qk];
-  if (m > 0x7fff0000 / row_bytes) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul_batched: weights beyond 2 GiB");
-  if (B > (1u << 24) || m > (1u << 24)) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul_batched: too many tokens or rows");
-  if ((uintptr_t)w % 4 != 0) return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: weights not 4-byte aligned");
+  for (int b = 0; b < nblk; ++b) {
+    const size_t m = ms[b];
+    if (m == 0) return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: empty weight block");
+    if (m > 0x7fff0000 / row_bytes) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul_batched: weights beyond 2 GiB");
+    if (B > (1u << 24) || m > (1u << 24)) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "matmul_batched: too many tokens or rows");
+    if ((uintptr_t)ws[b] % 4 != 0) return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: weights not 4-byte aligned");
+  }
   if (!aligned16(acts)) return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: activations not 16-byte aligned");
   const size_t Bp = (B + 127) / 128 * 128;
   const size_t planes_bytes = 2 * Bp * k * 2, sums_bytes = Bp * (k / 16) * 4, inv_bytes = Bp * 4;
@@ -641,24 +648,36 @@ int launch_qgemm(VtbHipCtx* ctx, int qk, float* out, const void* w, const float*
   xa.k = (int)k;
   int rc = launch(ctx, ctx->f_xsplit, (unsigned)Bp, 1, 1, 256, &xa);
   if (rc) return rc;
-  QGemmArgs a;
-  memset(&a, 0, sizeof a);
-  a.w = w;
-  a.planes = planes;
-  a.sums = sums;
-  a.inv_scale = inv_scale;
-  a.out = out;
-  // Rounded up to whole dwords: the last 2-byte-aligned field can end two
-  // bytes into one (see launch_gemv).
-  a.w_bytes = (unsigned)((m * row_bytes + 3) & ~(size_t)3);
-  a.m = (int)m;
-  a.k = (int)k;
-  a.B = (int)B;
-  a.Bp = (int)Bp;
-  a.row_bytes = (int)row_bytes;
-  a.n_rb = (int)((m + 127) / 128);
-  a.n_tb = (int)(Bp / 128);
-  return launch(ctx, ctx->f_qgemm[qk], (unsigned)(a.n_rb * a.n_tb), 1, 1, 256, &a);
+  for (int b = 0; b < nblk; ++b) {
+    QGemmArgs a;
+    memset(&a, 0, sizeof a);
+    a.w = ws[b];
+    a.planes = planes;
+    a.sums = sums;
+    a.inv_scale = inv_scale;
+    a.out = outs[b];
+    // Rounded up to whole dwords: the last 2-byte-aligned field can end two
+    // bytes into one (see launch_gemv).
+    a.w_bytes = (unsigned)((ms[b] * row_bytes + 3) & ~(size_t)3);
+    a.m = (int)ms[b];
+    a.k = (int)k;
+    a.B = (int)B;
+    a.Bp = (int)Bp;
+    a.row_bytes = (int)row_bytes;
+    a.n_rb = (int)((ms[b] + 127) / 128);
+    a.n_tb = (int)(Bp / 128);
+    rc = launch(ctx, ctx->f_qgemm[qk], (unsigned)(a.n_rb * a.n_tb), 1, 1, 256, &a);
+    if (rc) return rc;
+  }
+  return VTB_HIP_OK;
+}
+
+int launch_qgemm(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* acts, size_t m, size_t k,
+                 size_t B) {
+  float* const outs[1] = {out};
+  const void* const ws[1] = {w};
+  const size_t ms[1] = {m};
+  return launch_qgemm_blocks(ctx, qk, 1, outs, ws, ms, acts, k, B);
 }
 
 int launch_append(VtbHipCtx* ctx, void* dst, const float* src, size_t n, int dtype) {
@@ -1249,6 +1268,45 @@ static int matmul_batched_entry(VtbHipCtx* ctx, int qk, VtbHipBuf* out_buf, VtbH
     return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: buffer too small");
   return launch_qgemm(ctx, qk, (float*)out_buf->ptr, bptr(w_buf, w_offset), (const float*)acts_buf->ptr, m, k, B);
 }
+
+// Two or three batched matmuls of one format over the same activations,
+// one activation pre-pass (m2 = 0: two).
+static int matmul_batched3_entry(VtbHipCtx* ctx, int qk, VtbHipBuf* out0, size_t w_off0, size_t m0, VtbHipBuf* out1,
+                                 size_t w_off1, size_t m1, VtbHipBuf* out2, size_t w_off2, size_t m2,
+                                 VtbHipBuf* w_buf, VtbHipBuf* acts_buf, size_t k, size_t B) {
+  if (!ctx || !out0 || !out1 || !w_buf || !acts_buf || (m2 && !out2)) return VTB_HIP_EINVAL;
+  if (m0 == 0 || m1 == 0 || k == 0 || B == 0 || k % kQuantBlockElems[qk] != 0 || m0 > ((size_t)1 << 31) ||
+      m1 > ((size_t)1 << 31) || m2 > ((size_t)1 << 31) || k > ((size_t)1 << 31) || B > ((size_t)1 << 31))
+    return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched3: bad shape");
+  const size_t row_bytes = k / kQuantBlockElems[qk] * kQuantBlockBytes[qk];
+  VtbHipBuf* outs_b[3] = {out0, out1, out2};
+  const size_t offs[3] = {w_off0, w_off1, w_off2}, ms[3] = {m0, m1, m2};
+  const int nblk = m2 ? 3 : 2;
+  float* outs[3] = {nullptr, nullptr, nullptr};
+  const void* ws[3] = {nullptr, nullptr, nullptr};
+  if (!buf_ok(acts_buf, 0, B * k * 4)) return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched3: buffer too small");
+  for (int b = 0; b < nblk; ++b) {
+    if (!buf_ok(w_buf, offs[b], ms[b] * row_bytes) || !buf_ok(outs_b[b], 0, B * ms[b] * 4))
+      return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched3: buffer too small");
+    outs[b] = (float*)outs_b[b]->ptr;
+    ws[b] = bptr(w_buf, offs[b]);
+  }
+  return launch_qgemm_blocks(ctx, qk, nblk, outs, ws, ms, (const float*)acts_buf->ptr, k, B);
+}
+
+#define VTB_MATMUL_BATCHED3_ENTRY(NAME, QK)                                                                   \
+  extern "C" void vtb_hip_segment_matmul_batched3_##NAME(                                                    \
+      VtbHipSeg* seg, VtbHipBuf* out0, size_t w_off0, size_t m0, VtbHipBuf* out1, size_t w_off1, size_t m1,  \
+      VtbHipBuf* out2, size_t w_off2, size_t m2, VtbHipBuf* w_buf, VtbHipBuf* acts_buf, size_t k, size_t B) { \
+    if (!seg) return;                                                                                        \
+    seg_note(seg, matmul_batched3_entry(seg->ctx, QK, out0, w_off0, m0, out1, w_off1, m1, out2, w_off2, m2,   \
+                                        w_buf, acts_buf, k, B));                                             \
+  }
+
+VTB_MATMUL_BATCHED3_ENTRY(q8_0, 0)
+VTB_MATMUL_BATCHED3_ENTRY(q4_k, 1)
+VTB_MATMUL_BATCHED3_ENTRY(q5_k, 2)
+VTB_MATMUL_BATCHED3_ENTRY(q6_k, 3)
 
 #define VTB_MATMUL_BATCHED_ENTRIES(NAME, QK)                                                              \
   extern "C" void vtb_hip_segment_matmul_batched_##NAME(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* w_buf, \

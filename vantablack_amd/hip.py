@@ -93,6 +93,10 @@ SIGNATURES = {
     "vtb_hip_segment_matmul_gated_q4_k": ([_P, _P, _P, _S, _S, _P, _S, _S, _I], None),
     "vtb_hip_segment_matmul_gated_q5_k": ([_P, _P, _P, _S, _S, _P, _S, _S, _I], None),
     "vtb_hip_segment_matmul_gated_q6_k": ([_P, _P, _P, _S, _S, _P, _S, _S, _I], None),
+    "vtb_hip_segment_matmul_batched3_q8_0": ([_P, _P, _S, _S, _P, _S, _S, _P, _S, _S, _P, _P, _S, _S], None),
+    "vtb_hip_segment_matmul_batched3_q4_k": ([_P, _P, _S, _S, _P, _S, _S, _P, _S, _S, _P, _P, _S, _S], None),
+    "vtb_hip_segment_matmul_batched3_q5_k": ([_P, _P, _S, _S, _P, _S, _S, _P, _S, _S, _P, _P, _S, _S], None),
+    "vtb_hip_segment_matmul_batched3_q6_k": ([_P, _P, _S, _S, _P, _S, _S, _P, _S, _S, _P, _P, _S, _S], None),
     "vtb_hip_segment_matmul3_q8_0": ([_P, _P, _S, _S, _P, _S, _S, _P, _S, _S, _P, _P, _S], None),
     "vtb_hip_segment_matmul3_q4_k": ([_P, _P, _S, _S, _P, _S, _S, _P, _S, _S, _P, _P, _S], None),
     "vtb_hip_segment_matmul3_q5_k": ([_P, _P, _S, _S, _P, _S, _S, _P, _S, _S, _P, _P, _S], None),
@@ -295,6 +299,19 @@ class Segment:
         act = {"silu": 0, "gelu_approx": 1}[activation]
         getattr(lib(), f"vtb_hip_segment_matmul_gated_{kind}")(self.h, out.h, w.h, w_off_gate, w_off_up, acts.h, m, k,
                                                                act)
+
+    def matmul_batched3(self, kind: str, w: Buffer, acts: Buffer, k: int, n_tokens: int, blocks):
+        """Two or three batched matmuls of one format over the same tokens,
+        one activation pre-pass: blocks = [(out, w_offset, m), ...]."""
+        if kind not in QUANT_KINDS:
+            raise ValueError(f"unknown quant kind {kind!r}")
+        if len(blocks) not in (2, 3):
+            raise ValueError("matmul_batched3 takes two or three weight blocks")
+        b = list(blocks) + ([(None, 0, 0)] if len(blocks) == 2 else [])
+        args = []
+        for out, off, m in b:
+            args += [out.h if out is not None else None, off, m]
+        getattr(lib(), f"vtb_hip_segment_matmul_batched3_{kind}")(self.h, *args, w.h, acts.h, k, n_tokens)
 
     def matmul3(self, kind: str, w: Buffer, acts: Buffer, k: int, blocks):
         """Two or three GEMVs of one format over the same acts in one launch:

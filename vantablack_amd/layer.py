@@ -227,7 +227,8 @@ def gpu_prefill_layer(seg, s: PrefillScratch, weights, off: LayerOffsets, kv_k, 
                       pos0: int):
     """prefillLayer (src/runtime/prefill.zig:151-231) on the GPU for the B
     tokens at positions pos0 .. pos0+B-1 (s.x holds their embeddings, [B][dim]):
-    per-token rmsnorm, batched Q/K/V projections (MFMA), RoPE per (token,
+    per-token rmsnorm, batched Q/K/V projections (MFMA; one activation
+    pre-pass when they share a format, as gate/up below), RoPE per (token,
     head), the B K/V rows written at pos0, causal attention (MFMA for f16/bf16
     caches), O projection + residual, per-token rmsnorm, batched gate/up, the
     activation, batched down projection + residual.  Updates s.x in place."""
@@ -241,9 +242,13 @@ def gpu_prefill_layer(seg, s: PrefillScratch, weights, off: LayerOffsets, kv_k, 
     row_bytes = kv_dim * KV_BYTES[c.kv_dtype]
     layer_off = layer * c.max_seq * row_bytes
     seg.rmsnorm_rows(s.xb, s.x, weights, off.attn_norm, c.dim, B, c.rms_eps)
-    seg.matmul_batched(off.kind_q, s.q, weights, off.wq, s.xb, c.dim, c.dim, B)
-    seg.matmul_batched(off.kind_k, s.k_cur, weights, off.wk, s.xb, kv_dim, c.dim, B)
-    seg.matmul_batched(off.kind_v, s.v_cur, weights, off.wv, s.xb, kv_dim, c.dim, B)
+    if off.kind_q == off.kind_k == off.kind_v:
+        seg.matmul_batched3(off.kind_q, weights, s.xb, c.dim, B,
+                            [(s.q, off.wq, c.dim), (s.k_cur, off.wk, kv_dim), (s.v_cur, off.wv, kv_dim)])
+    else:
+        seg.matmul_batched(off.kind_q, s.q, weights, off.wq, s.xb, c.dim, c.dim, B)
+        seg.matmul_batched(off.kind_k, s.k_cur, weights, off.wk, s.xb, kv_dim, c.dim, B)
+        seg.matmul_batched(off.kind_v, s.v_cur, weights, off.wv, s.xb, kv_dim, c.dim, B)
     seg.rope_rows(s.q, B, c.n_heads, c.head_dim, pos0, c.rope_base, c.rope_half)
     seg.rope_rows(s.k_cur, B, c.n_kv_heads, c.head_dim, pos0, c.rope_base, c.rope_half)
     seg.kv_append(kv_k, layer_off + pos0 * row_bytes, c.kv_dtype, s.k_cur, 0, B * kv_dim)
@@ -258,8 +263,12 @@ def gpu_prefill_layer(seg, s: PrefillScratch, weights, off: LayerOffsets, kv_k, 
     seg.matmul_batched(off.kind_o, s.xb2, weights, off.wo, s.attn_out, c.dim, c.dim, B)
     seg.residual_add(s.x, s.xb2, B * c.dim)
     seg.rmsnorm_rows(s.xb, s.x, weights, off.ffn_norm, c.dim, B, c.rms_eps)
-    seg.matmul_batched(off.kind_gate, s.gate, weights, off.wgate, s.xb, c.ffn_dim, c.dim, B)
-    seg.matmul_batched(off.kind_up, s.up, weights, off.wup, s.xb, c.ffn_dim, c.dim, B)
+    if off.kind_gate == off.kind_up:
+        seg.matmul_batched3(off.kind_gate, weights, s.xb, c.dim, B,
+                            [(s.gate, off.wgate, c.ffn_dim), (s.up, off.wup, c.ffn_dim)])
+    else:
+        seg.matmul_batched(off.kind_gate, s.gate, weights, off.wgate, s.xb, c.ffn_dim, c.dim, B)
+        seg.matmul_batched(off.kind_up, s.up, weights, off.wup, s.xb, c.ffn_dim, c.dim, B)
     if c.activation == "silu":
         seg.swiglu(s.gate, s.up, B * c.ffn_dim)
     elif c.activation == "gelu_approx":
