@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../kargs.h"
+
 namespace vtb {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));

@@ -41,31 +41,6 @@
 
 namespace vtb {
 
-struct DecodeArgs {
-  const float* q;       // [n_q][n_heads][D] f32
-  const void* k;        // layer base: row t at k + t*n_kv*D elements
-  const void* v;
-  float* out;           // [n_q][n_heads][D] f32
-  float* ws_o;          // [n_q][n_kv][n_splits][G][D]
-  float* ws_ml;         // [n_q][n_kv][n_splits][G][2]
-  float* wg_o;          // [n_q][n_kv][n_groups][G][D] group partials
-  float* wg_ml;         // [n_q][n_kv][n_groups][G][2]
-  unsigned* counters;   // [n_q][n_kv][n_groups + 1] x decode_counter_stride, zero between launches
-  int n_heads;
-  int n_kv;
-  int n_splits;
-  int rows_per_split;   // multiple of NW * RPW
-  long long pos0;       // absolute position of query 0
-  long long window;     // sliding window in rows; <= 0 disables it
-  float scale_log2;     // (1/sqrt(D)) * log2(e)
-  int pad;
-  const float* k_new;   // optional (decode only): f32 K/V row appended at
-  const float* v_new;   //   row pos0 before attention; null when not fused
-  const float* rope_inv_freq;  // optional: [D/2] 1/base^(2j/D); RoPE of q and
-  long long rope_pos;          //   k_new at absolute position rope_pos is
-  int rope_half;               //   fused when set (half form if rope_half)
-  int pad2;
-};
 
 
 // RoPE of element i of one head x[0..D) (math.rope / math.ropeHalf,

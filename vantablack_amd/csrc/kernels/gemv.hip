@@ -50,33 +50,6 @@
 
 namespace vtb {
 
-struct GemvArgs {
-  const uint8_t* w;   // m rows of row_bytes
-  const float* x;     // [k], 16-byte aligned
-  float* out;         // [m]
-  unsigned w_bytes;   // m * row_bytes rounded up to a multiple of 4
-  int m;
-  int k;
-  int row_bytes;
-  // Up to two more row blocks of the same format sharing x (the Q/K/V or
-  // gate/up projections of one layer): workgroups [wg1, wg2) compute block 1
-  // and [wg2, grid) block 2, each with its own weights, output and rows.
-  int nblk;           // 1, 2 or 3
-  int wg1, wg2;
-  const uint8_t* w1;
-  float* out1;
-  unsigned w_bytes1;
-  int m1;
-  const uint8_t* w2;
-  float* out2;
-  unsigned w_bytes2;
-  int m2;
-  // Gated pair (the FFN's gate and up with its activation, nblk 1): a
-  // workgroup takes rows [R/2 wg, +R/2) of both W_gate (w) and W_up (w1) and
-  // writes act(gate) * up to out; 1 = silu (swiglu), 2 = gelu_approx.
-  int gated;
-  int pad;
-};
 
 // Activation staging: 8 rows of 64 lanes + kGemvXPad float4 per wave, in
 // dynamic LDS that the host sizes with the same constants.

@@ -13,13 +13,6 @@
 
 namespace vtb {
 
-struct AppendArgs {
-  void* dst;         // already offset to the first destination element
-  const float* src;
-  long long n;
-  int vec;           // 1 when dst/src allow 16-byte (f32) / 8-byte (16-bit) stores
-  int pad;
-};
 
 template <typename KV>
 __device__ inline void append_body(const AppendArgs& a) {
@@ -64,12 +57,7 @@ extern "C" __global__ __launch_bounds__(256) void vtb_kv_append_bf16(vtb::Append
 }
 
 // Unaligned-safe scalar copy: dst and src may be any 4-byte aligned offsets.
-struct CopyArgs {
-  float* dst;
-  const float* src;
-  long long n;
-};
-extern "C" __global__ __launch_bounds__(256) void vtb_copy_f32(CopyArgs a) {
+extern "C" __global__ __launch_bounds__(256) void vtb_copy_f32(vtb::CopyArgs a) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < a.n) a.dst[i] = a.src[i];
 }

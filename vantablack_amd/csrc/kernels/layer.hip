@@ -28,43 +28,9 @@
 
 namespace vtb {
 
-struct RmsNormArgs {
-  float* out;
-  const float* in;
-  const float* w;
-  int n;
-  int n4;     // float4 chunks per row (n / 4 when every row of the three arrays is 16-byte aligned, else 0)
-  float eps;
-  int pad;    // rows: one workgroup per row of n (gridDim.x)
-};
 
-struct RopeRowsArgs {
-  float* x;               // [rows][heads][head_dim] f32
-  const float* inv_freq;  // [head_dim / 2]
-  long long pos0;         // position of row 0
-  int rows;
-  int heads;
-  int head_dim;
-  int half;               // ropeHalf pairing (i, i + d/2) instead of (2i, 2i+1)
-};
 
-struct AddNormArgs {
-  float* x;        // residual stream, updated in place
-  const float* b;  // addend
-  float* out;      // normalised output (may be x)
-  const float* w;
-  int n;
-  int n4;          // float4 chunks when all four arrays are 16-byte aligned, else 0
-  float eps;
-  int pad;
-};
 
-struct EltArgs {
-  float* a;        // gate (activations) or the residual target
-  const float* b;  // up, or the residual addend
-  int n;
-  int n4;          // as RmsNormArgs::n4
-};
 
 }  // namespace vtb
 

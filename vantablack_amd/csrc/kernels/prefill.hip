@@ -40,29 +40,7 @@
 
 namespace vtb {
 
-struct PrefillArgs {
-  const void* q;       // [n_q][n_heads][D] of DT
-  const void* k;       // layer base: row t at k + t*n_kv*D elements
-  const _Float16* vt;  // V^T from the pre-pass: [n_kv][D][vt_ld]
-  float* out;          // [n_q][n_heads][D] f32
-  int n_q;
-  int n_heads;
-  int n_kv;
-  int vt_ld;           // keys per V^T row (multiple of BN, >= pos0 + n_q)
-  long long pos0;      // absolute position of query 0
-  long long window;    // sliding window in rows; <= 0 disables it
-  float scale_log2;    // (1/sqrt(D)) * log2(e)
-  int pad1;
-};
 
-struct VtArgs {
-  const void* v;       // layer base: row t at v + t*n_kv*D elements
-  _Float16* vt;        // [n_kv][D][vt_ld]
-  int n_rows;          // rows of V to transpose; keys >= n_rows are zero
-  int n_kv;
-  int vt_ld;
-  int pad;
-};
 
 template <typename DT> struct Mfma;
 template <> struct Mfma<kv_bf16> {
@@ -138,7 +116,7 @@ __device__ __forceinline__ void vt_body(const VtArgs& a) {
       const int o = o0 + e;
       h[e] = tile[(16 * (o >> 4) + vt_col(o & 15)) * TP + d];
     }
-    *reinterpret_cast<f16x8*>(a.vt + ((long long)kvh * D + d) * a.vt_ld + key0 + o0) = h;
+    *reinterpret_cast<f16x8*>((_Float16*)a.vt + ((long long)kvh * D + d) * a.vt_ld + key0 + o0) = h;
   }
 }
 
@@ -217,7 +195,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
 
   const long long row_stride = (long long)a.n_kv * D;  // elements
   const uint16_t* kg = (const uint16_t*)a.k + (long long)kvh * D;
-  const _Float16* vtg = a.vt + (long long)kvh * D * a.vt_ld;
+  const _Float16* vtg = (const _Float16*)a.vt + (long long)kvh * D * a.vt_ld;
 
   // Tile staging through registers: thread chunk i of a tile is K row
   // (tid + NT i) / KCH, chunk (tid + NT i) % KCH, and V^T row (tid + NT i) /

@@ -42,16 +42,6 @@
 
 namespace vtb {
 
-struct XSplitArgs {
-  const float* x;     // [B][k]
-  uint16_t* planes;   // [2][Bp][k] f16 bits: h1, h2 of x * 2^e
-  float* sums;        // [Bp][k / 16]: sum of each 16-column group of x * 2^e
-  float* inv_scale;   // [Bp]: 2^-e of each token
-  int B;
-  int Bp;             // B rounded up to the token tile; rows >= B are zero
-  int k;
-  int pad;
-};
 
 __device__ inline float wave_max(float v) {
   v = fmaxf(v, dpp<DPP_XOR1>(v));
@@ -131,21 +121,6 @@ extern "C" __global__ __launch_bounds__(256) void vtb_xsplit(XSplitArgs a) {
   }
 }
 
-struct QGemmArgs {
-  const uint8_t* w;         // m rows of row_bytes
-  const uint16_t* planes;   // [2][Bp][k] f16 bits from vtb_xsplit
-  const float* sums;        // [Bp][k / 16] (of x * 2^e)
-  const float* inv_scale;   // [Bp]: 2^-e
-  float* out;               // [B][m]
-  unsigned w_bytes;         // m * row_bytes rounded up to a multiple of 4
-  int m;
-  int k;
-  int B;
-  int Bp;
-  int row_bytes;
-  int n_rb;                 // row blocks of 128
-  int n_tb;                 // token blocks of 128
-};
 
 constexpr int kQgTile = 128;  // tokens and rows per workgroup
 constexpr int kQgLd = 40;     // LDS row stride in 16-bit elements (80 bytes)

@@ -18,7 +18,21 @@
 #include <string>
 #include <vector>
 
+#include "kargs.h"
 #include "tiles.h"
+
+using vtb::AddNormArgs;
+using vtb::AppendArgs;
+using vtb::CopyArgs;
+using vtb::DecodeArgs;
+using vtb::EltArgs;
+using vtb::GemvArgs;
+using vtb::PrefillArgs;
+using vtb::QGemmArgs;
+using vtb::RmsNormArgs;
+using vtb::RopeRowsArgs;
+using vtb::VtArgs;
+using vtb::XSplitArgs;
 
 extern "C" {
 // Code objects embedded by blobs.S (.incbin of the hipcc --genco outputs).
@@ -41,71 +55,10 @@ const int kKvBytes[kNumKv] = {4, 2, 2};
 
 int d_index(size_t d) { return d == 64 ? 0 : d == 128 ? 1 : d == 256 ? 2 : -1; }
 
-// Arguments of vtb_decode_* (layout must match DecodeArgs in decode.hip).
-struct DecodeArgs {
-  const float* q;
-  const void* k;
-  const void* v;
-  float* out;
-  float* ws_o;
-  float* ws_ml;
-  float* wg_o;
-  float* wg_ml;
-  unsigned* counters;
-  int n_heads;
-  int n_kv;
-  int n_splits;
-  int rows_per_split;
-  long long pos0;
-  long long window;
-  float scale_log2;
-  int pad;
-  const float* k_new;
-  const float* v_new;
-  const float* rope_inv_freq;
-  long long rope_pos;
-  int rope_half;
-  int pad2;
-};
 
-// Arguments of vtb_prefill_* / vtb_vt_* (layouts must match prefill.hip).
-struct PrefillArgs {
-  const void* q;
-  const void* k;
-  const void* vt;
-  float* out;
-  int n_q;
-  int n_heads;
-  int n_kv;
-  int vt_ld;
-  long long pos0;
-  long long window;
-  float scale_log2;
-  int pad1;
-};
 
-struct VtArgs {
-  const void* v;
-  void* vt;
-  int n_rows;
-  int n_kv;
-  int vt_ld;
-  int pad;
-};
 
-struct AppendArgs {
-  void* dst;
-  const float* src;
-  long long n;
-  int vec;
-  int pad;
-};
 
-struct CopyArgs {
-  float* dst;
-  const float* src;
-  long long n;
-};
 
 }  // namespace
 
@@ -117,55 +70,7 @@ constexpr size_t kQuantBlockElems[kNumQuant] = {32, 256, 256, 256};
 constexpr int kNumGemvR = 3;
 constexpr int kGemvRs[kNumGemvR] = {1, 2, 4};
 
-// Arguments of vtb_gemv_* (layout must match gemv.hip).
-struct GemvArgs {
-  const void* w;
-  const float* x;
-  float* out;
-  unsigned w_bytes;
-  int m;
-  int k;
-  int row_bytes;
-  int nblk;
-  int wg1, wg2;
-  const void* w1;
-  float* out1;
-  unsigned w_bytes1;
-  int m1;
-  const void* w2;
-  float* out2;
-  unsigned w_bytes2;
-  int m2;
-  int gated;
-  int pad;
-};
 
-// Mirrors vtb::XSplitArgs / vtb::QGemmArgs (kernels/qgemm.hip).
-struct XSplitArgs {
-  const float* x;
-  uint16_t* planes;
-  float* sums;
-  float* inv_scale;
-  int B;
-  int Bp;
-  int k;
-  int pad;
-};
-struct QGemmArgs {
-  const void* w;
-  const uint16_t* planes;
-  const float* sums;
-  const float* inv_scale;
-  float* out;
-  unsigned w_bytes;
-  int m;
-  int k;
-  int B;
-  int Bp;
-  int row_bytes;
-  int n_rb;
-  int n_tb;
-};
 
 struct VtbHipCtx {
   int device = 0;
@@ -520,7 +425,7 @@ int launch_gemv_blocks(VtbHipCtx* ctx, int qk, int nblk, float* const outs[], co
   auto wbytes = [&](size_t rows) { return (unsigned)((rows * row_bytes + 3) & ~(size_t)3); };
   GemvArgs a;
   memset(&a, 0, sizeof a);
-  a.w = ws[0];
+  a.w = (const uint8_t*)ws[0];
   a.x = x;
   a.out = outs[0];
   a.w_bytes = wbytes(ms[0]);
@@ -531,12 +436,12 @@ int launch_gemv_blocks(VtbHipCtx* ctx, int qk, int nblk, float* const outs[], co
   size_t grid = (ms[0] + R - 1) / R;
   if (nblk > 1) {
     a.wg1 = (int)grid;
-    a.w1 = ws[1], a.out1 = outs[1], a.w_bytes1 = wbytes(ms[1]), a.m1 = (int)ms[1];
+    a.w1 = (const uint8_t*)ws[1], a.out1 = outs[1], a.w_bytes1 = wbytes(ms[1]), a.m1 = (int)ms[1];
     grid += (ms[1] + R - 1) / R;
   }
   if (nblk > 2) {
     a.wg2 = (int)grid;
-    a.w2 = ws[2], a.out2 = outs[2], a.w_bytes2 = wbytes(ms[2]), a.m2 = (int)ms[2];
+    a.w2 = (const uint8_t*)ws[2], a.out2 = outs[2], a.w_bytes2 = wbytes(ms[2]), a.m2 = (int)ms[2];
     grid += (ms[2] + R - 1) / R;
   }
   const unsigned waves = (unsigned)((k + 2047) / 2048);
@@ -575,7 +480,7 @@ int launch_gemv_gated(VtbHipCtx* ctx, int qk, int act, float* out, const void* w
   const size_t RH = (size_t)kGemvRs[ri] / 2;
   GemvArgs a;
   memset(&a, 0, sizeof a);
-  a.w = w_gate;
+  a.w = (const uint8_t*)w_gate;
   a.x = x;
   a.out = out;
   a.w_bytes = (unsigned)((m * row_bytes + 3) & ~(size_t)3);
@@ -583,7 +488,7 @@ int launch_gemv_gated(VtbHipCtx* ctx, int qk, int act, float* out, const void* w
   a.k = (int)k;
   a.row_bytes = (int)row_bytes;
   a.nblk = 1;
-  a.w1 = w_up;
+  a.w1 = (const uint8_t*)w_up;
   a.w_bytes1 = a.w_bytes;
   a.m1 = (int)m;
   a.gated = act;
@@ -651,7 +556,7 @@ int launch_qgemm_blocks(VtbHipCtx* ctx, int qk, int nblk, float* const outs[], c
   for (int b = 0; b < nblk; ++b) {
     QGemmArgs a;
     memset(&a, 0, sizeof a);
-    a.w = ws[b];
+    a.w = (const uint8_t*)ws[b];
     a.planes = planes;
     a.sums = sums;
     a.inv_scale = inv_scale;
@@ -890,26 +795,6 @@ extern "C" void vtb_hip_segment_copy(VtbHipSeg* seg, VtbHipBuf* dst_buf, size_t 
   seg_note(seg, launch(ctx, ctx->f_copy, (unsigned)((n_floats + 255) / 256), 1, 1, 256, &a));
 }
 
-// Layer ops around the projections (kernels/layer.hip): the Metal bridge's
-// segment encoders rmsnorm / swiglu / gelu_approx / residual_add
-// (src/metal/bridge.h:115-150), which gpuLayerStep (forward.zig:419-513)
-// chains between its matmuls.  f32 arrays of n elements; float4 access when
-// every array is 16-byte aligned, element access otherwise.
-struct RmsNormArgs {
-  float* out;
-  const float* in;
-  const float* w;
-  int n;
-  int n4;
-  float eps;
-  int pad;
-};
-struct EltArgs {
-  float* a;
-  const float* b;
-  int n;
-  int n4;
-};
 
 extern "C" void vtb_hip_segment_rmsnorm_rows(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* in_buf,
                                              VtbHipBuf* weight_buf, size_t weight_offset, size_t n, size_t rows,
@@ -936,15 +821,6 @@ extern "C" void vtb_hip_segment_rmsnorm(VtbHipSeg* seg, VtbHipBuf* out_buf, VtbH
   vtb_hip_segment_rmsnorm_rows(seg, out_buf, in_buf, weight_buf, weight_offset, n, 1, eps);
 }
 
-struct RopeRowsArgs {
-  float* x;
-  const float* inv_freq;
-  long long pos0;
-  int rows;
-  int heads;
-  int head_dim;
-  int half;
-};
 
 extern "C" void vtb_hip_segment_rope_rows(VtbHipSeg* seg, VtbHipBuf* x_buf, size_t rows, size_t n_heads,
                                           size_t head_dim, size_t pos0, float base, int half) {
@@ -961,16 +837,6 @@ extern "C" void vtb_hip_segment_rope_rows(VtbHipSeg* seg, VtbHipBuf* x_buf, size
   seg_note(seg, launch(ctx, ctx->f_rope_rows, (unsigned)((pairs + 255) / 256), 1, 1, 256, &a));
 }
 
-struct AddNormArgs {
-  float* x;
-  const float* b;
-  float* out;
-  const float* w;
-  int n;
-  int n4;
-  float eps;
-  int pad;
-};
 
 extern "C" void vtb_hip_segment_residual_add_rmsnorm(VtbHipSeg* seg, VtbHipBuf* x_buf, VtbHipBuf* b_buf,
                                                      VtbHipBuf* out_buf, VtbHipBuf* weight_buf,
