@@ -257,10 +257,15 @@ void vtb_hip_segment_attn_decode_rope_append(VtbHipSeg *seg, VtbHipBuf *out_buf,
  * pos0+b] of the layer whose row 0 is at layer_offset_bytes in k/v, where
  * window_start follows forward.zig:195-203.  Replaces the per-position loop
  * `for b: attentionCausal` (prefill.zig:193-197, 237-287), which has no Metal
- * counterpart.  q: [n_tokens][n_heads*head_dim]; out: f32, same shape.
- * For f16/bf16 caches q holds that dtype and the kernel runs on MFMA
- * (P is rounded to f16 for the PV product); for f32 caches q is f32 and the
- * exact f32 decode kernel runs per query. */
+ * counterpart.  q: f32 [n_tokens][n_heads*head_dim], as prefill.zig's s.q
+ * (:167-189); out: f32, same shape.  For f16/bf16 caches the kernel runs on
+ * f16 MFMA: each (query, head) row of q is scaled by a power of two and
+ * rounded to f16, K and V are converted to f16 per 64-key tile with a
+ * power-of-two scale where a bf16 tile exceeds f16's range, and P is
+ * rounded to f16 for the PV product; the scales are exact and taken back
+ * out.  For f32 caches the exact f32 decode kernel runs per query.  The
+ * context keeps a prefill scratch of about 2*n_kv*head_dim*(pos0+n_tokens)
+ * bytes (twice that for bf16), grown on demand. */
 void vtb_hip_segment_attn_prefill(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *q_buf,
                                   VtbHipBuf *k_cache_buf, VtbHipBuf *v_cache_buf,
                                   size_t layer_offset_bytes, size_t n_tokens, size_t pos0,
@@ -374,8 +379,8 @@ int vtb_hip_layer_attention_rope(VtbHipSeg *seg, VtbHipKvCache *cache, const Vtb
 /* Prefill, one layer (prefill.zig:174-197): write the n_tokens rows of
  * k_cur/v_cur (f32 [n_tokens][kv_dim]) into slots pos..pos+n_tokens-1, then
  * causal attention for every query (q f32 [n_tokens][n_heads*head_dim]) into
- * attn_out.  For f16/bf16 caches q is rounded to the cache dtype before the
- * MFMA kernel.  Does not advance pos.  3 if pos + n_tokens > max_seq. */
+ * attn_out, exactly as vtb_hip_segment_attn_prefill computes it.  Does not
+ * advance pos.  3 if pos + n_tokens > max_seq. */
 int vtb_hip_prefill_attention(VtbHipSeg *seg, VtbHipKvCache *cache, const VtbHipAttnConfig *c,
                               size_t layer, size_t n_tokens, VtbHipBuf *q, VtbHipBuf *k_cur,
                               VtbHipBuf *v_cur, VtbHipBuf *attn_out);

@@ -485,8 +485,9 @@ def cpu_prefill_layer(x: np.ndarray, lw: LayerWeights, cache: OracleKvCache, c: 
     """prefill.prefillLayer (src/runtime/prefill.zig:151-231) for the B tokens
     of x ([B][dim]) at positions cache.pos .. cache.pos+B-1; returns the new
     x and writes the B K/V rows into the cache.  kv_round, when given, maps
-    the f32 K/V rows (and the queries) to the values a lower-precision cache
-    holds, as the GPU path stores them."""
+    the f32 K/V rows to the values a lower-precision cache holds, as the GPU
+    path stores them; the queries stay f32, as the reference's s.q is
+    (prefill.zig:167-197)."""
     B = x.shape[0]
     n_heads, n_kv, hd = c.n_heads, c.n_kv_heads, c.head_dim
     kv_dim = n_kv * hd
@@ -499,7 +500,7 @@ def cpu_prefill_layer(x: np.ndarray, lw: LayerWeights, cache: OracleKvCache, c: 
         q[b] = rope(q[b], pos0 + b, rope_base, rope_half)
         k[b] = rope(k[b], pos0 + b, rope_base, rope_half)
     if kv_round is not None:
-        k, v, q = kv_round(k), kv_round(v), kv_round(q)
+        k, v = kv_round(k), kv_round(v)
     for b in range(B):
         cache.pos = pos0 + b
         cache.key_slot(layer)[:] = k[b].reshape(-1)

@@ -53,14 +53,17 @@ TINY = [
 
 
 def tiny_inputs(n_heads, n_kv, d, dtype, n_rows, n_tokens, seed):
+    """Seeded inputs of a tiny case: (q, q, k stored, k exact, v stored,
+    v exact).  The queries are f32 for every cache dtype, as the reference's
+    State.q / s.q are (forward.zig:37, prefill.zig:167-197); only the cache
+    rows take the cache dtype.  q is returned twice so callers can unpack the
+    stored/exact pairs uniformly."""
     k = orc.normal(seed * 10 + 1, n_rows * n_kv * d).reshape(n_rows, n_kv, d)
     v = orc.normal(seed * 10 + 2, n_rows * n_kv * d).reshape(n_rows, n_kv, d)
     q = orc.normal(seed * 10 + 3, n_tokens * n_heads * d).reshape(n_tokens, n_heads * d)
     ks, kx = orc.to_dtype(k, dtype)
     vs, vx = orc.to_dtype(v, dtype)
-    qs, qx = orc.to_dtype(q, dtype)
-    return (qs.reshape(q.shape), qx.reshape(q.shape), ks.reshape(k.shape), kx.reshape(k.shape),
-            vs.reshape(v.shape), vx.reshape(v.shape))
+    return (q, q, ks.reshape(k.shape), kx.reshape(k.shape), vs.reshape(v.shape), vx.reshape(v.shape))
 
 
 def tiny_output(case):

@@ -29,7 +29,7 @@ class Buf:
 
 class Scratch:
     def __init__(self, B=1):
-        for n in ("x", "xb", "xb2", "q", "q_dt", "k_cur", "v_cur", "attn_out", "gate", "up", "ffn_out", "logits"):
+        for n in ("x", "xb", "xb2", "q", "k_cur", "v_cur", "attn_out", "gate", "up", "ffn_out", "logits"):
             setattr(self, n, Buf(n))
         self.B = B
 
@@ -90,18 +90,27 @@ def test_prefill_layer_order():
     gpu_prefill_layer(seg, Scratch(B=8), Buf("w"), _off(), Buf("k"), Buf("v"), C, 0, 4)
     names = [n for n, _ in seg.calls]
     assert names == ["rmsnorm_rows", "matmul_batched3", "rope_rows", "rope_rows", "kv_append", "kv_append",
-                     "kv_append", "attn_prefill", "matmul_batched", "residual_add", "rmsnorm_rows",
+                     "attn_prefill", "matmul_batched", "residual_add", "rmsnorm_rows",
                      "matmul_batched3", "swiglu", "matmul_batched", "residual_add"]
+    # the queries reach the attention as the f32 s.q (prefill.zig:167-197)
+    assert dict(seg.calls)["attn_prefill"][1].name == "q"
 
 
 def test_guards():
+    """Every guard raises before the first launch is encoded: a bad config
+    leaves the segment, the residual stream and the cache untouched."""
     bad = LayerConfig(dim=200, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, max_seq=32)
-    with pytest.raises(ValueError):
-        gpu_layer_step(Recorder(), Scratch(), Buf("w"), _off(), Buf("k"), Buf("v"), bad, 0, 0)
-    with pytest.raises(ValueError):
-        gpu_token_step(Recorder(), Scratch(), Buf("w"), [_off()], Buf("k"), Buf("v"), C, 32, 0, 0, "q8_0", 7)
-    with pytest.raises(ValueError):
-        gpu_prefill_layer(Recorder(), Scratch(B=30), Buf("w"), _off(), Buf("k"), Buf("v"), C, 0, 4)  # past max_seq
-    with pytest.raises(ValueError):
-        c = LayerConfig(dim=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, max_seq=32, activation="relu")
-        gpu_layer_step(Recorder(), Scratch(), Buf("w"), _off(), Buf("k"), Buf("v"), c, 0, 0)
+    relu = LayerConfig(dim=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, max_seq=32, activation="relu")
+    cases = [
+        lambda seg: gpu_layer_step(seg, Scratch(), Buf("w"), _off(), Buf("k"), Buf("v"), bad, 0, 0),
+        lambda seg: gpu_token_step(seg, Scratch(), Buf("w"), [_off()], Buf("k"), Buf("v"), C, 32, 0, 0, "q8_0", 7),
+        lambda seg: gpu_prefill_layer(seg, Scratch(B=30), Buf("w"), _off(), Buf("k"), Buf("v"), C, 0, 4),
+        lambda seg: gpu_layer_step(seg, Scratch(), Buf("w"), _off(), Buf("k"), Buf("v"), relu, 0, 0),
+        lambda seg: gpu_token_step(seg, Scratch(), Buf("w"), [_off()], Buf("k"), Buf("v"), relu, 0, 0, 0, "q8_0", 7),
+        lambda seg: gpu_prefill_layer(seg, Scratch(B=8), Buf("w"), _off(), Buf("k"), Buf("v"), relu, 0, 0),
+    ]
+    for case in cases:
+        seg = Recorder()
+        with pytest.raises(ValueError):
+            case(seg)
+        assert seg.calls == [], [n for n, _ in seg.calls]

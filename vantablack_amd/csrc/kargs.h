@@ -44,36 +44,80 @@ static_assert(offsetof(DecodeArgs, n_heads) == 72 && offsetof(DecodeArgs, pos0) 
                   offsetof(DecodeArgs, rope_pos) == 136 && offsetof(DecodeArgs, rope_half) == 144,
               "DecodeArgs layout");
 
-// Causal prefill attention (vtb_prefill_*, vtb_prefill8_*).
+// Causal prefill attention (vtb_prefill_d*, vtb_prefill8_d*).  Every MFMA
+// operand is f16: the f32 queries are converted in registers with a
+// power-of-two scale per wave (32 queries of one head); keys come from the
+// conversion pass (or straight from an f16 cache) with a power-of-two
+// exponent per 64-key tile, V^T with one per KV head.  A workgroup takes q
+// and P as two f16 pieces each when its head is flagged by the conversion
+// pass (values with a crest factor above 8) or when the Cauchy-Schwarz
+// bound on its scores, max |q| * max |k| * scale_log2, exceeds 32.
 struct PrefillArgs {
-  const void* q;       // [n_q][n_heads][D] of the cache dtype
-  const void* k;       // layer base: row t at k + t*n_kv*D elements
-  const void* vt;      // f16 V^T from the pre-pass: [n_kv][D][vt_ld]
-  float* out;          // [n_q][n_heads][D] f32
+  const float* q;            // [n_q][n_heads][D] f32 (prefill.zig's s.q)
+  const void* k;             // f16 keys: key t of KV head h at k + h*k_head_stride + t*k_row_stride elements
+  const void* vt;            // f16 V^T from the pre-pass: [n_kv][D][vt_ld]
+  float* out;                // [n_q][n_heads][D] f32
+  const int* kexp;           // [n_kv][vt_ld / 64]: the keys of a tile were scaled by 2^-e; null: 0
+  const int* vexp;           // [n_kv]: the values of a head were scaled by 2^-e; null: 0
+  const int* hflag;          // [n_kv]: 1 = two-piece q and P for this head
+  const float* knorm;        // [n_kv]: largest key-row norm |k_t| of the head
+  long long k_row_stride;    // elements between consecutive keys of one head
+  long long k_head_stride;   // elements between KV heads
+  long long pos0;            // absolute position of query 0
+  long long window;          // sliding window in rows; <= 0 disables it
   int n_q;
   int n_heads;
   int n_kv;
-  int vt_ld;           // keys per V^T row (multiple of BN, >= pos0 + n_q)
-  long long pos0;      // absolute position of query 0
-  long long window;    // sliding window in rows; <= 0 disables it
-  float scale_log2;    // (1/sqrt(D)) * log2(e)
+  int vt_ld;                 // keys per V^T row (multiple of 64, >= pos0 + n_q)
+  float scale_log2;          // (1/sqrt(D)) * log2(e)
   int pad1;
 };
-static_assert(sizeof(PrefillArgs) == 72, "PrefillArgs layout");
-static_assert(offsetof(PrefillArgs, n_q) == 32 && offsetof(PrefillArgs, pos0) == 48 &&
-                  offsetof(PrefillArgs, scale_log2) == 64,
+static_assert(sizeof(PrefillArgs) == 120, "PrefillArgs layout");
+static_assert(offsetof(PrefillArgs, kexp) == 32 && offsetof(PrefillArgs, hflag) == 48 &&
+                  offsetof(PrefillArgs, knorm) == 56 && offsetof(PrefillArgs, k_row_stride) == 64 &&
+                  offsetof(PrefillArgs, pos0) == 80 && offsetof(PrefillArgs, n_q) == 96 &&
+                  offsetof(PrefillArgs, vt_ld) == 108 && offsetof(PrefillArgs, scale_log2) == 112,
               "PrefillArgs layout");
 
-// V^T pre-pass of the prefill (vtb_vt_*).
-struct VtArgs {
-  const void* v;       // layer base: row t at v + t*n_kv*D elements
-  void* vt;            // f16 [n_kv][D][vt_ld]
-  int n_rows;          // rows of V to transpose; keys >= n_rows are zero
+// Prefill statistics pass (vtb_kvstat_*): grid (n_part, n_kv); partition p
+// of KV head h covers rows [p*rows_per_part, +rows_per_part) and writes
+// part[h][p] = {max |K|, max |V|, sum K^2, sum V^2, max row |k_t|^2, 0, 0, 0}
+// as f32.
+struct KvStatArgs {
+  const void* k;       // layer base: row t at k + t*n_kv*D elements
+  const void* v;
+  float* part;         // [n_kv][n_part][8]
+  int n_rows;
   int n_kv;
-  int vt_ld;
+  int rows_per_part;
   int pad;
 };
-static_assert(sizeof(VtArgs) == 32 && offsetof(VtArgs, n_rows) == 16, "VtArgs layout");
+static_assert(sizeof(KvStatArgs) == 40 && offsetof(KvStatArgs, n_rows) == 24, "KvStatArgs layout");
+
+// Prefill conversion pass (vtb_kvt_*): one workgroup per (64-key tile, KV
+// head).  V^T as f16 (keys permuted inside each 16-key group) and, for bf16
+// caches, the keys as f16.  A bf16 key tile is scaled by the power of two
+// 2^-e that brings its largest magnitude into [2^14, 2^15) (e to kexp); a
+// bf16 head's values likewise by one exponent per head (e to vexp).  From
+// the statistics pass's partials it also flags the heads whose values have
+// a crest factor (max / rms) above 8 (hflag) and records the largest
+// key-row norm (knorm).
+struct KvtArgs {
+  const void* k;         // layer base: row t at k + t*n_kv*D elements
+  const void* v;
+  void* k16;             // bf16 caches: f16 keys [n_kv][vt_ld][D]; null for f16 caches
+  void* vt;              // f16 [n_kv][D][vt_ld]
+  const float* part;     // the statistics pass's [n_kv][n_part][8]
+  int* kexp;             // bf16 caches: [n_kv][vt_ld / 64]; null for f16 caches
+  int* vexp;             // bf16 caches: [n_kv]; null for f16 caches
+  int* hflag;            // [n_kv]
+  float* knorm;          // [n_kv]
+  int n_rows;            // rows of K/V to convert; keys >= n_rows are zero
+  int n_kv;
+  int vt_ld;
+  int n_part;            // 1 .. 64
+};
+static_assert(sizeof(KvtArgs) == 88 && offsetof(KvtArgs, n_rows) == 72, "KvtArgs layout");
 
 // KV-slot append (vtb_kv_append_*).
 struct AppendArgs {

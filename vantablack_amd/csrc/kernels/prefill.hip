@@ -6,16 +6,34 @@
 //   out[b,h] = sum_t softmax_t(q[b,h].K[t,kv_h] / sqrt(D)) V[t,kv_h]
 // over t in [window_start(pos0+b), pos0+b], kv_h = (h*n_kv)/n_heads.
 //
-// Two kernels per call:
-//   vtb_vt_<dt>_d<D>       V pre-pass: writes V^T as f16, [kv_h][d][key],
-//                          keys permuted inside each 16-key group (vt_col),
-//                          zero-padded to a whole number of key tiles.  A bf16
-//                          V is converted to f16 here (exact for |v| in f16's
-//                          normal range).  One pass over V: ~5 us at 8K keys.
-//   vtb_prefill_<dt>_d<D>  flash attention, transposed so that every lane
+// Kernels per call:
+//   vtb_kvstat_<dt>_d<D>   statistics pass: the largest |K| and |V| and the
+//                          sums of squares of each KV head over keys
+//                          [0, pos0 + n_q), as up to 64 partials per head.
+//   vtb_kvt_<dt>_d<D>      conversion pass, one workgroup per (64-key tile,
+//                          KV head): V^T as f16, [kv_h][d][key], keys
+//                          permuted inside each 16-key group (vt_col),
+//                          zero-padded to whole tiles; for bf16 caches also
+//                          the keys as f16 [kv_h][key][d].  bf16 values are
+//                          scaled by the power of two 2^-e that brings the
+//                          head's largest |V| into [2^14, 2^15), and each
+//                          bf16 key tile likewise by its own: exact for every
+//                          value within 2^29 of that maximum (f16's normal
+//                          range holds every 8-bit bf16 mantissa), whatever
+//                          the absolute range; the exponents go to vexp /
+//                          kexp.  f16 caches are f16 already.  A head whose
+//                          keys or values have a crest factor (max / rms)
+//                          above 8 is flagged (hflag) for the two-piece path.
+//   vtb_prefill_d<D>       flash attention, transposed so that every lane
 //                          owns one query:
-//     S^T = K Q^T          v_mfma_f32_32x32x16_{bf16,f16}; A = K rows from LDS,
-//                          B = Q^T kept in registers for the whole key loop.
+//     q                    read as f32 (prefill.zig's s.q), scaled per wave
+//                          (32 queries of one head) by the power of two that
+//                          brings the largest magnitude into [2^14, 2^15),
+//                          rounded to f16 (11 significant bits); the score
+//                          multiplier takes the scales of q and K back.
+//     S^T = K Q^T          v_mfma_f32_32x32x16_f16; A = K rows from LDS,
+//                          B = Q^T kept in registers for the whole key loop;
+//                          the tile's key exponent joins the score multiplier.
 //     online softmax       the 32x32 accumulator puts one query per lane
 //                          column (lane % 32) and 16 keys per lane, so the row
 //                          max / sum need one cross-lane step (lane ^ 32).
@@ -26,9 +44,17 @@
 //     O^T += V^T P^T       v_mfma_f32_32x32x16_f16; B = P^T straight from the
 //                          S^T accumulators (rounded to f16), A = V^T from LDS.
 //                          The pre-pass permutation makes the 8 keys a lane
-//                          holds in P^T 8 contiguous f16 of a V^T row.
+//                          holds in P^T 8 contiguous f16 of a V^T row.  The
+//                          value scale comes back out with the final 1/l.
 // P is rounded to f16 (11 significant bits; bf16's 8 bits would give ~2e-3
 // relative error, at the parity bar).
+//
+// Precision.  With 11-bit q and P the output error grows with the crest
+// factor of K (q's rounding error is weighted by |k|) and of V (P's rounding
+// error is weighted by |v - out|).  N(0,1) data (crest ~5) stays near 7e-4
+// of max|out|; channel outliers x20 (crest ~27) reach ~7e-3.  Flagged heads
+// therefore enter q and P as two f16 pieces each (hi + lo, 22 significant
+// bits): twice the MFMA work for those heads only, the error below 1e-4.
 //
 // Workgroup = 4 waves x 32 queries = 128 queries of one head; key tiles of BN
 // rows stream through LDS (K row-major, V^T row-major, both padded so the
@@ -42,25 +68,9 @@ namespace vtb {
 
 
 
-template <typename DT> struct Mfma;
-template <> struct Mfma<kv_bf16> {
-  typedef bf16x8 frag;
-  __device__ static inline f32x16 qk(frag a, frag b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-  }
-  // bf16 bits -> f16 value (via the exact f32 upcast).
-  __device__ static inline _Float16 to_f16(uint16_t bits) {
-    return (_Float16)__builtin_bit_cast(float, (uint32_t)bits << 16);
-  }
-};
-template <> struct Mfma<kv_f16> {
-  typedef f16x8 frag;
-  __device__ static inline f32x16 qk(frag a, frag b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-  }
-  __device__ static inline _Float16 to_f16(uint16_t bits) { return __builtin_bit_cast(_Float16, bits); }
-};
-
+__device__ inline f32x16 mfma_qk(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
 __device__ inline f32x16 mfma_pv(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
@@ -85,28 +95,217 @@ __device__ inline void lane_halves(float v, float& lo_half, float& hi_half) {
 }
 
 // ---------------------------------------------------------------- pre-pass
-template <typename DT, int D>
-__device__ __forceinline__ void vt_body(const VtArgs& a) {
-  constexpr int TK = 64;            // keys per workgroup
-  constexpr int TP = D + 8;         // LDS pitch (f16)
-  __shared__ __attribute__((aligned(16))) _Float16 tile[TK * TP];
-  const int tid = threadIdx.x;
-  const int kvh = blockIdx.y;
-  const long long key0 = (long long)blockIdx.x * TK;
-  const long long row_stride = (long long)a.n_kv * D;
-  const uint16_t* vg = (const uint16_t*)a.v + (long long)kvh * D;
-  // Load 64 keys x D dims (16-byte chunks), convert to f16, stage row-major.
-  for (int c = tid; c < TK * D / 8; c += 256) {
-    const int key = c / (D / 8), dc = (c % (D / 8)) * 8;
-    u32x4 w = {0u, 0u, 0u, 0u};
-    if (key0 + key < a.n_rows) w = load16(vg + (key0 + key) * row_stride + dc);
-    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-    f16x8 h;
+// Power-of-two scaling.  scale_exp(m) is the e for which m * 2^-e lies in
+// [2^14, 2^15), from the biased exponent of the magnitude m, clamped to
+// [-100, 114] (m = 0 or an f32 subnormal gives 0; NaN or inf give 114 and stay
+// NaN / inf); pow2f(e) = 2^e for -126 <= e <= 127.
+__device__ inline int scale_exp(float m) {
+  const int be = (int)((__builtin_bit_cast(uint32_t, m) >> 23) & 0xffu);
+  if (be == 0) return 0;
+  const int e = be - 127 - 14;
+  return e < -100 ? -100 : e;
+}
+__device__ inline float pow2f(int e) { return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23); }
+
+// Largest |x| of the eight bf16 values of w, as bf16 magnitude bits.
+__device__ inline uint32_t bf16x8_absmax(u32x4 w) {
+  uint32_t m = 0;
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = Mfma<DT>::to_f16((uint16_t)(ww[e >> 1] >> (16 * (e & 1))));
-    *reinterpret_cast<f16x8*>(&tile[key * TP + dc]) = h;
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = ww[i] & 0x7fffu, hi = (ww[i] >> 16) & 0x7fffu;
+    m = m > lo ? m : lo;
+    m = m > hi ? m : hi;
+  }
+  return m;
+}
+
+// Max over the 64 lanes of a wave (every lane gets it).
+__device__ inline float wave_max(float v) {
+  v = fmaxf(v, dpp<DPP_XOR1>(v));
+  v = fmaxf(v, dpp<DPP_XOR2>(v));
+  v = fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp<DPP_MIRROR>(v));
+  v = xor_max<16>(v);
+  return xor_max<32>(v);
+}
+__device__ inline uint32_t wave_max_u16(uint32_t m) {
+  // Magnitude bits in the high half of an f32 keep their order.
+  return __builtin_bit_cast(uint32_t, wave_max(__builtin_bit_cast(float, m << 16))) >> 16;
+}
+
+// |x| maximum over the eight 16-bit values of w; returns their sum of
+// squares.
+template <typename DT>
+__device__ inline float stat8(u32x4 w, float& mx) {
+  float f[8];
+  Unpack<DT>::run(w, f);
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    mx = fmaxf(mx, fabsf(f[e]));
+    ss = fmaf(f[e], f[e], ss);
+  }
+  return ss;
+}
+
+template <typename DT, int D>
+__device__ __forceinline__ void kvstat_body(const KvStatArgs& a) {
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  constexpr int NB = 4;       // K and V load pairs in flight per thread
+  __shared__ float s_p[4][5];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int p = blockIdx.x, kvh = blockIdx.y;
+  const long long r0 = (long long)p * a.rows_per_part;
+  long long r1 = r0 + a.rows_per_part;
+  r1 = r1 < a.n_rows ? r1 : a.n_rows;
+  const long long n_chunks = r1 > r0 ? (r1 - r0) * CPR : 0;
+  const long long row_stride = (long long)a.n_kv * D;
+  const uint16_t* kg = (const uint16_t*)a.k + (long long)kvh * D;
+  const uint16_t* vg = (const uint16_t*)a.v + (long long)kvh * D;
+  float kmx = 0.0f, vmx = 0.0f, kss = 0.0f, vss = 0.0f, kn2 = 0.0f;
+  // Batches of NB independent load pairs per thread (ordinary, cached loads:
+  // the conversion pass reads the same rows next).  Chunks past the range
+  // load chunk 0 and are not counted.
+  for (long long c0 = tid; c0 < n_chunks; c0 += 256LL * NB) {
+    u32x4 kw[NB], vw[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const long long c = c0 + 256LL * i < n_chunks ? c0 + 256LL * i : 0;
+      const long long off = (r0 + c / CPR) * row_stride + (int)(c % CPR) * 8;
+      kw[i] = load16_cached(kg + off);
+      vw[i] = load16_cached(vg + off);
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      // A row's CPR chunks sit in CPR consecutive lanes (256 and 64 are
+      // multiples of CPR), all in range or all out: its |k_t|^2 is their sum.
+      const bool in = c0 + 256LL * i < n_chunks;
+      float kc = stat8<DT>(kw[i], kmx), vc = stat8<DT>(vw[i], vmx);
+      kc = in ? kc : 0.0f;
+      vc = in ? vc : 0.0f;
+      kss += kc;
+      vss += vc;
+      kn2 = fmaxf(kn2, group_sum<CPR>(kc));
+    }
+  }
+  kmx = wave_max(kmx);
+  vmx = wave_max(vmx);
+  kss = group_sum<64>(kss);
+  vss = group_sum<64>(vss);
+  kn2 = wave_max(kn2);
+  if (lane == 0) {
+    s_p[wave][0] = kmx;
+    s_p[wave][1] = vmx;
+    s_p[wave][2] = kss;
+    s_p[wave][3] = vss;
+    s_p[wave][4] = kn2;
   }
   __syncthreads();
+  if (tid == 0) {
+    f32x4 r = {0.0f, 0.0f, 0.0f, 0.0f}, r2 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      r[0] = fmaxf(r[0], s_p[i][0]);
+      r[1] = fmaxf(r[1], s_p[i][1]);
+      r[2] += s_p[i][2];
+      r[3] += s_p[i][3];
+      r2[0] = fmaxf(r2[0], s_p[i][4]);
+    }
+    float* dst = a.part + ((long long)kvh * gridDim.x + p) * 8;
+    *reinterpret_cast<f32x4*>(dst) = r;
+    *reinterpret_cast<f32x4*>(dst + 4) = r2;
+  }
+}
+
+template <typename DT, int D>
+__device__ __forceinline__ void kvt_body(const KvtArgs& a) {
+  constexpr int TK = 64;                 // keys per workgroup
+  constexpr int TP = D + 8;              // LDS pitch (16-bit elements)
+  constexpr int CH = TK * D / 8 / 256;   // 16-byte chunks per thread
+  constexpr bool kBf = __is_same(DT, kv_bf16);
+  static_assert(CH * 256 * 8 == TK * D, "tile does not match the workgroup");
+  __shared__ __attribute__((aligned(16))) uint16_t tile[TK * TP];
+  __shared__ uint32_t s_km[4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int kvh = blockIdx.y;
+  const int tix = blockIdx.x;
+  const long long key0 = (long long)tix * TK;
+  const long long row_stride = (long long)a.n_kv * D;
+  const uint16_t* vg = (const uint16_t*)a.v + (long long)kvh * D;
+  const uint16_t* kg = (const uint16_t*)a.k + (long long)kvh * D;
+  // The head's statistics from the partials (every wave reduces them
+  // itself: at most 64, one per lane): the value scale (bf16), the
+  // precision flag (crest factor max / rms of V above 8) and the largest
+  // key-row norm.
+  float vscale = 1.0f;
+  {
+    f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f}, st2 = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (lane < a.n_part) {
+      st = *reinterpret_cast<const f32x4*>(a.part + ((long long)kvh * a.n_part + lane) * 8);
+      st2 = *reinterpret_cast<const f32x4*>(a.part + ((long long)kvh * a.n_part + lane) * 8 + 4);
+    }
+    const float vmx = wave_max(st[1]), vss = group_sum<64>(st[3]), kn2 = wave_max(st2[0]);
+    if constexpr (kBf) {
+      const int ev = scale_exp(vmx);
+      vscale = pow2f(-ev);
+      if (tix == 0 && tid == 0) a.vexp[kvh] = ev;
+    }
+    if (tix == 0 && tid == 0) {
+      // crest^2 = max^2 * count / sum v^2, in f64 (no overflow for any f32).
+      const double cnt = (double)a.n_rows * D;
+      a.hflag[kvh] = (double)vmx * vmx * cnt > 64.0 * (double)vss ? 1 : 0;
+      a.knorm[kvh] = sqrtf(kn2);
+    }
+  }
+  // 64 keys x D dims of V into LDS row-major as they are; for bf16 the same
+  // chunks of K, kept in registers until the tile's key exponent is known.
+  u32x4 kw[CH];
+  uint32_t kmx = 0;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int c = tid + 256 * i;
+    const int key = c / (D / 8), dc = (c % (D / 8)) * 8;
+    const bool in = key0 + key < a.n_rows;
+    u32x4 w = {0u, 0u, 0u, 0u};
+    if (in) w = load16(vg + (key0 + key) * row_stride + dc);
+    *reinterpret_cast<u32x4*>(&tile[key * TP + dc]) = w;
+    if constexpr (kBf) {
+      u32x4 kk = {0u, 0u, 0u, 0u};
+      if (in) kk = load16(kg + (key0 + key) * row_stride + dc);
+      kw[i] = kk;
+      const uint32_t m = bf16x8_absmax(kk);
+      kmx = kmx > m ? kmx : m;
+    }
+  }
+  if constexpr (kBf) {
+    const uint32_t m = wave_max_u16(kmx);
+    if (lane == 0) s_km[wave] = m;
+  }
+  __syncthreads();
+  if constexpr (kBf) {
+    uint32_t km = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) km = km > s_km[i] ? km : s_km[i];
+    const int ek = scale_exp(__builtin_bit_cast(float, km << 16));
+    const float kscale = pow2f(-ek);
+    if (tid == 0) a.kexp[(long long)kvh * (a.vt_ld / TK) + tix] = ek;
+    // f16 keys [kv_h][key][d], scaled by 2^-ek.
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + 256 * i;
+      const int key = c / (D / 8), dc = (c % (D / 8)) * 8;
+      const uint32_t ww[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
+      f16x8 h;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        h[2 * e] = (_Float16)(__builtin_bit_cast(float, ww[e] << 16) * kscale);
+        h[2 * e + 1] = (_Float16)(__builtin_bit_cast(float, ww[e] & 0xffff0000u) * kscale);
+      }
+      *reinterpret_cast<f16x8*>((_Float16*)a.k16 + ((long long)kvh * a.vt_ld + key0 + key) * D + dc) = h;
+    }
+  }
   // Write V^T rows: output column o of a 16-key group holds key vt_col(o).
   for (int c = tid; c < D * TK / 8; c += 256) {
     const int d = c / (TK / 8), o0 = (c % (TK / 8)) * 8;
@@ -114,15 +313,23 @@ __device__ __forceinline__ void vt_body(const VtArgs& a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int o = o0 + e;
-      h[e] = tile[(16 * (o >> 4) + vt_col(o & 15)) * TP + d];
+      const uint16_t bits = tile[(16 * (o >> 4) + vt_col(o & 15)) * TP + d];
+      if constexpr (kBf)
+        h[e] = (_Float16)(__builtin_bit_cast(float, (uint32_t)bits << 16) * vscale);
+      else
+        h[e] = __builtin_bit_cast(_Float16, bits);
     }
     *reinterpret_cast<f16x8*>((_Float16*)a.vt + ((long long)kvh * D + d) * a.vt_ld + key0 + o0) = h;
   }
 }
 
 // ---------------------------------------------------------------- attention
-template <typename DT, int D, int NW>
-__device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
+// X2: q and P enter the MFMAs as two f16 pieces (hi + lo, 22 significant
+// bits), twice the products of the single-piece form.
+template <int D, int NW, bool X2>
+__device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, const int qb, const int kvh,
+                                             const f16x8 (&qf)[D / 16], const f16x8 (&ql)[D / 16],
+                                             const int eq) {
   constexpr int NT = 64 * NW;                 // threads per workgroup
   constexpr int BM = 32 * NW;                 // queries per workgroup (NW waves x 32)
   constexpr int BN = prefill_block_n(D);      // keys per tile
@@ -143,9 +350,12 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
 #define VTB_PF_VB 2
 #endif
   constexpr int KB = NS < VTB_PF_KB ? NS : VTB_PF_KB;  // S^T tiles per K-fragment batch
-  constexpr int VB = ND < VTB_PF_VB ? ND : VTB_PF_VB;  // O^T tiles per V-fragment batch
+  // O^T tiles per V-fragment batch (one in the two-piece form, whose second
+  // q and P pieces take the registers).
+  constexpr int VB = X2 ? 1 : (ND < VTB_PF_VB ? ND : VTB_PF_VB);
   static_assert(NS % KB == 0 && ND % VB == 0, "batches must divide the tiles");
-  typedef typename Mfma<DT>::frag frag;
+  // The register-tight case: the two-piece form of the 4-wave d128 kernel.
+  constexpr bool LATE = X2 && NW == 4 && D == 128;
 
   // Two K and two V^T stages: tile j is read from stage j%2 while tile j+1
   // is written into the other, so one barrier per tile suffices.
@@ -159,24 +369,6 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int hi = lane >> 5;   // lane half
   const int lc = lane & 31;   // lane column: the query this lane owns
-  const int nblk = gridDim.y;
-  int h, qb;
-  {
-    // Workgroups are dispatched round-robin over the 8 XCDs in linear order.
-    // When the heads split evenly, XCD x gets heads [x*hpx, (x+1)*hpx) --
-    // with GQA these share KV heads, so each XCD's L2 holds fewer K/V tiles
-    // -- and every XCD takes its longest (last) query blocks first.
-    const int i = blockIdx.y * gridDim.x + blockIdx.x;
-    if (a.n_heads % 8 == 0) {
-      const int hpx = a.n_heads / 8, j = i / 8;
-      h = (i % 8) * hpx + j % hpx;
-      qb = nblk - 1 - j / hpx;
-    } else {
-      h = blockIdx.x;
-      qb = nblk - 1 - (int)blockIdx.y;
-    }
-  }
-  const int kvh = (int)(((long long)h * a.n_kv) / a.n_heads);
 
   const int m0 = qb * BM;
   const int mq = m0 + wave * 32 + lc;  // this lane's query (may be >= n_q: padding)
@@ -193,8 +385,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   const long long wq_hi = a.pos0 + (m0 + wave * 32 + 31 < a.n_q ? m0 + wave * 32 + 31 : a.n_q - 1);
   const bool wave_live = m0 + wave * 32 < a.n_q;
 
-  const long long row_stride = (long long)a.n_kv * D;  // elements
-  const uint16_t* kg = (const uint16_t*)a.k + (long long)kvh * D;
+  const _Float16* kg = (const _Float16*)a.k + (long long)kvh * a.k_head_stride;
   const _Float16* vtg = (const _Float16*)a.vt + (long long)kvh * D * a.vt_ld;
 
   // Tile staging through registers: thread chunk i of a tile is K row
@@ -208,7 +399,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
       const int c = tid + NT * i;
       long long row = kt0 + c / KCH;
       row = row < kend ? row : kend - 1;
-      kpre[i] = load16_cached(kg + row * row_stride + 8 * (c % KCH));
+      kpre[i] = load16_cached(kg + row * a.k_row_stride + 8 * (c % KCH));
     }
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
@@ -229,21 +420,20 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
     }
   };
 
-  // Q^T fragments (B operand): lane holds Q[mq][16ks + 8hi .. +8].
-  frag qf[KS];
-  {
-    const int mr = mq < a.n_q ? mq : a.n_q - 1;
-    const uint16_t* qp = (const uint16_t*)a.q + ((long long)mr * a.n_heads + h) * D + 8 * hi;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = __builtin_bit_cast(frag, load16_cached(qp + 16 * ks));
-  }
+  // Q^T fragments (B operand) from the entry: qf (and the second pieces ql,
+  // read only by the two-piece form), scaled by 2^-eq.
+  // The head's value exponent (null: 0) and the key-tile exponents of the
+  // pre-pass: a tile's score multiplier is scale_log2 * 2^(eq + ek), the
+  // exponent sum clamped so the product stays a normal f32 (beyond it every
+  // score is ~0 or overflows, as in f32).
+  const int ev = a.vexp ? a.vexp[kvh] : 0;
+  const int* kexp_h = a.kexp ? a.kexp + (long long)kvh * (a.vt_ld >> 6) : nullptr;
 
   f32x16 o[ND];
 #pragma unroll
   for (int i = 0; i < ND; ++i) o[i] = f32x16{};
   float m_ref = -INFINITY;  // running reference max (log2 domain, scaled)
   float l_run = 0.0f;
-  const float sl = a.scale_log2;
   // The window as a 32-bit bound (positions stay below 2^30; a larger or
   // absent window keeps every causal key).
   const int wcap = (a.window > 0 && a.window < (1 << 30)) ? (int)a.window : (1 << 30);
@@ -253,30 +443,47 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
     bool live = wave_live && kt0 <= wq_hi;
     if (a.window > 0 && kt0 + BN - 1 < wq_lo - a.window + 1) live = false;
     if (!live) return;
+    int es = eq + (kexp_h ? kexp_h[kt0 >> 6] : 0);
+    es = es < -120 ? -120 : (es > 120 ? 120 : es);
+    const float sl = a.scale_log2 * pow2f(es);
+
 
     // S^T = K Q^T.  K fragments (row 32nt + lc, chunk 2ks + hi) are read in
-    // batches of KB S^T tiles so their LDS latency overlaps the MFMAs.
+    // batches of KB S^T tiles so their LDS latency overlaps the MFMAs (in
+    // KH parts of the k-steps in the register-tight two-piece form).
+    constexpr int KH = LATE ? 2 : 1;
+    constexpr int KSH = KS / KH;
     const char* kr = kl + lc * KPB + 16 * hi;
     f32x16 s[NS];
 #pragma unroll
     for (int nt = 0; nt < NS; ++nt) s[nt] = f32x16{};
 #pragma unroll
     for (int n0 = 0; n0 < NS; n0 += KB) {
-      u32x4 kf[KS][KB];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
+      for (int k0 = 0; k0 < KS; k0 += KSH) {
+        u32x4 kf[KSH][KB];
 #pragma unroll
-        for (int nb = 0; nb < KB; ++nb)
-          kf[ks][nb] = *reinterpret_cast<const u32x4*>(kr + 32 * (n0 + nb) * KPB + 32 * ks);
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_setprio(1);
+        for (int ks = 0; ks < KSH; ++ks)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
+          for (int nb = 0; nb < KB; ++nb)
+            kf[ks][nb] = *reinterpret_cast<const u32x4*>(kr + 32 * (n0 + nb) * KPB + 32 * (k0 + ks));
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-        for (int nb = 0; nb < KB; ++nb)
-          s[n0 + nb] = Mfma<DT>::qk(__builtin_bit_cast(frag, kf[ks][nb]), qf[ks], s[n0 + nb]);
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_setprio(0);
+        for (int ks = 0; ks < KSH; ++ks)
+#pragma unroll
+          for (int nb = 0; nb < KB; ++nb)
+            s[n0 + nb] = mfma_qk(__builtin_bit_cast(f16x8, kf[ks][nb]), qf[k0 + ks], s[n0 + nb]);
+        if constexpr (X2) {
+#pragma unroll
+          for (int ks = 0; ks < KSH; ++ks)
+#pragma unroll
+            for (int nb = 0; nb < KB; ++nb)
+              s[n0 + nb] = mfma_qk(__builtin_bit_cast(f16x8, kf[ks][nb]), ql[k0 + ks], s[n0 + nb]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+      }
     }
 
     // First V^T batch (dims 0 .. 32VB) for the PV product, in flight during
@@ -330,12 +537,16 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
     }
     const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;  // row masked so far
 
-    f16x8 pf[PS];
+    f16x8 pf[PS], pl[X2 ? PS : 1];
 #pragma unroll
     for (int nt = 0; nt < NS; ++nt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        pf[2 * nt + (r >> 3)][r & 7] = (_Float16)exp2_fast(fmaf(s[nt][r], sl, -m_use));
+      {
+        const float pv = exp2_fast(fmaf(s[nt][r], sl, -m_use));
+        pf[2 * nt + (r >> 3)][r & 7] = (_Float16)pv;
+        if constexpr (X2) pl[2 * nt + (r >> 3)][r & 7] = (_Float16)(pv - (float)pf[2 * nt + (r >> 3)][r & 7]);
+      }
     }
     // Row sum over the f16-rounded P, the values the PV MFMAs consume:
     // v_dot2_f32_f16 against (1, 1) adds two of them per instruction.
@@ -348,6 +559,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
       for (int e = 0; e < 8; e += 2) {
         const h2 pr = {pf[i][e], pf[i][e + 1]};
         ls = __builtin_amdgcn_fdot2(pr, ones, ls, false);
+        if constexpr (X2) {
+          const h2 pr2 = {pl[i][e], pl[i][e + 1]};
+          ls = __builtin_amdgcn_fdot2(pr2, ones, ls, false);
+        }
       }
     l_run += ls;
 
@@ -369,6 +584,13 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
 #pragma unroll
         for (int db = 0; db < VB; ++db)
           o[d0 + db] = mfma_pv(__builtin_bit_cast(f16x8, vf[ks][db]), pf[ks], o[d0 + db]);
+      if constexpr (X2) {
+#pragma unroll
+        for (int ks = 0; ks < PS; ++ks)
+#pragma unroll
+          for (int db = 0; db < VB; ++db)
+            o[d0 + db] = mfma_pv(__builtin_bit_cast(f16x8, vf[ks][db]), pl[ks], o[d0 + db]);
+      }
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(0);
     }
@@ -377,7 +599,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   // Key loop, two tiles per trip so each stage is a fixed LDS object.  Per
   // tile: barrier (the stage to read is complete; every wave is done with the
   // other stage), fetch the next tile into registers, compute, then store the
-  // fetched tile into the other stage.
+  // fetched tile into the other stage.  The two-piece form of the 4-wave
+  // d128 kernel fetches after the compute instead (its registers do not
+  // hold the next tile during it), the same barriers in the same order.
   if (kt_first < kend) {
     fetch(kt_first);
     stage(k_lds0, v_lds0);
@@ -385,15 +609,17 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   for (long long kt0 = kt_first; kt0 < kend; kt0 += 2 * BN) {
     __syncthreads();
     const bool more1 = kt0 + BN < kend;
-    if (more1) fetch(kt0 + BN);
+    if (!LATE && more1) fetch(kt0 + BN);
     compute(k_lds0, v_lds0, kt0);
     if (!more1) break;
+    if (LATE) fetch(kt0 + BN);
     stage(k_lds1, v_lds1);
     __syncthreads();
     const bool more2 = kt0 + 2 * BN < kend;
-    if (more2) fetch(kt0 + 2 * BN);
+    if (!LATE && more2) fetch(kt0 + 2 * BN);
     compute(k_lds1, v_lds1, kt0 + BN);
     if (!more2) break;
+    if (LATE) fetch(kt0 + 2 * BN);
     stage(k_lds0, v_lds0);
   }
 
@@ -403,7 +629,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   lane_halves(l_run, l0, l1);
   const float l_tot = l0 + l1;
   if (mq < a.n_q) {
-    const float inv = 1.0f / l_tot;
+    const float inv = (1.0f / l_tot) * pow2f(ev);
     float* op = a.out + ((long long)mq * a.n_heads + h) * D + 4 * hi;
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt) {
@@ -418,35 +644,132 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   }
 }
 
+// Entry: the workgroup's (head, query block), its queries in registers
+// (f32) and its precision path: two f16 pieces for q and P when the head is
+// flagged (values with a crest factor above 8) or when the Cauchy-Schwarz
+// bound on the workgroup's scores in log2 units, max |q| * max |k_t| *
+// scale_log2, exceeds 32 (then q's 11-bit rounding alone could move a score
+// by 2^-7).
+template <int D, int NW>
+__device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
+  constexpr int KS = D / 16;
+  __shared__ float s_qn[NW];
+  const int nblk = gridDim.y;
+  int h, qb;
+  {
+    // Workgroups are dispatched round-robin over the 8 XCDs in linear order.
+    // When the heads split evenly, XCD x gets heads [x*hpx, (x+1)*hpx) --
+    // with GQA these share KV heads, so each XCD's L2 holds fewer K/V tiles
+    // -- and every XCD takes its longest (last) query blocks first.
+    const int i = blockIdx.y * gridDim.x + blockIdx.x;
+    if (a.n_heads % 8 == 0) {
+      const int hpx = a.n_heads / 8, j = i / 8;
+      h = (i % 8) * hpx + j % hpx;
+      qb = nblk - 1 - j / hpx;
+    } else {
+      h = blockIdx.x;
+      qb = nblk - 1 - (int)blockIdx.y;
+    }
+  }
+  const int kvh = (int)(((long long)h * a.n_kv) / a.n_heads);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hi = lane >> 5, lc = lane & 31;
+  const int mq = qb * 32 * NW + wave * 32 + lc;
+  const int mr = mq < a.n_q ? mq : a.n_q - 1;  // padding lanes reuse the last query
+  const float* qp = a.q + ((long long)mr * a.n_heads + h) * D + 8 * hi;
+  // Q^T fragments (B operand): lane holds Q[mq][16ks + 8hi .. +8], read as
+  // f32 and rounded to f16 after scaling by 2^-eq, eq from the largest |q|
+  // of the wave's 32 (query, head) rows (wave-uniform); the score
+  // multiplier takes 2^eq back.  A power-of-two scale is exact for every
+  // value it keeps in f16's normal range.  The second piece lo = f16(x - hi)
+  // makes 22 significant bits for the two-piece form.
+  f16x8 qf[KS], ql[KS];
+  int eq;
+  float n2 = 0.0f;  // |q|^2 of the lane's half row
+  {
+    f32x4 qv[KS][2];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qv[ks][0] = *reinterpret_cast<const f32x4*>(qp + 16 * ks);
+      qv[ks][1] = *reinterpret_cast<const f32x4*>(qp + 16 * ks + 4);
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          mx = fmaxf(mx, fabsf(qv[ks][j][e]));
+          n2 = fmaf(qv[ks][j][e], qv[ks][j][e], n2);
+        }
+    eq = __builtin_amdgcn_readfirstlane(scale_exp(wave_max(mx)));
+    const float qscale = pow2f(-eq);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = qv[ks][j][e] * qscale;
+          qf[ks][4 * j + e] = (_Float16)x;
+          ql[ks][4 * j + e] = (_Float16)(x - (float)qf[ks][4 * j + e]);
+        }
+  }
+  // |q|^2 of the lane's row (the lane pair hi = 0, 1 holds it), max over
+  // the workgroup.
+  float n2lo, n2hi;
+  lane_halves(n2, n2lo, n2hi);
+  const float wn2 = wave_max(n2lo + n2hi);
+  if (lane == 0) s_qn[wave] = wn2;
+  __syncthreads();
+  float qn2 = s_qn[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) qn2 = fmaxf(qn2, s_qn[w]);
+  const bool x2 = (a.hflag && a.hflag[kvh] != 0) ||
+                  (a.knorm && sqrtf(qn2) * a.knorm[kvh] * a.scale_log2 > 32.0f);
+  if (x2)
+    prefill_body<D, NW, true>(a, h, qb, kvh, qf, ql, eq);
+  else
+    prefill_body<D, NW, false>(a, h, qb, kvh, qf, ql, eq);
+}
+
 }  // namespace vtb
 
-#define VTB_PREFILL(DTN, DTT, D)                                                           \
-  extern "C" __global__ __launch_bounds__(256, vtb::prefill_waves_per_simd(D))                  \
-  void vtb_prefill_##DTN##_d##D(vtb::PrefillArgs a) {                                         \
-    vtb::prefill_body<vtb::DTT, D, 4>(a);                                                  \
+// The attention kernels are the same for both cache dtypes (f16 operands);
+// the statistics and conversion passes are per dtype.
+#define VTB_PREFILL(D)                                                                     \
+  extern "C" __global__ __launch_bounds__(256, vtb::prefill_waves_per_simd(D))             \
+  void vtb_prefill_d##D(vtb::PrefillArgs a) {                                              \
+    vtb::prefill_entry<D, 4>(a);                                                           \
+  }
+#define VTB_KVT(DTN, DTT, D)                                                               \
+  extern "C" __global__ __launch_bounds__(256) void vtb_kvt_##DTN##_d##D(vtb::KvtArgs a) { \
+    vtb::kvt_body<vtb::DTT, D>(a);                                                         \
   }                                                                                        \
-  extern "C" __global__ __launch_bounds__(256) void vtb_vt_##DTN##_d##D(vtb::VtArgs a) {   \
-    vtb::vt_body<vtb::DTT, D>(a);                                                          \
+  extern "C" __global__ __launch_bounds__(256) void vtb_kvstat_##DTN##_d##D(vtb::KvStatArgs a) { \
+    vtb::kvstat_body<vtb::DTT, D>(a);                                                      \
   }
 
 // Wide variant (d <= 128): 8 waves x 32 queries share one set of staged
 // K / V^T tiles.  The body needs ~214 VGPRs, so a CU holds one such
 // workgroup: the same 8 waves (2 per SIMD) as two 4-wave workgroups, with
 // each staged byte feeding twice the queries.
-#define VTB_PREFILL_WIDE(DTN, DTT, D)                                                      \
+#define VTB_PREFILL_WIDE(D)                                                                \
   extern "C" __global__ __launch_bounds__(512, 2)                                          \
-  void vtb_prefill8_##DTN##_d##D(vtb::PrefillArgs a) {                                        \
-    vtb::prefill_body<vtb::DTT, D, 8>(a);                                                  \
+  void vtb_prefill8_d##D(vtb::PrefillArgs a) {                                             \
+    vtb::prefill_entry<D, 8>(a);                                                           \
   }
 
-VTB_PREFILL_WIDE(bf16, kv_bf16, 64)
-VTB_PREFILL_WIDE(bf16, kv_bf16, 128)
-VTB_PREFILL_WIDE(f16, kv_f16, 64)
-VTB_PREFILL_WIDE(f16, kv_f16, 128)
-
-VTB_PREFILL(bf16, kv_bf16, 64)
-VTB_PREFILL(bf16, kv_bf16, 128)
-VTB_PREFILL(bf16, kv_bf16, 256)
-VTB_PREFILL(f16, kv_f16, 64)
-VTB_PREFILL(f16, kv_f16, 128)
-VTB_PREFILL(f16, kv_f16, 256)
+VTB_PREFILL_WIDE(64)
+VTB_PREFILL_WIDE(128)
+VTB_PREFILL(64)
+VTB_PREFILL(128)
+VTB_PREFILL(256)
+VTB_KVT(bf16, kv_bf16, 64)
+VTB_KVT(bf16, kv_bf16, 128)
+VTB_KVT(bf16, kv_bf16, 256)
+VTB_KVT(f16, kv_f16, 64)
+VTB_KVT(f16, kv_f16, 128)
+VTB_KVT(f16, kv_f16, 256)

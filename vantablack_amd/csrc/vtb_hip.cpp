@@ -31,7 +31,8 @@ using vtb::PrefillArgs;
 using vtb::QGemmArgs;
 using vtb::RmsNormArgs;
 using vtb::RopeRowsArgs;
-using vtb::VtArgs;
+using vtb::KvStatArgs;
+using vtb::KvtArgs;
 using vtb::XSplitArgs;
 
 extern "C" {
@@ -79,9 +80,10 @@ struct VtbHipCtx {
   hipModule_t mod_decode = nullptr, mod_prefill = nullptr, mod_kvcopy = nullptr, mod_gemv = nullptr,
               mod_qgemm = nullptr;
   hipFunction_t f_decode[kNumKv][kNumD][kNumG] = {};
-  hipFunction_t f_prefill[kNumKv][kNumD] = {};
-  hipFunction_t f_prefill8[kNumKv][kNumD] = {};  // wide (8-wave) variant, d <= 128
-  hipFunction_t f_vt[kNumKv][kNumD] = {};
+  hipFunction_t f_prefill[kNumD] = {};
+  hipFunction_t f_prefill8[kNumD] = {};  // wide (8-wave) variant, d <= 128
+  hipFunction_t f_kvt[kNumKv][kNumD] = {};  // conversion pass per cache dtype (f16, bf16)
+  hipFunction_t f_kvstat[kNumKv][kNumD] = {};  // statistics pass per cache dtype
   hipFunction_t f_append[kNumKv] = {};
   hipFunction_t f_copy = nullptr;
   hipFunction_t f_gemv[kNumQuant][kNumGemvR] = {};  // vtb_gemv_<kind>_r<1|2|4>
@@ -95,12 +97,10 @@ struct VtbHipCtx {
   size_t ws_bytes = 0;
   unsigned* counters = nullptr;
   size_t n_counters = 0;
-  // Prefill query-conversion scratch (f32 -> cache dtype).
-  void* qconv = nullptr;
-  size_t qconv_bytes = 0;
-  // Prefill V^T scratch (f16, written by the vtb_vt_* pre-pass).
-  void* vt = nullptr;
-  size_t vt_bytes = 0;
+  // Prefill scratch written by the vtb_kvt_* pre-pass: f16 V^T, f16 keys
+  // (bf16 caches) and the per-tile multipliers.
+  void* pf = nullptr;
+  size_t pf_bytes = 0;
   // Batched-matmul activation scratch: three bf16 planes [3][Bp][k] and the
   // 16-column sums [Bp][k/16], written by vtb_xsplit.
   void* qg = nullptr;
@@ -316,14 +316,58 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
                 (unsigned)n_q, 64 * vtb::decode_waves(G), &a);
 }
 
-int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const void* q, const void* k, const void* v,
+// Prefill scratch layout for keys [0, vt_ld) of n_kv heads: f16 V^T
+// [n_kv][D][vt_ld], the statistics partials [n_kv][64][8], the precision
+// flags [n_kv] and the key-row norms [n_kv], then (bf16 caches) f16 keys [n_kv][vt_ld][D], the key-tile
+// exponents [n_kv][vt_ld / 64] and the value exponents [n_kv]; sections
+// 256-byte aligned.
+constexpr int kPrefillMaxParts = 64;
+struct PrefillScratch {
+  size_t vt = 0, part = 0, hflag = 0, knorm = 0, k16 = 0, kexp = 0, vexp = 0, bytes = 0;
+};
+PrefillScratch prefill_scratch(size_t n_kv, size_t head_dim, long long vt_ld, int dtype) {
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  PrefillScratch p;
+  const size_t plane = n_kv * head_dim * (size_t)vt_ld * 2;
+  p.vt = 0;
+  p.part = up(plane);
+  p.hflag = p.part + up(n_kv * kPrefillMaxParts * 8 * sizeof(float));
+  p.knorm = p.hflag + up(n_kv * sizeof(int));
+  p.bytes = p.knorm + up(n_kv * sizeof(float));
+  if (dtype == VTB_HIP_BF16) {
+    p.k16 = p.bytes;
+    p.kexp = p.k16 + up(plane);
+    p.vexp = p.kexp + up(n_kv * (size_t)(vt_ld / 64) * sizeof(int));
+    p.bytes = p.vexp + up(n_kv * sizeof(int));
+  }
+  return p;
+}
+
+// Grow a context scratch buffer.  Growth waits for in-flight work first, so
+// a buffer is never freed under a running kernel.
+int ensure_scratch(VtbHipCtx* ctx, void** buf, size_t* have, size_t need, const char* what) {
+  if (need <= *have) return VTB_HIP_OK;
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  if (*buf) HIP_TRY(ctx, hipFree(*buf), "hipFree");
+  *buf = nullptr;
+  *have = 0;
+  HIP_TRY(ctx, hipMalloc(buf, need), what);
+  *have = need;
+  return VTB_HIP_OK;
+}
+
+// MFMA prefill: q is f32 (prefill.zig's s.q); k/v the layer base of an f16
+// or bf16 cache.  A statistics pass and a conversion pass (V^T, the
+// precision flags and, for bf16, the scaled f16 keys) over keys
+// [0, pos0 + n_q), then the attention.
+int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* k, const void* v,
                         size_t n_q, size_t n_heads, size_t n_kv, size_t head_dim, long long pos0,
                         long long window, float inv_sqrt_hd, int dtype) {
   const int di = d_index(head_dim);
   if (di < 0) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "head_dim must be 64, 128 or 256");
   if (dtype != VTB_HIP_F16 && dtype != VTB_HIP_BF16)
     return set_err(ctx, VTB_HIP_EINVAL, "MFMA prefill needs an f16 or bf16 cache");
-  if (!ctx->f_prefill[dtype][di] || !ctx->f_vt[dtype][di])
+  if (!ctx->f_prefill[di] || !ctx->f_kvt[dtype][di] || !ctx->f_kvstat[dtype][di])
     return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prefill kernel not built for this shape");
   if (!aligned16(k) || !aligned16(v) || !aligned16(q))
     return set_err(ctx, VTB_HIP_EINVAL, "q/K/V not 16-byte aligned");
@@ -332,41 +376,73 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const void* q, const void* k
   // prompts keep the 4-wave kernel's parallelism.
   const size_t bm_wide = (size_t)vtb::prefill_block_m_wide;
   const long long wide_min = env_int("VTB_PREFILL_WIDE_MIN_WGS", 2LL * std::max(ctx->cu_count, 1));
-  const bool wide = ctx->f_prefill8[dtype][di] != nullptr &&
+  const bool wide = ctx->f_prefill8[di] != nullptr &&
                     (long long)(n_heads * ((n_q + bm_wide - 1) / bm_wide)) >= wide_min;
   const size_t bm = wide ? bm_wide : (size_t)vtb::prefill_block_m((int)head_dim);
   const size_t nblk = (n_q + bm - 1) / bm;
   if (nblk > 65535 || n_heads > 0x7fffffff) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "grid too large");
-  // V pre-pass: V^T as f16 for keys [0, pos0 + n_q), padded to whole tiles.
+  // Pre-pass over keys [0, pos0 + n_q), padded to whole 64-key tiles.
   const long long n_rows = pos0 + (long long)n_q;
   const long long bn = vtb::prefill_block_n((int)head_dim);
   const long long vt_ld = (n_rows + 63) / 64 * 64;  // multiple of the pre-pass tile and of bn
   // The kernels compare positions in 32-bit arithmetic.
   if (vt_ld % bn != 0 || vt_ld >= (1LL << 30)) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prompt too long");
-  const size_t vt_need = (size_t)n_kv * head_dim * (size_t)vt_ld * 2;
-  if (vt_need > ctx->vt_bytes) {
-    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
-    if (ctx->vt) HIP_TRY(ctx, hipFree(ctx->vt), "hipFree");
-    ctx->vt = nullptr;
-    ctx->vt_bytes = 0;
-    HIP_TRY(ctx, hipMalloc(&ctx->vt, vt_need), "hipMalloc(V^T)");
-    ctx->vt_bytes = vt_need;
+  const PrefillScratch ps = prefill_scratch(n_kv, head_dim, vt_ld, dtype);
+  int rc = ensure_scratch(ctx, &ctx->pf, &ctx->pf_bytes, ps.bytes, "hipMalloc(prefill scratch)");
+  if (rc) return rc;
+  char* base = (char*)ctx->pf;
+  const bool bf = dtype == VTB_HIP_BF16;
+  KvtArgs ka;
+  memset(&ka, 0, sizeof ka);
+  ka.k = k;
+  ka.v = v;
+  ka.vt = base + ps.vt;
+  ka.n_rows = (int)n_rows;
+  ka.n_kv = (int)n_kv;
+  ka.vt_ld = (int)vt_ld;
+  // Statistics pass: about one workgroup per CU over all heads, at most 64
+  // partitions per head.
+  long long n_part = (std::max(ctx->cu_count, 1) + (long long)n_kv - 1) / (long long)n_kv;
+  n_part = std::min<long long>(std::min<long long>(n_part, kPrefillMaxParts), n_rows);
+  KvStatArgs sa;
+  memset(&sa, 0, sizeof sa);
+  sa.k = k;
+  sa.v = v;
+  sa.part = (float*)(base + ps.part);
+  sa.n_rows = (int)n_rows;
+  sa.n_kv = (int)n_kv;
+  sa.rows_per_part = (int)((n_rows + n_part - 1) / n_part);
+  rc = launch(ctx, ctx->f_kvstat[dtype][di], (unsigned)n_part, (unsigned)n_kv, 1, 256, &sa);
+  if (rc) return rc;
+  ka.part = sa.part;
+  ka.hflag = (int*)(base + ps.hflag);
+  ka.knorm = (float*)(base + ps.knorm);
+  ka.n_part = (int)n_part;
+  if (bf) {
+    ka.k16 = base + ps.k16;
+    ka.kexp = (int*)(base + ps.kexp);
+    ka.vexp = (int*)(base + ps.vexp);
   }
-  VtArgs va;
-  memset(&va, 0, sizeof va);
-  va.v = v;
-  va.vt = ctx->vt;
-  va.n_rows = (int)n_rows;
-  va.n_kv = (int)n_kv;
-  va.vt_ld = (int)vt_ld;
-  int rc = launch(ctx, ctx->f_vt[dtype][di], (unsigned)(vt_ld / 64), (unsigned)n_kv, 1, 256, &va);
+  rc = launch(ctx, ctx->f_kvt[dtype][di], (unsigned)(vt_ld / 64), (unsigned)n_kv, 1, 256, &ka);
   if (rc) return rc;
 
   PrefillArgs a;
   memset(&a, 0, sizeof a);
   a.q = q;
-  a.k = k;
-  a.vt = ctx->vt;
+  if (bf) {  // the pre-pass's f16 keys, [n_kv][vt_ld][D]
+    a.k = ka.k16;
+    a.k_row_stride = (long long)head_dim;
+    a.k_head_stride = vt_ld * (long long)head_dim;
+  } else {   // the f16 cache itself, [row][n_kv][D]
+    a.k = k;
+    a.k_row_stride = (long long)(n_kv * head_dim);
+    a.k_head_stride = (long long)head_dim;
+  }
+  a.vt = ka.vt;
+  a.kexp = ka.kexp;
+  a.vexp = ka.vexp;
+  a.hflag = ka.hflag;
+  a.knorm = ka.knorm;
   a.vt_ld = (int)vt_ld;
   a.out = out;
   a.n_q = (int)n_q;
@@ -377,8 +453,8 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const void* q, const void* k
   a.scale_log2 = inv_sqrt_hd * 1.4426950408889634f;
   // x = head (fastest), y = query block: the longest (causal) blocks of every
   // head are dispatched first.
-  return launch(ctx, wide ? ctx->f_prefill8[dtype][di] : ctx->f_prefill[dtype][di], (unsigned)n_heads,
-                (unsigned)nblk, 1, wide ? 512 : 256, &a);
+  return launch(ctx, wide ? ctx->f_prefill8[di] : ctx->f_prefill[di], (unsigned)n_heads, (unsigned)nblk, 1,
+                wide ? 512 : 256, &a);
 }
 
 // Quantised GEMV launcher: out[m] = W[m, k] . x.  One workgroup per R rows
@@ -641,15 +717,20 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
         ok = hipModuleGetFunction(&ctx->f_decode[kv][di][gi], ctx->mod_decode, name) == hipSuccess;
       }
       if (kv != VTB_HIP_F32) {
-        snprintf(name, sizeof name, "vtb_prefill_%s_d%d", kKvNames[kv], D);
-        if (hipModuleGetFunction(&ctx->f_prefill[kv][di], ctx->mod_prefill, name) != hipSuccess)
-          ctx->f_prefill[kv][di] = nullptr;  // shape not built: reported at launch
-        snprintf(name, sizeof name, "vtb_prefill8_%s_d%d", kKvNames[kv], D);
-        if (D > 128 || hipModuleGetFunction(&ctx->f_prefill8[kv][di], ctx->mod_prefill, name) != hipSuccess)
-          ctx->f_prefill8[kv][di] = nullptr;  // not built for d256: the 4-wave kernel runs
-        snprintf(name, sizeof name, "vtb_vt_%s_d%d", kKvNames[kv], D);
-        if (hipModuleGetFunction(&ctx->f_vt[kv][di], ctx->mod_prefill, name) != hipSuccess)
-          ctx->f_vt[kv][di] = nullptr;
+        snprintf(name, sizeof name, "vtb_kvt_%s_d%d", kKvNames[kv], D);
+        if (hipModuleGetFunction(&ctx->f_kvt[kv][di], ctx->mod_prefill, name) != hipSuccess)
+          ctx->f_kvt[kv][di] = nullptr;  // shape not built: reported at launch
+        snprintf(name, sizeof name, "vtb_kvstat_%s_d%d", kKvNames[kv], D);
+        if (hipModuleGetFunction(&ctx->f_kvstat[kv][di], ctx->mod_prefill, name) != hipSuccess)
+          ctx->f_kvstat[kv][di] = nullptr;
+      }
+      if (kv == 0) {
+        snprintf(name, sizeof name, "vtb_prefill_d%d", D);
+        if (hipModuleGetFunction(&ctx->f_prefill[di], ctx->mod_prefill, name) != hipSuccess)
+          ctx->f_prefill[di] = nullptr;
+        snprintf(name, sizeof name, "vtb_prefill8_d%d", D);
+        if (D > 128 || hipModuleGetFunction(&ctx->f_prefill8[di], ctx->mod_prefill, name) != hipSuccess)
+          ctx->f_prefill8[di] = nullptr;  // not built for d256: the 4-wave kernel runs
       }
     }
     if (ok) {
@@ -687,8 +768,7 @@ extern "C" void vtb_hip_destroy(VtbHipCtx* ctx) {
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->ws) (void)hipFree(ctx->ws);
   if (ctx->counters) (void)hipFree(ctx->counters);
-  if (ctx->qconv) (void)hipFree(ctx->qconv);
-  if (ctx->vt) (void)hipFree(ctx->vt);
+  if (ctx->pf) (void)hipFree(ctx->pf);
   if (ctx->qg) (void)hipFree(ctx->qg);
   for (auto& t : ctx->rope_tables) (void)hipFree(t.dev);
   if (ctx->mod_decode) (void)hipModuleUnload(ctx->mod_decode);
@@ -1007,8 +1087,7 @@ extern "C" void vtb_hip_segment_attn_prefill(VtbHipSeg* seg, VtbHipBuf* out_buf,
     return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_prefill: bad shape"));
   if (n_tokens == 0) return;  // prefillCpu returns early for B == 0 (prefill.zig:120)
   const size_t qelems = n_tokens * n_heads * head_dim;
-  const size_t qb = dtype == VTB_HIP_F32 ? 4 : 2;
-  if (!buf_ok(out_buf, 0, qelems * 4) || !buf_ok(q_buf, 0, qelems * qb))
+  if (!buf_ok(out_buf, 0, qelems * 4) || !buf_ok(q_buf, 0, qelems * 4))
     return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_prefill: q/out too small"));
   const size_t rows = pos0 + n_tokens;
   const size_t kv_rows_bytes = rows * n_kv_heads * head_dim * eb;
@@ -1022,7 +1101,8 @@ extern "C" void vtb_hip_segment_attn_prefill(VtbHipSeg* seg, VtbHipBuf* out_buf,
                        bptr(k_cache_buf, layer_offset_bytes), bptr(v_cache_buf, layer_offset_bytes),
                        n_tokens, n_heads, n_kv_heads, head_dim, (long long)pos0, w, inv_sqrt_hd, dtype);
   else
-    rc = launch_prefill_mfma(ctx, (float*)out_buf->ptr, q_buf->ptr, bptr(k_cache_buf, layer_offset_bytes),
+    rc = launch_prefill_mfma(ctx, (float*)out_buf->ptr, (const float*)q_buf->ptr,
+                             bptr(k_cache_buf, layer_offset_bytes),
                              bptr(v_cache_buf, layer_offset_bytes), n_tokens, n_heads, n_kv_heads,
                              head_dim, (long long)pos0, w, inv_sqrt_hd, dtype);
   seg_note(seg, rc);
@@ -1375,21 +1455,9 @@ extern "C" int vtb_hip_prefill_attention(VtbHipSeg* seg, VtbHipKvCache* c, const
                        n_tokens, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, (long long)c->pos, w,
                        inv_sqrt_hd, c->dtype);
   } else if (!rc) {
-    // Round q to the cache dtype into the context's scratch, then MFMA.
-    const size_t need = qn * 2;
-    if (need > ctx->qconv_bytes) {
-      if (hipStreamSynchronize(ctx->stream) != hipSuccess) return set_err(ctx, VTB_HIP_EDEVICE, "sync");
-      if (ctx->qconv) (void)hipFree(ctx->qconv);
-      ctx->qconv = nullptr;
-      ctx->qconv_bytes = 0;
-      if (hipMalloc(&ctx->qconv, need) != hipSuccess) return set_err(ctx, VTB_HIP_EDEVICE, "hipMalloc(qconv)");
-      ctx->qconv_bytes = need;
-    }
-    rc = launch_append(ctx, ctx->qconv, (const float*)q->ptr, qn, c->dtype);
-    if (!rc)
-      rc = launch_prefill_mfma(ctx, (float*)attn_out->ptr, ctx->qconv, bptr(c->k, lo), bptr(c->v, lo), n_tokens,
-                               cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, (long long)c->pos, w,
-                               inv_sqrt_hd, c->dtype);
+    rc = launch_prefill_mfma(ctx, (float*)attn_out->ptr, (const float*)q->ptr, bptr(c->k, lo), bptr(c->v, lo),
+                             n_tokens, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, (long long)c->pos, w,
+                             inv_sqrt_hd, c->dtype);
   }
   seg_note(seg, rc);
   return rc;

@@ -103,11 +103,18 @@ class LayerScratch:
                 b.release()
 
 
-def _check(c: LayerConfig, pos: int):
+ACTIVATIONS = ("silu", "gelu_approx")
+
+
+def _check(c: LayerConfig, pos: int, n_tokens: int = 1):
+    """Every config check, before the first launch is encoded: a bad config
+    leaves the residual stream and the cache untouched."""
     if c.n_heads * c.head_dim != c.dim:
         raise ValueError("n_heads * head_dim must equal dim (as forward.zig:441-510 assumes)")
-    if pos >= c.max_seq:
-        raise ValueError("position beyond max_seq")
+    if c.activation not in ACTIVATIONS:
+        raise ValueError(f"unknown activation {c.activation!r}")
+    if pos + n_tokens > c.max_seq:
+        raise ValueError("position beyond max_seq (KvCacheFull)")
 
 
 def _attention(seg, s, weights, off, kv_k, kv_v, c, layer, pos, grouped=False):
@@ -133,8 +140,6 @@ def _attention(seg, s, weights, off, kv_k, kv_v, c, layer, pos, grouped=False):
 def _ffn(seg, s, weights, off, c, grouped=False):
     """gate/up GEMVs and the gated activation (one gated launch when grouped
     and the two share a format), then the down GEMV into s.ffn_out."""
-    if c.activation not in ("silu", "gelu_approx"):
-        raise ValueError(f"unknown activation {c.activation!r}")
     if grouped and off.kind_gate == off.kind_up:
         # gate/up GEMVs and the activation in one launch, into s.gate
         seg.matmul_gated(off.kind_gate, s.gate, weights, off.wgate, off.wup, s.xb, c.ffn_dim, c.dim, c.activation)
@@ -198,8 +203,7 @@ def gpu_final_step(seg, s: LayerScratch, weights, output_norm_off: int, output_o
 
 class PrefillScratch:
     """Device activations of a B-token prefill (prefill.zig Scratch: x, xb,
-    xb2, q, k_cur, v_cur, attn_out, gate, up, ffn_out), plus the queries in
-    the cache dtype for the MFMA attention."""
+    xb2, q, k_cur, v_cur, attn_out, gate, up, ffn_out)."""
 
     def __init__(self, ctx, c: LayerConfig, B: int):
         kv_dim = c.n_kv_heads * c.head_dim
@@ -209,7 +213,6 @@ class PrefillScratch:
         self.xb = ctx.alloc(B * c.dim * 4)
         self.xb2 = ctx.alloc(B * c.dim * 4)
         self.q = ctx.alloc(B * q_dim * 4)
-        self.q_dt = ctx.alloc(B * q_dim * 2)
         self.k_cur = ctx.alloc(B * kv_dim * 4)
         self.v_cur = ctx.alloc(B * kv_dim * 4)
         self.attn_out = ctx.alloc(B * q_dim * 4)
@@ -218,7 +221,7 @@ class PrefillScratch:
         self.ffn_out = ctx.alloc(B * c.dim * 4)
 
     def release(self):
-        for b in (self.x, self.xb, self.xb2, self.q, self.q_dt, self.k_cur, self.v_cur, self.attn_out, self.gate,
+        for b in (self.x, self.xb, self.xb2, self.q, self.k_cur, self.v_cur, self.attn_out, self.gate,
                   self.up, self.ffn_out):
             b.release()
 
@@ -233,12 +236,8 @@ def gpu_prefill_layer(seg, s: PrefillScratch, weights, off: LayerOffsets, kv_k, 
     caches), O projection + residual, per-token rmsnorm, batched gate/up, the
     activation, batched down projection + residual.  Updates s.x in place."""
     B = s.B
-    if c.n_heads * c.head_dim != c.dim:
-        raise ValueError("n_heads * head_dim must equal dim")
-    if pos0 + B > c.max_seq:
-        raise ValueError("prefill beyond max_seq (KvCacheFull)")
+    _check(c, pos0, B)
     kv_dim = c.n_kv_heads * c.head_dim
-    q_dim = c.n_heads * c.head_dim
     row_bytes = kv_dim * KV_BYTES[c.kv_dtype]
     layer_off = layer * c.max_seq * row_bytes
     seg.rmsnorm_rows(s.xb, s.x, weights, off.attn_norm, c.dim, B, c.rms_eps)
@@ -253,12 +252,7 @@ def gpu_prefill_layer(seg, s: PrefillScratch, weights, off: LayerOffsets, kv_k, 
     seg.rope_rows(s.k_cur, B, c.n_kv_heads, c.head_dim, pos0, c.rope_base, c.rope_half)
     seg.kv_append(kv_k, layer_off + pos0 * row_bytes, c.kv_dtype, s.k_cur, 0, B * kv_dim)
     seg.kv_append(kv_v, layer_off + pos0 * row_bytes, c.kv_dtype, s.v_cur, 0, B * kv_dim)
-    if c.kv_dtype == hip.F32:
-        q = s.q
-    else:
-        seg.kv_append(s.q_dt, 0, c.kv_dtype, s.q, 0, B * q_dim)  # f32 -> cache dtype, nearest even
-        q = s.q_dt
-    seg.attn_prefill(s.attn_out, q, kv_k, kv_v, layer_off, B, pos0, c.sliding_window, c.n_heads, c.n_kv_heads,
+    seg.attn_prefill(s.attn_out, s.q, kv_k, kv_v, layer_off, B, pos0, c.sliding_window, c.n_heads, c.n_kv_heads,
                      c.head_dim, 1.0 / math.sqrt(c.head_dim), c.kv_dtype)
     seg.matmul_batched(off.kind_o, s.xb2, weights, off.wo, s.attn_out, c.dim, c.dim, B)
     seg.residual_add(s.x, s.xb2, B * c.dim)
@@ -271,9 +265,7 @@ def gpu_prefill_layer(seg, s: PrefillScratch, weights, off: LayerOffsets, kv_k, 
         seg.matmul_batched(off.kind_up, s.up, weights, off.wup, s.xb, c.ffn_dim, c.dim, B)
     if c.activation == "silu":
         seg.swiglu(s.gate, s.up, B * c.ffn_dim)
-    elif c.activation == "gelu_approx":
-        seg.gelu_approx(s.gate, s.up, B * c.ffn_dim)
     else:
-        raise ValueError(f"unknown activation {c.activation!r}")
+        seg.gelu_approx(s.gate, s.up, B * c.ffn_dim)
     seg.matmul_batched(off.kind_down, s.ffn_out, weights, off.wdown, s.gate, c.dim, c.ffn_dim, B)
     seg.residual_add(s.x, s.ffn_out, B * c.dim)
