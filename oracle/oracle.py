@@ -456,10 +456,12 @@ class LayerWeights:
 
 def cpu_layer_step(x: np.ndarray, lw: LayerWeights, cache: OracleKvCache, c: ConfigC, layer: int, dim: int,
                    ffn_dim: int, rms_eps: float, rope_base: float, rope_half: bool = False,
-                   activation: str = "silu") -> np.ndarray:
+                   activation: str = "silu", kv_round=None) -> np.ndarray:
     """forward.cpuLayerStep (src/runtime/forward.zig:230-288) for one token at
     cache.pos, composed from the restatements above; returns the new x (f32)
-    and writes this token's K/V rows into the cache slot."""
+    and writes this token's K/V rows into the cache slot.  kv_round, when
+    given, maps the f32 K/V row to the values a lower-precision cache holds
+    (the query stays f32, as State.q is)."""
     n_heads, n_kv, hd = c.n_heads, c.n_kv_heads, c.head_dim
     kv_dim = n_kv * hd
     xb = rms_norm(x, lw.attn_norm, rms_eps)
@@ -468,6 +470,8 @@ def cpu_layer_step(x: np.ndarray, lw: LayerWeights, cache: OracleKvCache, c: Con
     v = matmul_quant(lw.kind, lw.wv, xb, kv_dim, dim)
     q = rope(q.reshape(n_heads, hd), cache.pos, rope_base, rope_half).reshape(-1)
     k = rope(k.reshape(n_kv, hd), cache.pos, rope_base, rope_half).reshape(-1)
+    if kv_round is not None:
+        k, v = kv_round(k), kv_round(v)
     cache.key_slot(layer)[:] = k
     cache.value_slot(layer)[:] = v
     attn = cpu_attention(q, cache, c, layer)

@@ -28,11 +28,21 @@ VOCAB = 2048
 TIE_REL = 1e-3
 
 
+_W = {}
+
+
+def _projection(orc, seed, dim):
+    """The seeded VOCAB x dim projection (f64), drawn once per (seed, dim)."""
+    key = (seed, dim)
+    if key not in _W:
+        _W[key] = orc.normal(seed, VOCAB * dim).astype(np.float64).reshape(VOCAB, dim)
+    return _W[key]
+
+
 def downstream_logits(orc, out: np.ndarray, n_rows: int, seed: int = 777) -> np.ndarray:
     """W @ out_row for every row (query), W ~ N(0,1) seeded, in f64."""
     o = np.asarray(out, np.float64).reshape(n_rows, -1)
-    W = orc.normal(seed, VOCAB * o.shape[1]).astype(np.float64).reshape(VOCAB, o.shape[1])
-    return o @ W.T
+    return o @ _projection(orc, seed, o.shape[1]).T
 
 
 def downstream_argmax(orc, out: np.ndarray, n_rows: int, seed: int = 777) -> np.ndarray:

@@ -228,6 +228,73 @@ def test_model_decode_matches_cpu_layer_steps(ctx, orc, variant, path):
             b.release()
 
 
+@pytest.mark.parametrize("kv", ["f16", "bf16"])
+@pytest.mark.parametrize("variant", ["llama_q4_k", "mistral_q8_0_gqa_window"])
+def test_model_decode_half_cache(ctx, orc, variant, kv):
+    """gpu_token_step (grouped GEMVs, fused RoPE + append + attention, fused
+    residual + rmsnorm) over an f16 / bf16 cache -- the bench's full_decode
+    configuration -- against cpu_layer_step with the stored K/V rows rounded
+    to the cache dtype (queries stay f32).  The decode attention computes in
+    f32 on the rounded rows, so the f32 bar holds: 1e-4 of the largest value."""
+    import vantablack_amd as vb
+    from vantablack_amd.layer import LayerConfig, LayerScratch, gpu_token_step
+    dt = vb.F16 if kv == "f16" else vb.BF16
+    if variant == "llama_q4_k":
+        c = LayerConfig(dim=256, n_heads=4, n_kv_heads=4, head_dim=64, ffn_dim=512, max_seq=16, kv_dtype=dt)
+        kind, n_tok = "q4_k", 6
+    else:
+        c = LayerConfig(dim=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn_dim=768, max_seq=16,
+                        sliding_window=4, kv_dtype=dt)
+        kind, n_tok = "q8_0", 8
+    rnd = _f16_round if kv == "f16" else _bf16_round
+    n_layers, vocab = 2, 768
+    kinds = dict({n: kind for n in ("q", "k", "v", "o", "gate", "up", "down")}, out="q8_0")
+    m = TinyModel(orc, c, n_layers, vocab, kinds, seed=len(variant) + 3)
+    wbuf = ctx.to_device(m.blob)
+    kv_bytes = n_layers * c.max_seq * c.n_kv_heads * c.head_dim * 2
+    kk, kvv = ctx.alloc(kv_bytes), ctx.alloc(kv_bytes)
+    s = LayerScratch(ctx, c, vocab)
+    cache = orc.OracleKvCache(n_layers, c.n_kv_heads, c.head_dim, c.max_seq)
+    oc = orc.config(c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq, c.sliding_window)
+    rng = np.random.default_rng(12)
+    try:
+        for pos in range(n_tok):
+            x = rng.standard_normal(c.dim).astype(np.float32)
+            ctx.upload(s.x, x)
+            with ctx.segment() as seg:
+                gpu_token_step(seg, s, wbuf, m.offsets, kk, kvv, c, pos, m.out_norm_off, m.out_off, m.out_kind, vocab)
+            ctx.wait_idle()
+            got_x = ctx.download(s.x, np.float32, c.dim)
+            got_logits = ctx.download(s.logits, np.float32, vocab)
+            cache.pos = pos
+            xr = x
+            for l in range(n_layers):
+                xr = orc.cpu_layer_step(xr, m.oracle_layers[l], cache, oc, l, c.dim, c.ffn_dim, c.rms_eps,
+                                        c.rope_base, c.rope_half, c.activation, kv_round=rnd)
+            xr = orc.rms_norm(xr, m.out_norm, c.rms_eps)
+            logits = orc.matmul_quant(m.out_kind, m.w_out, xr, vocab, c.dim)
+            assert np.max(np.abs(got_x - xr)) <= 1e-4 * np.max(np.abs(xr)), f"{variant} {kv} pos {pos}: x"
+            bar = 1e-4 * np.max(np.abs(logits))
+            assert np.max(np.abs(got_logits - logits)) <= bar, f"{variant} {kv} pos {pos}: logits"
+            top2 = np.sort(logits)[-2:]
+            if top2[1] - top2[0] > bar:
+                assert orc.argmax(got_logits) == orc.argmax(logits), f"{variant} {kv} pos {pos}: argmax"
+        # The appended rows are the cache-dtype rounding of K rows that agree
+        # with the oracle's to f32 summation order: at most one step of the
+        # cache dtype apart.
+        step = 2.0 ** -10 if kv == "f16" else 2.0 ** -7
+        for l in range(n_layers):
+            bits = ctx.download(kk, np.uint16, n_tok * c.n_kv_heads * c.head_dim,
+                                offset=l * c.max_seq * c.n_kv_heads * c.head_dim * 2)
+            got_k = orc.f16_bits_to_f32(bits) if kv == "f16" else orc.bf16_bits_to_f32(bits)
+            ref_k = cache.layer_rows("k", l)[:n_tok].reshape(-1)
+            assert np.all(np.abs(got_k - ref_k) <= step * np.abs(ref_k) + 1e-30), f"{variant} {kv}: layer {l} K rows"
+    finally:
+        s.release()
+        for b in (wbuf, kk, kvv):
+            b.release()
+
+
 # ---------------------------------------------------------------- prefill
 
 @pytest.mark.parametrize("n", [4096, 1003])
@@ -267,14 +334,20 @@ def _bf16_round(a):
     return o.bf16_bits_to_f32(o.f32_to_bf16_bits(np.ascontiguousarray(a, np.float32))).reshape(a.shape)
 
 
+def _f16_round(a):
+    from oracle import oracle as o
+    return o.f16_bits_to_f32(o.f32_to_f16_bits(np.ascontiguousarray(a, np.float32))).reshape(a.shape)
+
+
 @pytest.mark.parametrize("variant", ["llama_q4_k_f32cache", "mistral_q8_0_bf16_window_pos7"])
 def test_model_prefill_matches_cpu_prefill_layers(ctx, orc, variant):
     """Two layers of prefill on the GPU (gpu_prefill_layer: MFMA projections
     and attention, batched RoPE, per-token norms) against
     oracle.cpu_prefill_layer (prefillLayer, prefill.zig:151-231).  Bars: 1e-4 of
     the residual stream's largest value with an f32 cache; 2e-3 with a bf16
-    cache (queries, keys and values rounded to bf16 on both sides; P in f16
-    inside the MFMA attention)."""
+    cache (keys and values rounded to bf16 on both sides, queries f32 on
+    both; f16 MFMA operands, two-piece where this model's large scores call
+    for it)."""
     import vantablack_amd as vb
     from vantablack_amd.layer import LayerConfig, PrefillScratch, gpu_prefill_layer
     if variant == "llama_q4_k_f32cache":
