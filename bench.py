@@ -487,9 +487,11 @@ def bench_full_prefill(ctx, torch, B=8192, reps=2):
     vantablack_amd.layer.gpu_prefill_layer): per layer per-token rmsnorm,
     Q/K/V projections on MFMA, batched RoPE, the K/V rows into a bf16 cache,
     MFMA causal attention, O projection + residual, rmsnorm, gate/up, SwiGLU,
-    down + residual.  Q4_K projections (random blocks, small f16 scales), a
-    distinct weight set per layer (3.9 GB).  Returns ms per prompt from HIP
-    events on the context stream."""
+    down + residual; then, as prefillCpu ends (prefill.zig:143-146), the final
+    rmsnorm and the LM head (128256 x 4096, Q6_K) on the last token's row.
+    Q4_K projections (random blocks, small f16 scales), a distinct weight set
+    per layer (3.9 GB).  Returns ms per prompt from HIP events on the context
+    stream."""
     import numpy as np
     from vantablack_amd import layer as ly
     dim, nh, nkv, hd, ffn, n_layers = 4096, 32, 8, 128, 14336, 32
@@ -524,8 +526,14 @@ def bench_full_prefill(ctx, torch, B=8192, reps=2):
         fn = put(norm)
         offs.append(ly.LayerOffsets(an, o["q"], o["k"], o["v"], o["o"], fn, o["gate"], o["up"], o["down"],
                                     *(["q4_k"] * 7)))
+    vocab = 128256
+    out_norm = put(norm)
+    qb6, qe6 = QUANT_BLOCK["q6_k"]
+    w6 = torch.randint(0, 256, (vocab * dim // qe6, qb6), generator=g, dtype=torch.uint8, device=dev)
+    w6[:, qb6 - 2:] = scale  # Q6_K's f16 d sits at the end of the block
+    out_w = put(w6.reshape(-1))
     blob = torch.cat(tensors)
-    del tensors
+    del tensors, w6
     kc = torch.zeros((n_layers, B, nkv, hd), dtype=torch.bfloat16, device=dev)
     vc = torch.zeros_like(kc)
     x0 = (torch.randn((B, dim), generator=g, device=dev) * 0.1).contiguous()
@@ -533,11 +541,16 @@ def bench_full_prefill(ctx, torch, B=8192, reps=2):
     wb, kb, vb_ = ctx.wrap_tensor(blob), ctx.wrap_tensor(kc), ctx.wrap_tensor(vc)
     xin = ctx.wrap_tensor(x0)
     s = ly.PrefillScratch(ctx, c, B)
+    last = ctx.wrap(s.x.ptr + (B - 1) * dim * 4, dim * 4, keepalive=s.x)
+    logits = ctx.alloc(vocab * 4)
 
     def prompt(seg):
         seg.copy(s.x, 0, xin, 0, B * dim)
         for l in range(n_layers):
             ly.gpu_prefill_layer(seg, s, wb, offs[l], kb, vb_, c, l, 0)
+        # Final RMSNorm + LM head on the last position only (prefill.zig:143-146).
+        seg.rmsnorm(last, last, wb, out_norm, dim, c.rms_eps)
+        seg.matmul_quant("q6_k", logits, wb, out_w, last, vocab, dim)
 
     with ctx.segment() as seg:
         prompt(seg)
@@ -552,10 +565,10 @@ def bench_full_prefill(ctx, torch, B=8192, reps=2):
     ctx.wait_idle()
     torch.cuda.synchronize()
     t = e0.elapsed_time(e1) * 1e-3 / reps
-    proj_flops = 2.0 * B * n_layers * sum(m * k for _, m, k in shapes)
+    proj_flops = 2.0 * B * n_layers * sum(m * k for _, m, k in shapes) + 2.0 * vocab * dim
     attn_flops = n_layers * prefill_flops(B, nh, hd)
     s.release()
-    for b in (wb, kb, vb_, xin):
+    for b in (wb, kb, vb_, xin, last, logits):
         b.release()
     del blob, kc, vc, x0
     torch.cuda.empty_cache()
@@ -794,7 +807,8 @@ def main():
     if fullp:
         line["full_prefill"] = dict(
             workload="Llama-3-8B shapes (32 layers, 32q/8kv heads x d128, ffn 14336), 8192-token prompt, Q4_K "
-                     "projections on MFMA, bf16 KV, MFMA causal attention; every op on the GPU",
+                     "projections on MFMA, bf16 KV, MFMA causal attention, then the final rmsnorm and the "
+                     "128256-row Q6_K LM head on the last token (prefill.zig:143-146); every op on the GPU",
             **fullp)
     if full:
         line["full_decode"] = dict(

@@ -129,3 +129,105 @@ def test_cpu_layer_step_matches_an_f64_layer(orc, activation, half):
             a = 0.5 * g * (1 + np.tanh(np.sqrt(2 / np.pi) * (g + 0.044715 * g ** 3))) * u
         ref = xd + W["down"] @ a
         assert np.max(np.abs(got - ref)) <= 2e-5 * np.max(np.abs(ref)), f"pos {pos}"
+
+
+# ---- The reference's own known-answer tests (src/kernels/math.zig), ported.
+
+def test_rmsnorm_reference_kat(orc):
+    # math.zig:205-215 "rmsNorm: identity weight zeros eps": x = 1..8, w = 1,
+    # eps = 0 against the f32 ss / sqrt formula, within 1e-4.
+    x = np.arange(1, 9, dtype=np.float32)
+    w = np.ones(8, np.float32)
+    ss = np.float32(0)
+    for v in x:
+        ss = np.float32(ss + v * v)
+    inv = np.float32(1.0) / np.sqrt(np.float32(ss / np.float32(8)))
+    ref = x * inv
+    got = orc.rms_norm(x, w, 0.0)
+    assert np.max(np.abs(got - ref)) <= 1e-4
+
+
+def test_geglu_approx_reference_kat(orc):
+    # math.zig:232-241: gelu_approx at known points (the reference's own
+    # high-precision values), up = 1, within 1e-4.  These pin the constants
+    # sqrt(2/pi) and 0.044715, which the odd-symmetry check above cannot.
+    gate = np.array([-2.0, -0.5, 0.0, 0.5, 1.0, 2.0], np.float32)
+    expected = np.array([-0.045402, -0.154286, 0.0, 0.345714, 0.841192, 1.954598], np.float32)
+    got = orc.geglu_approx(gate, np.ones_like(gate))
+    assert np.max(np.abs(got - expected)) <= 1e-4
+
+
+def test_geglu_approx_kat_catches_a_wrong_constant():
+    # A restatement with 0.0447 or sqrt(1/pi) misses the known points by more
+    # than the KAT's 1e-4 at z = 2.
+    z = 2.0
+    def g(c, k):
+        return 0.5 * z * (1 + np.tanh(k * (z + c * z ** 3)))
+    right = g(0.044715, np.sqrt(2 / np.pi))
+    assert abs(right - 1.954598) < 1e-5
+    assert abs(g(0.0447, np.sqrt(2 / np.pi)) - right) > 1e-5 or abs(g(0.044715, np.sqrt(1 / np.pi)) - right) > 1e-4
+    assert abs(g(0.044715, np.sqrt(1 / np.pi)) - right) > 1e-4
+
+
+def test_swiglu_reference_kat(orc):
+    # math.zig:243-250 "swiglu against scalar reference": g / (1 + exp(-g)) * u
+    # in f32, within 1e-5.
+    g = np.array([0.5, -1.0, 2.0, 0.0], np.float32)
+    u = np.array([1.0, 2.0, 0.5, 4.0], np.float32)
+    ref = (g / (np.float32(1.0) + np.exp(-g))) * u
+    got = orc.swiglu(g, u)
+    assert np.max(np.abs(got - ref)) <= 1e-5
+
+
+def test_cpu_prefill_layer_matches_an_f64_layer(orc):
+    """prefillLayer restated (oracle.cpu_prefill_layer) for B tokens after an
+    earlier prompt, with a sliding window, against the same layer written out
+    in f64 with dequantised weights: per-token rmsnorm, batched projections,
+    RoPE at pos0 + b, all B rows written before attention, causal windowed
+    attention, residual, gated FFN (prefill.zig:151-231)."""
+    dim, nh, nkv, ffn, kind = 256, 4, 2, 512, "q4_k"  # Q4_K blocks hold 256 weights
+    hd = dim // nh
+    B, pos0, W = 5, 3, 4
+    rng = np.random.default_rng(17)
+    ws = {n: random_weights(kind, m, k, seed=40 + s) for s, (n, m, k) in enumerate(
+        [("q", dim, dim), ("k", nkv * hd, dim), ("v", nkv * hd, dim), ("o", dim, dim),
+         ("gate", ffn, dim), ("up", ffn, dim), ("down", dim, ffn)])}
+    an = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    fn = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    lw = orc.LayerWeights(kind, an, ws["q"], ws["k"], ws["v"], ws["o"], fn, ws["gate"], ws["up"], ws["down"])
+    Wd = {n: np_dequant(kind, w).astype(np.float64).reshape(-1, k)
+          for (n, w), k in zip(ws.items(), [dim] * 6 + [ffn])}
+    max_seq = pos0 + B + 2
+    cache = orc.OracleKvCache(1, nkv, hd, max_seq)
+    prior_k = rng.standard_normal((pos0, nkv, hd)).astype(np.float32)
+    prior_v = rng.standard_normal((pos0, nkv, hd)).astype(np.float32)
+    cache.layer_rows("k", 0)[:pos0] = prior_k
+    cache.layer_rows("v", 0)[:pos0] = prior_v
+    cache.pos = pos0
+    c = orc.config(nh, nkv, hd, max_seq, W)
+    x = rng.standard_normal((B, dim)).astype(np.float32)
+    got = orc.cpu_prefill_layer(x, lw, cache, c, 0, dim, ffn, 1e-5, 10000.0, False, "silu")
+    xd = x.astype(np.float64)
+    h = xd * an / np.sqrt(np.mean(xd * xd, axis=1, keepdims=True) + 1e-5)
+    q = np.stack([_rope_f64((Wd["q"] @ h[b]).reshape(nh, hd), pos0 + b, 10000.0, False) for b in range(B)])
+    k = np.stack([_rope_f64((Wd["k"] @ h[b]).reshape(nkv, hd), pos0 + b, 10000.0, False) for b in range(B)])
+    v = np.stack([(Wd["v"] @ h[b]).reshape(nkv, hd) for b in range(B)])
+    K = np.concatenate([prior_k.astype(np.float64), k])
+    V = np.concatenate([prior_v.astype(np.float64), v])
+    att = np.zeros((B, nh, hd))
+    for b in range(B):
+        cur = pos0 + b
+        ws0 = 0 if cur < W else cur - W + 1
+        for hh in range(nh):
+            kv = hh * nkv // nh
+            s = K[ws0:cur + 1, kv] @ q[b, hh] / np.sqrt(hd)
+            p = np.exp(s - s.max())
+            att[b, hh] = (p / p.sum()) @ V[ws0:cur + 1, kv]
+    xd = xd + att.reshape(B, -1) @ Wd["o"].T
+    h = xd * fn / np.sqrt(np.mean(xd * xd, axis=1, keepdims=True) + 1e-5)
+    g, u = h @ Wd["gate"].T, h @ Wd["up"].T
+    ref = xd + (g / (1 + np.exp(-g)) * u) @ Wd["down"].T
+    assert np.max(np.abs(got - ref)) <= 2e-5 * np.max(np.abs(ref))
+    # The B rows landed in the cache at pos0.. before the attention read them.
+    rows = cache.layer_rows("k", 0)[pos0:pos0 + B]
+    assert np.max(np.abs(rows - k)) <= 2e-5 * np.max(np.abs(k))

@@ -129,6 +129,16 @@ struct AppendArgs {
 };
 static_assert(sizeof(AppendArgs) == 32 && offsetof(AppendArgs, n) == 16, "AppendArgs layout");
 
+// Fill (vtb_fill_u32): dst[i] = value for i < n.  Clears counters with a
+// kernel rather than hipMemsetAsync, which some callers cannot capture.
+struct FillArgs {
+  uint32_t* dst;
+  long long n;
+  uint32_t value;
+  int pad;
+};
+static_assert(sizeof(FillArgs) == 24 && offsetof(FillArgs, value) == 16, "FillArgs layout");
+
 // Plain f32 copy (vtb_copy_f32).
 struct CopyArgs {
   float* dst;

@@ -211,9 +211,15 @@ __device__ inline void buffer_load8_coherent(__amdgpu_buffer_rsrc_t r, int off, 
 __device__ inline void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Gated activations of the FFN (math.zig:154-175): silu(z) * u and the
-// tanh-approximate gelu(z) * u, in the reference's operation order.
-__device__ inline float silu_mul(float z, float u) { return z / (1.0f + expf(-z)) * u; }
+// tanh-approximate gelu(z) * u, in the reference's operation order with no
+// contraction into FMAs (hipcc contracts a*b+c by default; Zig's f32 does
+// not).
+__device__ inline float silu_mul(float z, float u) {
+#pragma clang fp contract(off)
+  return z / (1.0f + expf(-z)) * u;
+}
 __device__ inline float gelu_approx_mul(float z, float u) {
+#pragma clang fp contract(off)
   const float inner = 0.7978845608028654f * (z + 0.044715f * z * z * z);
   return 0.5f * z * (1.0f + tanhf(inner)) * u;
 }

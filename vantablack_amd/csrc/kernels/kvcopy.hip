@@ -9,6 +9,7 @@
 // so one launch writes them all (prefill.zig:175-191).
 //
 // vtb_copy_f32: dst[i] = src[i], the plain Metal copy_f32.
+// vtb_fill_u32: dst[i] = value (clears counters).
 #include "common.h"
 
 namespace vtb {
@@ -60,4 +61,9 @@ extern "C" __global__ __launch_bounds__(256) void vtb_kv_append_bf16(vtb::Append
 extern "C" __global__ __launch_bounds__(256) void vtb_copy_f32(vtb::CopyArgs a) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < a.n) a.dst[i] = a.src[i];
+}
+
+extern "C" __global__ __launch_bounds__(256) void vtb_fill_u32(vtb::FillArgs a) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < a.n) a.dst[i] = a.value;
 }

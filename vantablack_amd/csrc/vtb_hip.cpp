@@ -26,6 +26,7 @@ using vtb::AppendArgs;
 using vtb::CopyArgs;
 using vtb::DecodeArgs;
 using vtb::EltArgs;
+using vtb::FillArgs;
 using vtb::GemvArgs;
 using vtb::PrefillArgs;
 using vtb::QGemmArgs;
@@ -86,6 +87,7 @@ struct VtbHipCtx {
   hipFunction_t f_kvstat[kNumKv][kNumD] = {};  // statistics pass per cache dtype
   hipFunction_t f_append[kNumKv] = {};
   hipFunction_t f_copy = nullptr;
+  hipFunction_t f_fill = nullptr;
   hipFunction_t f_gemv[kNumQuant][kNumGemvR] = {};  // vtb_gemv_<kind>_r<1|2|4>
   hipFunction_t f_xsplit = nullptr;
   hipModule_t mod_layer = nullptr;  // rmsnorm, swiglu, gelu_approx, residual_add
@@ -192,8 +194,12 @@ int ensure_workspace(VtbHipCtx* ctx, size_t ws_bytes, size_t n_counters) {
     ctx->n_counters = 0;
     size_t n = std::max(n_counters, (size_t)4096);
     HIP_TRY(ctx, hipMalloc((void**)&ctx->counters, n * sizeof(unsigned)), "hipMalloc(counters)");
-    HIP_TRY(ctx, hipMemsetAsync(ctx->counters, 0, n * sizeof(unsigned), ctx->stream),
-            "hipMemsetAsync(counters)");
+    FillArgs fa;
+    memset(&fa, 0, sizeof fa);
+    fa.dst = ctx->counters;
+    fa.n = (long long)n;
+    const int rc = launch(ctx, ctx->f_fill, (unsigned)((n + 255) / 256), 1, 1, 256, &fa);
+    if (rc) return rc;
     ctx->n_counters = n;
   }
   return VTB_HIP_OK;
@@ -739,6 +745,7 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
     }
   }
   ok = ok && hipModuleGetFunction(&ctx->f_copy, ctx->mod_kvcopy, "vtb_copy_f32") == hipSuccess;
+  ok = ok && hipModuleGetFunction(&ctx->f_fill, ctx->mod_kvcopy, "vtb_fill_u32") == hipSuccess;
   for (int qk = 0; ok && qk < kNumQuant; ++qk)
     for (int ri = 0; ok && ri < kNumGemvR; ++ri) {
       snprintf(name, sizeof name, "vtb_gemv_%s_r%d", kQuantNames[qk], kGemvRs[ri]);
