@@ -231,6 +231,25 @@ void vtb_hip_segment_attn_decode_append(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbH
                                         size_t n_heads, size_t n_kv_heads, size_t head_dim,
                                         size_t seq_len, float inv_sqrt_hd, int kv_dtype);
 
+/* vtb_hip_segment_attn_decode_append computing the same outputs, allocating
+ * nothing: no counterpart in the reference.  For callers that cannot allocate
+ * device or host memory mid-stream (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The split-K partials and
+ * arrival counters live in a fixed 8 MiB array of the decode code object
+ * (256 KiB of counters, the rest partials; each context holds its own copy
+ * until it is destroyed), not in the context's growable workspace.  A shape
+ * whose workspace would exceed it is rejected with 5 (EUNSUPPORTED) at
+ * commit; every n_q = 1 shape of the default one-workgroup-per-CU plan fits
+ * (partials about n_kv * n_splits * G * (head_dim + 2) * 4 bytes).  Calls
+ * that overlap on one context race on the array; calls on one stream do
+ * not (each launch leaves its counters at zero for the next). */
+void vtb_hip_segment_attn_decode_append_noalloc(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *q_buf,
+                                                VtbHipBuf *k_cache_buf, size_t k_cache_offset_bytes,
+                                                VtbHipBuf *v_cache_buf, size_t v_cache_offset_bytes,
+                                                VtbHipBuf *k_cur_buf, VtbHipBuf *v_cur_buf,
+                                                size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                                size_t seq_len, float inv_sqrt_hd, int kv_dtype);
+
 /* vtb_hip_segment_attn_decode_append with RoPE fused in front: q (all
  * n_heads) and k_cur (all n_kv_heads) are rotated at absolute position
  * rope_pos -- math.rope, interleaved pairs, or with rope_half math.ropeHalf,

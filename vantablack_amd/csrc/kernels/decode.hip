@@ -469,6 +469,19 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
 
 }  // namespace vtb
 
+// Split-K workspace of the no-allocation decode entry
+// (vtb_hip_segment_attn_decode_append_noalloc): a fixed device array of this
+// code object, zero at load, its address taken once by the host with
+// hipModuleGetGlobal (the module-API counterpart of hipGetSymbolAddress; the
+// kernels are loaded with hipModuleLoadData, so the name is exported with C
+// linkage -- a definition in an extern "C" block -- rather than made static,
+// and marked used so the linker keeps it).  Each context loads its own copy
+// of the code object and so holds its own array.  The kernels reach it only through
+// the pointers the host passes in DecodeArgs.
+extern "C" {
+__device__ __attribute__((aligned(256), used)) unsigned char vtb_decode_scratch[vtb::decode_scratch_bytes];
+}
+
 // Kernel entry points, one per (KV dtype, head_dim, max GQA group).  Looked
 // up by name with hipModuleGetFunction: vtb_decode_<kv>_d<D>_g<G>.
 #define VTB_DECODE(KVN, KVT, D, G)                                                     \

@@ -48,6 +48,12 @@ constexpr int decode_counter_stride = 32;
 constexpr int decode_merge_flat = 32;
 constexpr int decode_merge_group = 16;
 
+// The decode code object's file-scope scratch (vtb_decode_scratch), used by
+// the no-allocation decode entry: arrival counters in the first
+// decode_scratch_counter_bytes, the split and group partials after them.
+constexpr unsigned long long decode_scratch_bytes = 8ull << 20;
+constexpr unsigned long long decode_scratch_counter_bytes = 256ull << 10;
+
 // Rows read by one wave load instruction (the split granularity).
 constexpr int decode_rows_per_load(int head_dim, int kv_bytes) {
   return 64 / (head_dim * kv_bytes / 16);

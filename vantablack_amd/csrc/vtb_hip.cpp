@@ -99,6 +99,10 @@ struct VtbHipCtx {
   size_t ws_bytes = 0;
   unsigned* counters = nullptr;
   size_t n_counters = 0;
+  // The decode code object's fixed scratch (vtb_decode_scratch): device
+  // address from hipModuleGetGlobal at init, counters cleared there once.
+  // Used only by the no-allocation decode entry; null if unavailable.
+  unsigned char* dscratch = nullptr;
   // Prefill scratch written by the vtb_kvt_* pre-pass: f16 V^T, f16 keys
   // (bf16 caches) and the per-tile multipliers.
   void* pf = nullptr;
@@ -248,10 +252,21 @@ struct RopeArgs {
   int half = 0;
 };
 
+// A caller-provided split-K workspace (the no-allocation entry's fixed
+// scratch): partials of ws_bytes and n_counters arrival counters that are
+// zero on entry.  Null: the context's workspace, grown on demand.
+struct DecodeWorkspace {
+  float* ws;
+  size_t ws_bytes;
+  unsigned* counters;
+  size_t n_counters;
+};
+
 int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, const void* v,
                   size_t n_q, size_t n_heads, size_t n_kv, size_t head_dim, long long pos0,
                   long long window, float inv_sqrt_hd, int dtype, const float* k_new = nullptr,
-                  const float* v_new = nullptr, RopeArgs rope = RopeArgs()) {
+                  const float* v_new = nullptr, RopeArgs rope = RopeArgs(),
+                  const DecodeWorkspace* fixed = nullptr) {
   const int di = d_index(head_dim);
   if (di < 0) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "head_dim must be 64, 128 or 256");
   if (dtype < 0 || dtype >= kNumKv) return set_err(ctx, VTB_HIP_EINVAL, "bad kv dtype");
@@ -290,8 +305,22 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
   const size_t n_part = n_q * n_kv * (size_t)n_splits * G;
   const size_t n_gpart = n_q * n_kv * n_groups * G;
   const size_t ws_need = n_splits > 1 ? (n_part + n_gpart) * (head_dim + 2) * sizeof(float) : 0;
-  int rc = ensure_workspace(ctx, ws_need, n_q * n_kv * (n_groups + 1) * vtb::decode_counter_stride);
-  if (rc) return rc;
+  const size_t ctr_need = n_q * n_kv * (n_groups + 1) * vtb::decode_counter_stride;
+  float* ws = nullptr;
+  unsigned* counters = nullptr;
+  if (fixed) {
+    if (ws_need > fixed->ws_bytes || ctr_need > fixed->n_counters)
+      return set_err(ctx, VTB_HIP_EUNSUPPORTED,
+                     "attn_decode_append_noalloc: the split-K workspace this shape needs exceeds the fixed "
+                     "scratch (8 MiB: 256 KiB of counters, the rest partials)");
+    ws = fixed->ws;
+    counters = fixed->counters;
+  } else {
+    int rc = ensure_workspace(ctx, ws_need, ctr_need);
+    if (rc) return rc;
+    ws = (float*)ctx->ws;
+    counters = ctx->counters;
+  }
 
   DecodeArgs a;
   memset(&a, 0, sizeof a);
@@ -299,11 +328,11 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
   a.k = k;
   a.v = v;
   a.out = out;
-  a.ws_o = (float*)ctx->ws;
+  a.ws_o = ws;
   a.ws_ml = a.ws_o + n_part * head_dim;
   a.wg_o = a.ws_ml + n_part * 2;
   a.wg_ml = a.wg_o + n_gpart * head_dim;
-  a.counters = ctx->counters;
+  a.counters = counters;
   a.n_heads = (int)n_heads;
   a.n_kv = (int)n_kv;
   a.n_splits = (int)n_splits;
@@ -705,6 +734,7 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
   if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return nullptr;
   if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return nullptr;
   VtbHipCtx* ctx = new VtbHipCtx();
+  ctx->err.reserve(512);  // error texts (< 512 bytes) then never allocate
   ctx->device = dev;
   ctx->cu_count = prop.multiProcessorCount;
   bool ok = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) == hipSuccess;
@@ -766,6 +796,26 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
   if (!ok) {
     vtb_hip_destroy(ctx);
     return nullptr;
+  }
+  // The no-allocation decode entry's scratch: this device's copy of the
+  // code object's array, its counter region cleared once (it is zero at
+  // load; every launch leaves its counters at zero again).
+  {
+    hipDeviceptr_t p = nullptr;
+    size_t sz = 0;
+    if (hipModuleGetFunction(&ctx->f_fill, ctx->mod_kvcopy, "vtb_fill_u32") == hipSuccess &&
+        hipModuleGetGlobal(&p, &sz, ctx->mod_decode, "vtb_decode_scratch") == hipSuccess &&
+        sz == vtb::decode_scratch_bytes && p != nullptr) {
+      FillArgs fa;
+      memset(&fa, 0, sizeof fa);
+      fa.dst = (uint32_t*)p;
+      fa.n = (long long)(vtb::decode_scratch_counter_bytes / sizeof(uint32_t));
+      if (launch(ctx, ctx->f_fill, (unsigned)((fa.n + 255) / 256), 1, 1, 256, &fa) == VTB_HIP_OK &&
+          hipStreamSynchronize(ctx->stream) == hipSuccess)
+        ctx->dscratch = (unsigned char*)p;
+    }
+    (void)hipGetLastError();
+    ctx->err.clear();
   }
   return ctx;
 }
@@ -1021,26 +1071,33 @@ static void decode_append_entry(const char* name, VtbHipSeg* seg, VtbHipBuf* out
                                 VtbHipBuf* k_cache_buf, size_t k_cache_offset_bytes, VtbHipBuf* v_cache_buf,
                                 size_t v_cache_offset_bytes, VtbHipBuf* k_cur_buf, VtbHipBuf* v_cur_buf,
                                 size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t seq_len,
-                                float inv_sqrt_hd, int kv_dtype, const RopeArgs& rope) {
+                                float inv_sqrt_hd, int kv_dtype, const RopeArgs& rope,
+                                const DecodeWorkspace* fixed = nullptr) {
   VtbHipCtx* ctx = seg->ctx;
-  const std::string who(name);
+  char msg[128];
   const int eb = kv_bytes(kv_dtype);
   if (!eb || n_heads == 0 || n_kv_heads == 0 || head_dim == 0 || n_heads > 65535 ||
-      n_kv_heads > 65535 || head_dim > 4096 || seq_len == 0)
-    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, (who + ": bad shape").c_str()));
+      n_kv_heads > 65535 || head_dim > 4096 || seq_len == 0) {
+    snprintf(msg, sizeof msg, "%s: bad shape", name);
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, msg));
+  }
   const size_t qbytes = n_heads * head_dim * 4;
   const size_t kv_dim = n_kv_heads * head_dim;
   if (!buf_ok(out_buf, 0, qbytes) || !buf_ok(q_buf, 0, qbytes) || !buf_ok(k_cur_buf, 0, kv_dim * 4) ||
-      !buf_ok(v_cur_buf, 0, kv_dim * 4))
-    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, (who + ": q/out/k_cur/v_cur too small").c_str()));
+      !buf_ok(v_cur_buf, 0, kv_dim * 4)) {
+    snprintf(msg, sizeof msg, "%s: q/out/k_cur/v_cur too small", name);
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, msg));
+  }
   const size_t kv_rows_bytes = seq_len * kv_dim * eb;
   if (!buf_ok(k_cache_buf, k_cache_offset_bytes, kv_rows_bytes) ||
-      !buf_ok(v_cache_buf, v_cache_offset_bytes, kv_rows_bytes))
-    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, (who + ": K/V range outside buffer").c_str()));
+      !buf_ok(v_cache_buf, v_cache_offset_bytes, kv_rows_bytes)) {
+    snprintf(msg, sizeof msg, "%s: K/V range outside buffer", name);
+    return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, msg));
+  }
   seg_note(seg, launch_decode(ctx, (float*)out_buf->ptr, (const float*)q_buf->ptr,
                               bptr(k_cache_buf, k_cache_offset_bytes), bptr(v_cache_buf, v_cache_offset_bytes),
                               1, n_heads, n_kv_heads, head_dim, (long long)seq_len - 1, 0, inv_sqrt_hd,
-                              kv_dtype, (const float*)k_cur_buf->ptr, (const float*)v_cur_buf->ptr, rope));
+                              kv_dtype, (const float*)k_cur_buf->ptr, (const float*)v_cur_buf->ptr, rope, fixed));
 }
 
 // RoPE arguments for a fused launch, or an error (base must be finite and
@@ -1065,6 +1122,26 @@ extern "C" void vtb_hip_segment_attn_decode_append(
   decode_append_entry("attn_decode_append", seg, out_buf, q_buf, k_cache_buf, k_cache_offset_bytes, v_cache_buf,
                       v_cache_offset_bytes, k_cur_buf, v_cur_buf, n_heads, n_kv_heads, head_dim, seq_len,
                       inv_sqrt_hd, kv_dtype, RopeArgs());
+}
+
+// The no-allocation form: the split-K workspace is the decode code object's
+// fixed scratch, so the call allocates nothing (host or device).
+extern "C" void vtb_hip_segment_attn_decode_append_noalloc(
+    VtbHipSeg* seg, VtbHipBuf* out_buf, VtbHipBuf* q_buf, VtbHipBuf* k_cache_buf, size_t k_cache_offset_bytes,
+    VtbHipBuf* v_cache_buf, size_t v_cache_offset_bytes, VtbHipBuf* k_cur_buf, VtbHipBuf* v_cur_buf,
+    size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t seq_len, float inv_sqrt_hd, int kv_dtype) {
+  if (!seg) return;
+  VtbHipCtx* ctx = seg->ctx;
+  if (!ctx->dscratch)
+    return seg_note(seg, set_err(ctx, VTB_HIP_EUNSUPPORTED, "attn_decode_append_noalloc: no fixed scratch"));
+  DecodeWorkspace fixed;
+  fixed.counters = (unsigned*)ctx->dscratch;
+  fixed.n_counters = vtb::decode_scratch_counter_bytes / sizeof(unsigned);
+  fixed.ws = (float*)(ctx->dscratch + vtb::decode_scratch_counter_bytes);
+  fixed.ws_bytes = vtb::decode_scratch_bytes - vtb::decode_scratch_counter_bytes;
+  decode_append_entry("attn_decode_append_noalloc", seg, out_buf, q_buf, k_cache_buf, k_cache_offset_bytes,
+                      v_cache_buf, v_cache_offset_bytes, k_cur_buf, v_cur_buf, n_heads, n_kv_heads, head_dim,
+                      seq_len, inv_sqrt_hd, kv_dtype, RopeArgs(), &fixed);
 }
 
 extern "C" void vtb_hip_segment_attn_decode_rope_append(

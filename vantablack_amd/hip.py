@@ -104,6 +104,8 @@ SIGNATURES = {
     "vtb_hip_segment_kv_append": ([_P, _P, _S, _I, _P, _S, _S], None),
     "vtb_hip_segment_attn_decode": ([_P, _P, _P, _P, _S, _P, _S, _S, _S, _S, _S, _F, _I], None),
     "vtb_hip_segment_attn_decode_append": ([_P, _P, _P, _P, _S, _P, _S, _P, _P, _S, _S, _S, _S, _F, _I], None),
+    "vtb_hip_segment_attn_decode_append_noalloc": ([_P, _P, _P, _P, _S, _P, _S, _P, _P, _S, _S, _S, _S, _F, _I],
+                                                   None),
     "vtb_hip_segment_attn_decode_rope_append": ([_P, _P, _P, _P, _S, _P, _S, _P, _P, _S, _S, _S, _S, _F, _I,
                                                  _S, _F, _I], None),
     "vtb_hip_segment_attn_prefill": ([_P, _P, _P, _P, _P, _S, _S, _S, _S, _S, _S, _S, _F, _I], None),
@@ -271,6 +273,15 @@ class Segment:
                            seq_len: int, inv_sqrt_hd: float, kv_dtype: int):
         lib().vtb_hip_segment_attn_decode_append(self.h, out.h, q.h, k.h, k_off, v.h, v_off, k_cur.h, v_cur.h,
                                                  n_heads, n_kv_heads, head_dim, seq_len, inv_sqrt_hd, kv_dtype)
+
+    def attn_decode_append_noalloc(self, out: Buffer, q: Buffer, k: Buffer, k_off: int, v: Buffer, v_off: int,
+                                   k_cur: Buffer, v_cur: Buffer, n_heads: int, n_kv_heads: int, head_dim: int,
+                                   seq_len: int, inv_sqrt_hd: float, kv_dtype: int):
+        """attn_decode_append with the split-K workspace in the decode code
+        object's fixed scratch: the call allocates nothing."""
+        lib().vtb_hip_segment_attn_decode_append_noalloc(self.h, out.h, q.h, k.h, k_off, v.h, v_off, k_cur.h,
+                                                         v_cur.h, n_heads, n_kv_heads, head_dim, seq_len,
+                                                         inv_sqrt_hd, kv_dtype)
 
     def attn_decode_rope_append(self, out: Buffer, q: Buffer, k: Buffer, k_off: int, v: Buffer, v_off: int,
                                 k_cur: Buffer, v_cur: Buffer, n_heads: int, n_kv_heads: int, head_dim: int,
