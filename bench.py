@@ -221,7 +221,7 @@ def prefill_flops(L, n_heads, d):
     return 4 * n_heads * d * L * (L + 1) // 2
 
 
-def prefill_kernel_name(torch, n_heads, n_q, d, dt="bf16"):
+def prefill_kernel_name(torch, n_heads, n_q, d):
     """The attention kernel one attn_prefill call runs, by the launcher's rule
     (launch_prefill_mfma in vantablack_amd/csrc/vtb_hip.cpp): the 8-wave
     kernel (256 queries per workgroup, d <= 128) when it still yields at
@@ -230,7 +230,7 @@ def prefill_kernel_name(torch, n_heads, n_q, d, dt="bf16"):
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     wide_min = int(os.environ.get("VTB_PREFILL_WIDE_MIN_WGS", 2 * max(cus, 1)))
     wide = d <= 128 and n_heads * -(-n_q // 256) >= wide_min
-    return f"vtb_prefill{'8' if wide else ''}_{dt}_d{d}"
+    return f"vtb_prefill{'8' if wide else ''}_d{d}"
 
 
 def bench_prefill(ctx, torch, n_heads, n_kv, d, L, reps=5, warmup=2):
@@ -593,11 +593,16 @@ def cpu_baseline(seconds_budget=18.0):
     cache.pos = L - 1
     c = orc.config(n_heads, n_kv, d, L)
     q = (rng.standard_normal(n_heads * d, dtype=np.float32) / np.float32(np.sqrt(d)))
-    per = decode_bytes(L, n_heads, n_kv, d, 2)
+    # The oracle reads f32 K/V (vantablack's cache dtype), so its rate is
+    # counted in f32 bytes; the f16-equivalent rate is reported beside it.
+    per = decode_bytes(L, n_heads, n_kv, d, 4)
+    per16 = decode_bytes(L, n_heads, n_kv, d, 2)
     res = {}
-    # 16 = the GPU box's CPU share; pool.zig's own default is (ncpu + 1) / 2
-    # workers (pool.zig:53), timed as well.
-    workers = int(os.environ.get("VTB_CPU_WORKERS", "16"))
+    # Workers: the CPUs this process may run on, capped at the GPU box's CPU
+    # share (16); pool.zig's own default is (ncpu + 1) / 2 workers
+    # (pool.zig:53), timed as well.
+    affinity = len(os.sched_getaffinity(0))
+    workers = min(affinity, int(os.environ.get("VTB_CPU_WORKERS", "16")))
     for label, nw in (("faithful_1t", 1), ("pool", workers), ("pool_default", (workers + 1) // 2)):
         pool = orc.Pool(nw)
         try:
@@ -610,17 +615,41 @@ def cpu_baseline(seconds_budget=18.0):
                     break
         finally:
             pool.close()
-        res[label] = {"gbs": n * per / el / 1e9, "ms_per_layer": el / n * 1e3, "layers": n, "workers": nw}
+        res[label] = {"gbs": n * per / el / 1e9, "gbs_f16_equiv": n * per16 / el / 1e9,
+                      "ms_per_layer": el / n * 1e3, "layers": n, "workers": nw}
         log(f"cpu {label}: {res[label]['ms_per_layer']:.2f} ms per layer-step ({n} runs)")
+    res["affinity_cpus"] = affinity
+    res["cpu_model"] = cpu_model()
     return res
 
 
-def pmc_workload(ctx_rows=8192):
-    """One dispatch of each measured kernel shape, for rocprofv3 --pmc runs:
-    the calibration copy (vtb_copy_f32), one C2 decode launch at L = ctx+1
-    with the KV append fused (vtb_decode_f16_d128_g1), and one C4 prefill of
-    8192 tokens (vtb_vt_bf16_d128 + the attention kernel the launcher picks,
-    vtb_prefill8_bf16_d128 on a 256-CU MI355X)."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+# Kernel shapes of the counter-run workload: (label, n_heads, n_kv, d, kv dtype,
+# attended rows, layers).  C3's window of 4096 is the attended range.
+PMC_DECODE = [("C2", 32, 32, 128, "f16", 8193, 4), ("C3", 32, 8, 128, "bf16", 4096, 4),
+              ("C5", 8, 1, 256, "bf16", 32768, 4)]
+PMC_PREFILL = [("C4", 32, 8, 128, 8192), ("C5", 8, 1, 256, 4096)]
+
+
+def pmc_workload():
+    """The launches of every measured kernel shape, for rocprofv3 --pmc runs:
+    the calibration copy (vtb_copy_f32); the fused append + decode launch of
+    C2 (vtb_decode_f16_d128_g1), C3 (vtb_decode_bf16_d128_g4) and C5
+    (vtb_decode_bf16_d256_g8), each over PMC_DECODE's layer count of distinct
+    cache layers; and the C4 (8192 tokens) and C5 (4096 tokens) causal
+    prefill calls: the statistics and conversion passes (vtb_kvstat_*,
+    vtb_kvt_*) and the attention kernel the launcher picks (vtb_prefill8_d128,
+    vtb_prefill_d256)."""
     import numpy as np
     import torch
     import vantablack_amd as vb
@@ -636,49 +665,60 @@ def pmc_workload(ctx_rows=8192):
     ctx.wait_idle()
     log("pmc: copy done")
     del src, dst
-    n_heads, n_kv, d, L = 32, 32, 128, ctx_rows + 1
-    kc = torch.randn((L, n_kv, d), generator=g, device=dev).to(torch.float16)
-    vc = torch.randn((L, n_kv, d), generator=g, device=dev).to(torch.float16)
-    q = torch.randn(n_heads * d, generator=g, device=dev) / np.sqrt(d)
-    kcur, vcur, out = torch.randn(n_kv * d, device=dev), torch.randn(n_kv * d, device=dev), torch.empty(n_heads * d, device=dev)
-    torch.cuda.synchronize()
-    with ctx.segment() as seg:
-        seg.attn_decode_append(ctx.wrap_tensor(out), ctx.wrap_tensor(q), ctx.wrap_tensor(kc), 0, ctx.wrap_tensor(vc), 0,
-                               ctx.wrap_tensor(kcur), ctx.wrap_tensor(vcur), n_heads, n_kv, d, L, 1.0 / np.sqrt(d), vb.F16)
-    ctx.wait_idle()
-    log("pmc: decode done")
-    del kc, vc
-    n_heads, n_kv, d, L = 32, 8, 128, 8192
-    qp = torch.randn((L, n_heads * d), generator=g, device=dev)
-    kp = torch.randn((L, n_kv * d), generator=g, device=dev).to(torch.bfloat16)
-    vp = torch.randn((L, n_kv * d), generator=g, device=dev).to(torch.bfloat16)
-    op = torch.empty((L, n_heads * d), device=dev)
-    torch.cuda.synchronize()
-    with ctx.segment() as seg:
-        seg.attn_prefill(ctx.wrap_tensor(op), ctx.wrap_tensor(qp), ctx.wrap_tensor(kp), ctx.wrap_tensor(vp), 0, L, 0,
-                         vb.NO_WINDOW, n_heads, n_kv, d, 1.0 / np.sqrt(d), vb.BF16)
-    ctx.wait_idle()
-    log("pmc: prefill done")
+    tdt = {"f16": torch.float16, "bf16": torch.bfloat16}
+    for label, n_heads, n_kv, d, kv, L, n_layers in PMC_DECODE:
+        kc = torch.randn((n_layers, L, n_kv, d), generator=g, device=dev).to(tdt[kv])
+        vc = torch.randn((n_layers, L, n_kv, d), generator=g, device=dev).to(tdt[kv])
+        q = torch.randn((n_layers, n_heads * d), generator=g, device=dev) / np.sqrt(d)
+        kcur, vcur = torch.randn(n_kv * d, device=dev), torch.randn(n_kv * d, device=dev)
+        out = torch.empty(n_heads * d, device=dev)
+        torch.cuda.synchronize()
+        kb, vbuf = ctx.wrap_tensor(kc), ctx.wrap_tensor(vc)
+        lb = L * n_kv * d * 2
+        with ctx.segment() as seg:
+            for l in range(n_layers):
+                seg.attn_decode_append(ctx.wrap_tensor(out), ctx.wrap_tensor(q[l]), kb, l * lb, vbuf, l * lb,
+                                       ctx.wrap_tensor(kcur), ctx.wrap_tensor(vcur), n_heads, n_kv, d, L,
+                                       1.0 / np.sqrt(d), vb.hip.DTYPES[kv])
+        ctx.wait_idle()
+        log(f"pmc: decode {label} done")
+        del kc, vc
+    for label, n_heads, n_kv, d, L in PMC_PREFILL:
+        qp = torch.randn((L, n_heads * d), generator=g, device=dev)
+        kp = torch.randn((L, n_kv * d), generator=g, device=dev).to(torch.bfloat16)
+        vp = torch.randn((L, n_kv * d), generator=g, device=dev).to(torch.bfloat16)
+        op = torch.empty((L, n_heads * d), device=dev)
+        torch.cuda.synchronize()
+        with ctx.segment() as seg:
+            seg.attn_prefill(ctx.wrap_tensor(op), ctx.wrap_tensor(qp), ctx.wrap_tensor(kp), ctx.wrap_tensor(vp), 0,
+                             L, 0, vb.NO_WINDOW, n_heads, n_kv, d, 1.0 / np.sqrt(d), vb.BF16)
+        ctx.wait_idle()
+        log(f"pmc: prefill {label} done")
+        del qp, kp, vp, op
     ctx.close()
+
+
+def pmc_read(dirs):
+    """Per-dispatch average of every counter of the vtb_* kernels in the
+    rocprofv3 --pmc csv outputs under dirs: {kernel: {counter: value}}."""
+    import csv
+    import glob
+    vals = {}
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Kernel_Name"].startswith("vtb_"):
+                    name = r["Kernel_Name"].split("(")[0]
+                    vals.setdefault(name, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    return {k: {c: sum(v) / len(v) for c, v in cs.items()} for k, cs in vals.items()}
 
 
 def pmc_summary(fetch_dir, write_dir):
     """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the vtb_* kernels from
     two rocprofv3 --pmc csv outputs, scaled by the copy calibration, written
     to profiles/traffic.json and printed as a markdown table."""
-    import csv
-    import glob
-
-    def read(dirname, counter):
-        vals = {}
-        for f in glob.glob(os.path.join(dirname, "**", "*counter_collection.csv"), recursive=True):
-            for r in csv.DictReader(open(f)):
-                if r["Counter_Name"] == counter and r["Kernel_Name"].startswith("vtb_"):
-                    name = r["Kernel_Name"].split("(")[0]
-                    vals.setdefault(name, []).append(float(r["Counter_Value"]))
-        return {k: sum(v) / len(v) for k, v in vals.items()}
-
-    fetch, write = read(fetch_dir, "FETCH_SIZE"), read(write_dir, "WRITE_SIZE")
+    fetch = {k: v["FETCH_SIZE"] for k, v in pmc_read([fetch_dir]).items() if "FETCH_SIZE" in v}
+    write = {k: v["WRITE_SIZE"] for k, v in pmc_read([write_dir]).items() if "WRITE_SIZE" in v}
     copy_kib = PMC_COPY_FLOATS * 4 / 1024
     f_fetch = copy_kib / fetch["vtb_copy_f32"]
     f_write = copy_kib / write["vtb_copy_f32"]
@@ -688,7 +728,10 @@ def pmc_summary(fetch_dir, write_dir):
                          "traffic_bytes": int(round((fetch[name] * f_fetch + write[name] * f_write) * 1024))}
     out = {"calibration": {"kernel": "vtb_copy_f32", "bytes_each_way": PMC_COPY_FLOATS * 4,
                            "fetch_factor": round(f_fetch, 4), "write_factor": round(f_write, 4)},
-           "workload": "bench.py --pmc-workload: C2 decode at L=8193 (f16, KV append fused); C4 prefill 8192 tokens bf16",
+           "workload": "bench.py --pmc-workload: decode " +
+                       ", ".join(f"{c[0]} ({c[1]}q/{c[2]}kv d{c[3]} {c[4]} L={c[5]})" for c in PMC_DECODE) +
+                       " with the KV append fused; prefill " +
+                       ", ".join(f"{c[0]} ({c[1]}q/{c[2]}kv d{c[3]} bf16, {c[4]} tokens)" for c in PMC_PREFILL),
            "kernels": kernels}
     with open(TRAFFIC_FILE, "w") as f:
         json.dump(out, f, indent=1)
@@ -700,6 +743,96 @@ def pmc_summary(fetch_dir, write_dir):
         print(f"| {k} | {v['fetch_kib']:.1f} | {v['write_kib']:.1f} | {v['traffic_bytes'] / 1e6:.2f} |")
 
 
+COUNTERS_FILE = os.path.join(ROOT, "profiles", "counters.json")
+
+
+def pmc_sq_summary(dirs):
+    """Shader (SQ) and GRBM counters of the vtb_* kernels from rocprofv3
+    --pmc csv runs over `bench.py --pmc-workload`, with each dispatch's
+    duration from the same runs, written to profiles/counters.json and
+    printed as a markdown table.
+
+    Normalisation (gfx950, from the runs' agent_info: 8 XCDs, 256 CUs, 4 SIMDs
+    per CU, 2.4 GHz peak engine clock):
+      GRBM_GUI_ACTIVE is summed over the XCDs, so the dispatch's cycles on
+        one XCD are GRBM_GUI_ACTIVE / 8 (that window also holds about 20k
+        cycles of dispatch set-up: clock_ghz is only meaningful for long
+        kernels);
+      SQ_VALU_MFMA_BUSY_CYCLES is summed over every SIMD (a 32x32x16 f16 MFMA
+        counts 32), so mfma_busy = busy / (1024 SIMDs x cycles), with cycles
+        from GRBM (at the clock the kernel ran at) or from duration x 2.4 GHz
+        (against the peak clock, i.e. the dense-peak fraction);
+      SQ_INSTS_VALU_MFMA_MOPS_* count units of 512 flops;
+      SQ_ACTIVE_INST_VALU counts quad-cycles (4 clocks) per wave, summed, so
+        valu_busy = 4 x that / (1024 SIMDs x duration x 2.4 GHz)."""
+    import csv
+    import glob
+    agent = {}
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*agent_info.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Agent_Type"] == "GPU":
+                    agent = {"xcc": int(r["Num_Xcc"]), "cus": int(r["Cu_Count"]),
+                             "simds": int(r["Cu_Count"]) * int(r["Simd_Per_Cu"]),
+                             "clk_mhz": int(r["Max_Engine_Clk_Fcompute"])}
+    vals, durs = {}, {}
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            seen = set()
+            for r in csv.DictReader(open(f)):
+                if not r["Kernel_Name"].startswith("vtb_"):
+                    continue
+                name = r["Kernel_Name"].split("(")[0]
+                vals.setdefault(name, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+                key = (f, r["Dispatch_Id"])
+                if key not in seen:
+                    seen.add(key)
+                    durs.setdefault(name, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9)
+    clk = agent["clk_mhz"] * 1e6
+    kernels = {}
+    for name in sorted(vals):
+        c = {k: sum(v) / len(v) for k, v in vals[name].items()}
+        dur = sum(durs[name]) / len(durs[name])
+        e = {"dispatches": len(durs[name]), "dur_us": round(dur * 1e6, 2),
+             "counters": {k: int(round(v)) for k, v in sorted(c.items())}}
+        grbm_cyc = c.get("GRBM_GUI_ACTIVE", 0) / agent["xcc"]
+        if grbm_cyc:
+            e["clock_ghz"] = round(grbm_cyc / dur / 1e9, 3)
+        mops = c.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0) + c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0)
+        if mops:
+            e["mfma_flops"] = int(mops * 512)
+            busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0)
+            if grbm_cyc:
+                e["mfma_busy_at_clock"] = round(busy / (agent["simds"] * grbm_cyc), 4)
+            e["mfma_busy_at_peak_clock"] = round(busy / (agent["simds"] * dur * clk), 4)
+        if c.get("SQ_ACTIVE_INST_VALU"):
+            e["valu_busy_at_peak_clock"] = round(4 * c["SQ_ACTIVE_INST_VALU"] / (agent["simds"] * dur * clk), 4)
+        if c.get("SQ_WAVES"):
+            e["valu_insts_per_wave"] = round(c.get("SQ_INSTS_VALU", 0) / c["SQ_WAVES"], 1)
+            e["waves"] = int(c["SQ_WAVES"])
+        kernels[name] = e
+    out = {"agent": agent, "dirs": [os.path.basename(d.rstrip("/")) for d in dirs],
+           "workload": "bench.py --pmc-workload (see profiles/traffic.json for the shapes)",
+           "kernels": kernels}
+    with open(COUNTERS_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+    print("| kernel | dispatches | dur us | clock GHz (GRBM) | MFMA flops | MFMA busy @clock | MFMA busy @2.4GHz "
+          "| VALU busy @2.4GHz | VALU insts/wave | waves |")
+    print("|---|---|---|---|---|---|---|---|---|---|")
+    for k, e in kernels.items():
+        print(f"| {k} | {e['dispatches']} | {e['dur_us']} | {e.get('clock_ghz', '')} | {e.get('mfma_flops', '')} | "
+              f"{e.get('mfma_busy_at_clock', '')} | {e.get('mfma_busy_at_peak_clock', '')} | "
+              f"{e.get('valu_busy_at_peak_clock', '')} | {e.get('valu_insts_per_wave', '')} | {e.get('waves', '')} |")
+
+
+def load_counters():
+    try:
+        with open(COUNTERS_FILE) as f:
+            return json.load(f)["kernels"]
+    except (OSError, ValueError, KeyError):
+        return {}
+
+
 def load_traffic():
     try:
         with open(TRAFFIC_FILE) as f:
@@ -708,11 +841,40 @@ def load_traffic():
         return {}
 
 
+def mfma_busy_field(e):
+    """The prefill kernel's MFMA-busy figures from profiles/counters.json."""
+    if not e or "mfma_busy_at_clock" not in e:
+        return None
+    return {"at_clock": e["mfma_busy_at_clock"], "at_2p4ghz": e["mfma_busy_at_peak_clock"],
+            "clock_ghz": e.get("clock_ghz"), "dur_us": e["dur_us"],
+            "source": "profiles/counters.json: SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x cycles); cycles = "
+                      "GRBM_GUI_ACTIVE / 8 XCDs (at_clock) or duration x 2.4 GHz (at_2p4ghz); C4 8192 tokens"}
+
+
+def decode_counter_field(kname, tr, e):
+    """HBM traffic and VALU figures of one decode kernel from profiles/."""
+    if not tr and not e:
+        return None
+    out = {"kernel": kname}
+    if tr:
+        out["traffic_bytes"] = tr["traffic_bytes"]
+    if e:
+        out.update({"valu_busy_at_2p4ghz": e.get("valu_busy_at_peak_clock"),
+                    "valu_insts_per_wave": e.get("valu_insts_per_wave"), "waves": e.get("waves"),
+                    "profiled_dur_us": e["dur_us"]})
+    out["source"] = "profiles/traffic.json (FETCH_SIZE, WRITE_SIZE) and profiles/counters.json (SQ counters)"
+    return out
+
+
 def main():
     if len(sys.argv) > 1 and sys.argv[1] == "--pmc-workload":
         return pmc_workload()
     if len(sys.argv) > 1 and sys.argv[1] == "--pmc-summary":
         return pmc_summary(sys.argv[2], sys.argv[3])
+    if len(sys.argv) > 1 and sys.argv[1] == "--pmc-sq-summary":
+        return pmc_sq_summary(sys.argv[2:])
+    if len(sys.argv) > 1 and sys.argv[1] == "--pmc-dump":
+        return print(json.dumps(pmc_read(sys.argv[2:]), indent=1))
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=32)
@@ -761,6 +923,7 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline()
     ctx.close()
     traffic = load_traffic()
+    counters = load_counters()
     dec_tr = traffic.get("vtb_decode_f16_d128_g1", {}).get("traffic_bytes")
     pre_kernel = pre["C4_L8192"]["kernel"] if pre else None
     pre_tr = traffic.get(pre_kernel, {}).get("traffic_bytes") if pre_kernel else None
@@ -797,6 +960,9 @@ def main():
         },
     }
     if dec_more:
+        for cfg, kname in (("C3", "vtb_decode_bf16_d128_g4"), ("C5", "vtb_decode_bf16_d256_g8")):
+            if cfg in dec_more:
+                dec_more[cfg]["counters"] = decode_counter_field(kname, traffic.get(kname), counters.get(kname))
         line["decode_other_configs"] = dec_more
     if gemv:
         line["quant_gemv"] = {
@@ -832,9 +998,10 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(p8["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(p8["tflops"] / BF16_PEAK_TFLOPS, 4), "traffic": pre_tr,
                          "kernel": pre_kernel, "avg_launch_us": round(p8["avg_launch_s"] * 1e6, 2),
-                         "timed_span": "one attn_prefill call: the range and conversion passes "
-                                       "(vtb_kvmax_bf16_d128, vtb_kvt_bf16_d128) and the attention kernel",
-                         "flops_per_launch": p8["flops"]},
+                         "timed_span": "one attn_prefill call: the statistics and conversion passes "
+                                       "(vtb_kvstat_bf16_d128, vtb_kvt_bf16_d128) and the attention kernel",
+                         "flops_per_launch": p8["flops"],
+                         "mfma_busy": mfma_busy_field(counters.get(pre_kernel))},
             "all": {k: {"tflops": round(v["tflops"], 2), "us": round(v["avg_launch_s"] * 1e6, 2)}
                     for k, v in pre.items()},
         }
@@ -842,15 +1009,18 @@ def main():
         line["cpu_baseline"] = {
             "value": round(cpu["pool"]["gbs"], 3), "unit": "GB/s", "cores": cpu["pool"]["workers"],
             "kind": "port",
-            "sample": "one C2 layer at L=8192 (32 heads, d128, f32 values), repeated ~6 s per line (three lines); "
-                      "pool = heads split over pool.zig-style workers (vantablack itself runs attention "
-                      "single-threaded)",
+            "sample": "one C2 layer at L=8192 (32 heads, d128, f32 K/V values, as vantablack's f32 cache "
+                      "holds them), repeated ~6 s per line (three lines); GB/s counts the f32 bytes the "
+                      "oracle reads; pool = heads split over pool.zig-style workers (vantablack itself runs "
+                      "attention single-threaded)",
+            "cpu_model": cpu["cpu_model"], "affinity_cpus": cpu["affinity_cpus"],
+            "f16_equivalent_gbs": round(cpu["pool"]["gbs_f16_equiv"], 3),
             "faithful_1t": {"value": round(cpu["faithful_1t"]["gbs"], 3), "cores": 1,
                             "ms_per_layer": round(cpu["faithful_1t"]["ms_per_layer"], 3)},
             "pool_ms_per_layer": round(cpu["pool"]["ms_per_layer"], 3),
             "pool_default": {"value": round(cpu["pool_default"]["gbs"], 3), "cores": cpu["pool_default"]["workers"],
                              "ms_per_layer": round(cpu["pool_default"]["ms_per_layer"], 3),
-                             "note": "pool.zig's default worker count, (ncpu + 1) / 2 of the 16-core share"},
+                             "note": "pool.zig's default worker count, (workers + 1) / 2"},
         }
     print(json.dumps(line), flush=True)
 

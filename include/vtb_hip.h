@@ -374,6 +374,25 @@ VtbHipBuf *vtb_hip_kv_cache_v(VtbHipKvCache *cache);
  * unlike the Metal path).  0, or 4 if new_max_seq < pos. */
 int vtb_hip_kv_cache_shrink_to_fit(VtbHipKvCache *cache, size_t new_max_seq);
 
+/* ---- scratch reservation: the counterpart of prefill.zig Scratch.init
+ * (prefill.zig:67-88), which sizes the batch scratch for B tokens and the
+ * score rows for max_seq once, before the first forward.  Grows, once, every
+ * buffer the context otherwise grows on demand (which drains the stream and
+ * calls hipMalloc inside the call that needs it): the split-K decode
+ * workspace and counters for one query (and, on f32 caches, whose prefill
+ * runs the decode kernel, up to max_batch queries) over up to c->max_seq
+ * keys or the window; the prefill conversion scratch for a c->max_seq-key
+ * context (f16/bf16 caches, max_batch > 0); the batched-matmul activation
+ * scratch for max_batch tokens of width max_matmul_k (0: none); the RoPE
+ * table of rope_base (0: none).  Later calls within these bounds allocate
+ * nothing.  Waits for the stream.  5 if a bound is beyond what the kernels
+ * take (max_batch > max_seq, max_matmul_k > 32768). */
+int vtb_hip_reserve(VtbHipCtx *ctx, const VtbHipAttnConfig *c, int kv_dtype, size_t max_batch,
+                    size_t max_matmul_k, float rope_base);
+/* Bytes of device scratch ctx holds: unchanged by calls that needed no
+ * growth. */
+size_t vtb_hip_scratch_bytes(VtbHipCtx *ctx);
+
 /* ---- Layer-level entries mirroring the reference call sites.
  *
  * Decode, one layer (forward.zig:267-270 then cpuAttention :187-228): write

@@ -47,6 +47,8 @@ def test_null_handles_are_rejected_without_a_gpu(hip):
     assert L.vtb_hip_stream(None) is None
     cfg = hip.AttnConfigC(8, 8, 64, 16, hip.NO_WINDOW)
     assert L.vtb_hip_layer_attention(None, None, ctypes.byref(cfg), 0, None, None, None, None) == hip.EINVAL
+    assert L.vtb_hip_reserve(None, ctypes.byref(cfg), 0, 16, 0, 0.0) == hip.EINVAL
+    assert L.vtb_hip_scratch_bytes(None) == 0
 
 
 def test_code_objects_are_gfx950(hip):

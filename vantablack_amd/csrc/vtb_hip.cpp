@@ -252,6 +252,62 @@ struct RopeArgs {
   int half = 0;
 };
 
+// The split plan of a decode launch: one workgroup per CU (the workgroup's
+// waves fill the CU, and few splits keep the final merge short), rows per
+// split a multiple of the rows one wave load instruction covers; split
+// partials, then group partials (two-level merge), each (o[G][D],
+// m/l[G][2]); one arrival counter per group plus one for the groups.
+struct DecodePlan {
+  long long rps, n_splits;
+  size_t n_part, n_gpart, ws_need, ctr_need;
+};
+void decode_sizes(size_t n_q, size_t n_kv, size_t head_dim, int G, long long n_splits, DecodePlan* p) {
+  const size_t n_groups = ((size_t)n_splits + vtb::decode_merge_group - 1) / vtb::decode_merge_group;
+  p->n_splits = n_splits;
+  p->n_part = n_q * n_kv * (size_t)n_splits * G;
+  p->n_gpart = n_q * n_kv * n_groups * G;
+  p->ws_need = n_splits > 1 ? (p->n_part + p->n_gpart) * (head_dim + 2) * sizeof(float) : 0;
+  p->ctr_need = n_q * n_kv * (n_groups + 1) * vtb::decode_counter_stride;
+}
+long long decode_target_splits(VtbHipCtx* ctx, size_t n_q, size_t n_kv) {
+  const long long target = env_int("VTB_DECODE_TARGET_WGS", std::max(ctx->cu_count, 1));
+  const long long units = (long long)(n_kv * n_q);
+  return std::max(1LL, (target + units - 1) / units);
+}
+int plan_decode(VtbHipCtx* ctx, size_t n_q, size_t n_kv, size_t head_dim, long long Lmax, int dtype, int G,
+                DecodePlan* p) {
+  const long long quantum = vtb::decode_rows_per_load((int)head_dim, kKvBytes[dtype]);
+  const long long want = decode_target_splits(ctx, n_q, n_kv);
+  long long rps = (Lmax + want - 1) / want;
+  rps = std::max(quantum, (rps + quantum - 1) / quantum * quantum);
+  const long long n_splits = (Lmax + rps - 1) / rps;
+  if (n_splits > 65535) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "too many splits");
+  p->rps = rps;
+  decode_sizes(n_q, n_kv, head_dim, G, n_splits, p);
+  return VTB_HIP_OK;
+}
+
+// Largest workspace plan_decode asks for over every range length up to
+// Lmax_hi: rows per split are at least ceil(L / want) and at least one
+// load quantum, so a launch has at most min(want, ceil(Lmax_hi / quantum))
+// splits, and the sizes grow with the split count.
+void decode_bound(VtbHipCtx* ctx, size_t n_q, size_t n_kv, size_t head_dim, long long Lmax_hi, int dtype, int G,
+                  DecodePlan* p) {
+  const long long quantum = vtb::decode_rows_per_load((int)head_dim, kKvBytes[dtype]);
+  const long long n_splits = std::min(decode_target_splits(ctx, n_q, n_kv), (Lmax_hi + quantum - 1) / quantum);
+  p->rps = 0;
+  decode_sizes(n_q, n_kv, head_dim, G, std::max(1LL, n_splits), p);
+}
+
+// GQA group width the decode kernels are instantiated for (1, 2, 4, 8, 16),
+// or -1 above 16.
+int decode_group_index(size_t n_heads, size_t n_kv) {
+  const size_t gmax = (n_heads + n_kv - 1) / n_kv;
+  int gi = 0;
+  while (gi < kNumG && (size_t)kGs[gi] < gmax) ++gi;
+  return gi == kNumG ? -1 : gi;
+}
+
 // A caller-provided split-K workspace (the no-allocation entry's fixed
 // scratch): partials of ws_bytes and n_counters arrival counters that are
 // zero on entry.  Null: the context's workspace, grown on demand.
@@ -273,10 +329,8 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
   if (n_heads == 0 || n_kv == 0 || n_q == 0 || pos0 < 0)
     return set_err(ctx, VTB_HIP_EINVAL, "empty shape");
   if (!aligned16(k) || !aligned16(v)) return set_err(ctx, VTB_HIP_EINVAL, "K/V not 16-byte aligned");
-  const size_t gmax = (n_heads + n_kv - 1) / n_kv;
-  int gi = 0;
-  while (gi < kNumG && (size_t)kGs[gi] < gmax) ++gi;
-  if (gi == kNumG) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "GQA group wider than 16");
+  const int gi = decode_group_index(n_heads, n_kv);
+  if (gi < 0) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "GQA group wider than 16");
   const int G = kGs[gi];
   if (n_q > 65535 || n_kv > 65535) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "grid too large");
 
@@ -287,25 +341,11 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
     long long ws = (window <= 0 || qp < window) ? 0 : qp - window + 1;
     Lmax = std::max(Lmax, qp + 1 - ws);
   }
-  // One workgroup per CU: the workgroup's waves fill the CU, and few splits
-  // keep the final merge short.  Rows per split are a multiple of the rows
-  // one wave load instruction covers.
-  const long long quantum = vtb::decode_rows_per_load((int)head_dim, kKvBytes[dtype]);
-  const long long target = env_int("VTB_DECODE_TARGET_WGS", std::max(ctx->cu_count, 1));
-  const long long units = (long long)(n_kv * n_q);
-  long long want = std::max(1LL, (target + units - 1) / units);
-  long long rps = (Lmax + want - 1) / want;
-  rps = std::max(quantum, (rps + quantum - 1) / quantum * quantum);
-  long long n_splits = (Lmax + rps - 1) / rps;
-  if (n_splits > 65535) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "too many splits");
-
-  // Split partials, then group partials (two-level merge), each (o[G][D],
-  // m/l[G][2]); one arrival counter per group plus one for the groups.
-  const size_t n_groups = ((size_t)n_splits + vtb::decode_merge_group - 1) / vtb::decode_merge_group;
-  const size_t n_part = n_q * n_kv * (size_t)n_splits * G;
-  const size_t n_gpart = n_q * n_kv * n_groups * G;
-  const size_t ws_need = n_splits > 1 ? (n_part + n_gpart) * (head_dim + 2) * sizeof(float) : 0;
-  const size_t ctr_need = n_q * n_kv * (n_groups + 1) * vtb::decode_counter_stride;
+  DecodePlan pl;
+  int rc0 = plan_decode(ctx, n_q, n_kv, head_dim, Lmax, dtype, G, &pl);
+  if (rc0) return rc0;
+  const long long rps = pl.rps, n_splits = pl.n_splits;
+  const size_t n_part = pl.n_part, n_gpart = pl.n_gpart, ws_need = pl.ws_need, ctr_need = pl.ctr_need;
   float* ws = nullptr;
   unsigned* counters = nullptr;
   if (fixed) {
@@ -615,6 +655,14 @@ int launch_gemv(VtbHipCtx* ctx, int qk, float* out, const void* w, const float* 
   return launch_gemv_blocks(ctx, qk, 1, outs, ws, ms, x, k);
 }
 
+// Batched-matmul scratch for B tokens of width k: two bf16 planes
+// [2][Bp][k], the 16-column sums [Bp][k/16] and the inverse scales [Bp],
+// Bp = B rounded up to 128.
+size_t qgemm_scratch_bytes(size_t B, size_t k) {
+  const size_t Bp = (B + 127) / 128 * 128;
+  return 2 * Bp * k * 2 + Bp * (k / 16) * 4 + Bp * 4;
+}
+
 // Batched quantised matmul launcher: out[B][m] = acts[B][k] . W^T.  The
 // pre-pass scales each token by a power of two and splits it into two f16
 // planes, 16-column sums and the token's inverse scale in the
@@ -640,16 +688,10 @@ int launch_qgemm_blocks(VtbHipCtx* ctx, int qk, int nblk, float* const outs[], c
   }
   if (!aligned16(acts)) return set_err(ctx, VTB_HIP_EINVAL, "matmul_batched: activations not 16-byte aligned");
   const size_t Bp = (B + 127) / 128 * 128;
-  const size_t planes_bytes = 2 * Bp * k * 2, sums_bytes = Bp * (k / 16) * 4, inv_bytes = Bp * 4;
-  const size_t need = planes_bytes + sums_bytes + inv_bytes;
-  if (need > ctx->qg_bytes) {
-    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
-    if (ctx->qg) HIP_TRY(ctx, hipFree(ctx->qg), "hipFree");
-    ctx->qg = nullptr;
-    ctx->qg_bytes = 0;
-    HIP_TRY(ctx, hipMalloc(&ctx->qg, need), "hipMalloc(batched matmul scratch)");
-    ctx->qg_bytes = need;
-  }
+  const size_t planes_bytes = 2 * Bp * k * 2, sums_bytes = Bp * (k / 16) * 4;
+  int rc0 = ensure_scratch(ctx, &ctx->qg, &ctx->qg_bytes, qgemm_scratch_bytes(B, k),
+                           "hipMalloc(batched matmul scratch)");
+  if (rc0) return rc0;
   uint16_t* planes = (uint16_t*)ctx->qg;
   float* sums = (float*)((char*)ctx->qg + planes_bytes);
   float* inv_scale = (float*)((char*)ctx->qg + planes_bytes + sums_bytes);
@@ -1052,9 +1094,12 @@ extern "C" void vtb_hip_segment_attn_decode(VtbHipSeg* seg, VtbHipBuf* out_buf, 
     return seg_note(seg, set_err(ctx, VTB_HIP_EINVAL, "attn_decode: q/out too small"));
   if (seq_len == 0) {
     // Empty softmax: the reference leaves attn_out zeroed (forward.zig:205).
-    if (hipMemsetAsync(out_buf->ptr, 0, qbytes, ctx->stream) != hipSuccess)
-      seg_note(seg, set_err(ctx, VTB_HIP_EDEVICE, "hipMemsetAsync"));
-    return;
+    // A fill kernel, not hipMemsetAsync, so the call can be graph-captured.
+    FillArgs fa;
+    memset(&fa, 0, sizeof fa);
+    fa.dst = (uint32_t*)out_buf->ptr;
+    fa.n = (long long)(qbytes / 4);
+    return seg_note(seg, launch(ctx, ctx->f_fill, (unsigned)((fa.n + 255) / 256), 1, 1, 256, &fa));
   }
   const size_t kv_rows_bytes = seq_len * n_kv_heads * head_dim * eb;
   if (!buf_ok(k_cache_buf, k_cache_offset_bytes, kv_rows_bytes) ||
@@ -1545,4 +1590,72 @@ extern "C" int vtb_hip_prefill_attention(VtbHipSeg* seg, VtbHipKvCache* c, const
   }
   seg_note(seg, rc);
   return rc;
+}
+
+// Pre-size every buffer the context grows on demand, so that later calls
+// within these bounds allocate nothing and never drain the stream for a
+// growth.  The counterpart of prefill.zig's Scratch.init (prefill.zig:67-88),
+// which sizes the batch scratch for B tokens and the score rows for max_seq
+// once, before the first forward: here the split-K decode workspace and
+// arrival counters (one query, and up to max_batch queries on f32 caches,
+// whose prefill runs the decode kernel), the prefill conversion scratch for
+// a max_seq-key context (f16/bf16 caches), the batched-matmul activation
+// scratch for max_batch tokens of width max_matmul_k (0: none), and the
+// RoPE table for rope_base (0: none).
+extern "C" int vtb_hip_reserve(VtbHipCtx* ctx, const VtbHipAttnConfig* cfg, int kv_dtype, size_t max_batch,
+                               size_t max_matmul_k, float rope_base) {
+  if (!ctx || !cfg) return VTB_HIP_EINVAL;
+  const size_t D = cfg->head_dim, n_kv = cfg->n_kv_heads, n_heads = cfg->n_heads, max_seq = cfg->max_seq;
+  if (d_index(D) < 0) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "reserve: head_dim must be 64, 128 or 256");
+  if (!kv_bytes(kv_dtype)) return set_err(ctx, VTB_HIP_EINVAL, "reserve: bad kv dtype");
+  if (n_heads == 0 || n_kv == 0 || max_seq == 0 || n_kv > 65535 || n_heads > 65535)
+    return set_err(ctx, VTB_HIP_EINVAL, "reserve: bad shape");
+  if (max_seq >= ((size_t)1 << 30) || max_batch > max_seq)
+    return set_err(ctx, VTB_HIP_EUNSUPPORTED, "reserve: max_seq beyond 2^30 or max_batch beyond max_seq");
+  const int gi = decode_group_index(n_heads, n_kv);
+  if (gi < 0) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "reserve: GQA group wider than 16");
+  const int G = kGs[gi];
+  // A query attends at most max_seq rows, and at most the window.
+  long long L_hi = (long long)max_seq;
+  const long long w = window_arg(cfg->sliding_window);
+  if (w > 0) L_hi = std::min(L_hi, w);
+  size_t ws = 0, ctr = 0;
+  // Query counts from the target split count up plan one split each (no
+  // partials; counters grow with the count), so the scan stops there.
+  const size_t nq_hi = kv_dtype == VTB_HIP_F32 ? std::max<size_t>(max_batch, 1) : 1;
+  const size_t nq_scan = std::min(nq_hi, (size_t)decode_target_splits(ctx, 1, 1));
+  for (size_t nq = 1; nq <= nq_scan + 1; ++nq) {
+    DecodePlan p;
+    decode_bound(ctx, nq <= nq_scan ? nq : nq_hi, n_kv, D, L_hi, kv_dtype, G, &p);
+    ws = std::max(ws, p.ws_need);
+    ctr = std::max(ctr, p.ctr_need);
+  }
+  int rc = ensure_workspace(ctx, ws, ctr);
+  if (rc) return rc;
+  if (kv_dtype != VTB_HIP_F32 && max_batch > 0) {
+    const long long vt_ld = ((long long)max_seq + 63) / 64 * 64;
+    rc = ensure_scratch(ctx, &ctx->pf, &ctx->pf_bytes, prefill_scratch(n_kv, D, vt_ld, kv_dtype).bytes,
+                        "hipMalloc(prefill scratch)");
+    if (rc) return rc;
+  }
+  if (max_matmul_k > 0 && max_batch > 0) {
+    if (max_matmul_k > 32768) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "reserve: matmul k above 32768");
+    rc = ensure_scratch(ctx, &ctx->qg, &ctx->qg_bytes, qgemm_scratch_bytes(max_batch, max_matmul_k),
+                        "hipMalloc(batched matmul scratch)");
+    if (rc) return rc;
+  }
+  if (rope_base != 0.0f) {
+    RopeArgs ra;
+    rc = rope_args(ctx, D, 0, rope_base, 0, &ra);
+    if (rc) return rc;
+  }
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+  return VTB_HIP_OK;
+}
+
+// Bytes of device scratch the context holds (workspace, counters, prefill
+// and batched-matmul scratch); unchanged by any call that needed no growth.
+extern "C" size_t vtb_hip_scratch_bytes(VtbHipCtx* ctx) {
+  if (!ctx) return 0;
+  return ctx->ws_bytes + ctx->n_counters * sizeof(unsigned) + ctx->pf_bytes + ctx->qg_bytes;
 }

@@ -141,6 +141,8 @@ SIGNATURES = {
     "vtb_hip_segment_matmul_batched_q6_k": ([_P, _P, _P, _S, _P, _S, _S, _S], None),
     "vtb_hip_matmul_batched_q6_k": ([_P, _P, _P, _S, _P, _S, _S, _S], _I),
     "vtb_hip_prefill_attention": ([_P, _P, ctypes.POINTER(AttnConfigC), _S, _S, _P, _P, _P, _P], _I),
+    "vtb_hip_reserve": ([_P, ctypes.POINTER(AttnConfigC), _I, _S, _S, _F], _I),
+    "vtb_hip_scratch_bytes": ([_P], _S),
 }
 
 _lib = None
@@ -432,6 +434,20 @@ class Context:
 
     def wait_idle(self):
         _check(self.h, lib().vtb_hip_wait_idle(self.h), "wait_idle")
+
+    def reserve(self, cfg, kv_dtype, max_batch: int, max_matmul_k: int = 0, rope_base: float = 0.0):
+        """vtb_hip_reserve: grow every on-demand scratch buffer once (prefill.zig
+        Scratch.init's sizing), so later calls within the bounds allocate
+        nothing.  cfg is an AttnConfigC or anything with its five fields."""
+        c = cfg if isinstance(cfg, AttnConfigC) else AttnConfigC(
+            cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.max_seq, cfg.sliding_window)
+        dt = DTYPES[kv_dtype] if isinstance(kv_dtype, str) else kv_dtype
+        _check(self.h, lib().vtb_hip_reserve(self.h, ctypes.byref(c), dt, max_batch, max_matmul_k, rope_base),
+               "reserve")
+
+    @property
+    def scratch_bytes(self) -> int:
+        return int(lib().vtb_hip_scratch_bytes(self.h))
 
     def close(self):
         """Release every buffer and cache still alive on this context, then
