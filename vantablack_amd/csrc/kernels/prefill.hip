@@ -326,10 +326,24 @@ __device__ __forceinline__ void kvt_body(const KvtArgs& a) {
 // ---------------------------------------------------------------- attention
 // X2: q and P enter the MFMAs as two f16 pieces (hi + lo, 22 significant
 // bits), twice the products of the single-piece form.
+// The K and V^T tile stages of one workgroup: two of each, so tile j is read
+// from stage j%2 while tile j+1 is written into the other and one barrier
+// per tile suffices.  K rows are padded by one 16-byte chunk, V^T rows
+// likewise (bank spread).  Declared once per kernel in the entry and shared
+// by both precision paths, so a workgroup holds one set.
+template <int D>
+struct PrefillLds {
+  static constexpr int BN = prefill_block_n(D);
+  __attribute__((aligned(16))) char k0[BN * (D / 8 + 1) * 16];
+  __attribute__((aligned(16))) char k1[BN * (D / 8 + 1) * 16];
+  __attribute__((aligned(16))) char v0[D * (BN / 8 + 1) * 16];
+  __attribute__((aligned(16))) char v1[D * (BN / 8 + 1) * 16];
+};
+
 template <int D, int NW, bool X2>
 __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, const int qb, const int kvh,
                                              const f16x8 (&qf)[D / 16], const f16x8 (&ql)[D / 16],
-                                             const int eq) {
+                                             const int eq, PrefillLds<D>& lds) {
   constexpr int NT = 64 * NW;                 // threads per workgroup
   constexpr int BM = 32 * NW;                 // queries per workgroup (NW waves x 32)
   constexpr int BN = prefill_block_n(D);      // keys per tile
@@ -357,12 +371,11 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   // The register-tight case: the two-piece form of the 4-wave d128 kernel.
   constexpr bool LATE = X2 && NW == 4 && D == 128;
 
-  // Two K and two V^T stages: tile j is read from stage j%2 while tile j+1
-  // is written into the other, so one barrier per tile suffices.
-  __shared__ __attribute__((aligned(16))) char k_lds0[BN * KPB];
-  __shared__ __attribute__((aligned(16))) char k_lds1[BN * KPB];
-  __shared__ __attribute__((aligned(16))) char v_lds0[D * VPB];
-  __shared__ __attribute__((aligned(16))) char v_lds1[D * VPB];
+  static_assert(sizeof(lds.k0) == BN * KPB && sizeof(lds.v0) == D * VPB, "LDS stage size");
+  char* const k_lds0 = lds.k0;
+  char* const k_lds1 = lds.k1;
+  char* const v_lds0 = lds.v0;
+  char* const v_lds1 = lds.v1;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -729,10 +742,11 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
   for (int w = 1; w < NW; ++w) qn2 = fmaxf(qn2, s_qn[w]);
   const bool x2 = (a.hflag && a.hflag[kvh] != 0) ||
                   (a.knorm && sqrtf(qn2) * a.knorm[kvh] * a.scale_log2 > 32.0f);
+  __shared__ PrefillLds<D> lds;
   if (x2)
-    prefill_body<D, NW, true>(a, h, qb, kvh, qf, ql, eq);
+    prefill_body<D, NW, true>(a, h, qb, kvh, qf, ql, eq, lds);
   else
-    prefill_body<D, NW, false>(a, h, qb, kvh, qf, ql, eq);
+    prefill_body<D, NW, false>(a, h, qb, kvh, qf, ql, eq, lds);
 }
 
 }  // namespace vtb
