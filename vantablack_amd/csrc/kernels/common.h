@@ -125,6 +125,18 @@ __device__ inline float group_sum(float v) {
   return v;
 }
 
+// Max over aligned groups of N lanes; every lane of the group gets it.
+template <int N>
+__device__ inline float group_max(float v) {
+  if constexpr (N >= 2) v = fmaxf(v, dpp<DPP_XOR1>(v));
+  if constexpr (N >= 4) v = fmaxf(v, dpp<DPP_XOR2>(v));
+  if constexpr (N >= 8) v = fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
+  if constexpr (N >= 16) v = fmaxf(v, dpp<DPP_MIRROR>(v));
+  if constexpr (N >= 32) v = xor_max<16>(v);
+  if constexpr (N >= 64) v = xor_max<32>(v);
+  return v;
+}
+
 // Reduce across lanes that are STRIDE apart (STRIDE, 2*STRIDE, ... < 64):
 // combines the row groups of a wave that share a column slot.
 template <int STRIDE>
@@ -145,6 +157,18 @@ __device__ inline float stride_max(float v) {
 }
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Power-of-two scaling.  scale_exp(m) is the e for which m * 2^-e lies in
+// [2^14, 2^15), from the biased exponent of the magnitude m, clamped to
+// [-100, 114] (m = 0 or an f32 subnormal gives 0; NaN or inf give 114 and stay
+// NaN / inf); pow2f(e) = 2^e for -126 <= e <= 127.
+__device__ inline int scale_exp(float m) {
+  const int be = (int)((__builtin_bit_cast(uint32_t, m) >> 23) & 0xffu);
+  if (be == 0) return 0;
+  const int e = be - 127 - 14;
+  return e < -100 ? -100 : e;
+}
+__device__ inline float pow2f(int e) { return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23); }
 
 // f32 -> cache dtype, round to nearest even (NaN stays a quiet NaN).
 __device__ inline uint16_t f32_to_bf16_rne(float f) {

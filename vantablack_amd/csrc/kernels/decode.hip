@@ -11,26 +11,36 @@
 //   A workgroup owns one (query b, KV head, row split) and each of its waves
 //   a contiguous run of the split's rows.  Every K/V row is read from HBM once
 //   and used for all q heads of the GQA group, so GQA reuse costs no extra
-//   HBM traffic.
-//   Inside a wave, a K (or V) row of D elements is spread over LPR = D*bytes/16
-//   lanes, one 16-byte load per lane; RPW = 64/LPR rows are read per load
-//   instruction, NIT instructions per tile.  Tiles are double-buffered in
-//   registers: the next tile's loads are issued before this tile's math.
-//   Scores are reduced across the LPR lanes with DPP adds and the rows of a
-//   load instruction combined with DPP / permlane swaps (no LDS); the softmax
-//   is online (running max m, sum l, accumulator acc) per wave, in registers.
+//   HBM traffic.  Two forms of the row loop:
+//   - scalar (f32 caches; GQA groups of 1 or 2): a K (or V) row of D
+//     elements is spread over LPR = D*bytes/16 lanes, one 16-byte load per
+//     lane; scores are reduced across the LPR lanes with DPP adds and
+//     permlane swaps (no LDS);
+//   - MFMA (f16/bf16 caches, GQA groups of 4..16): the G dot products of a
+//     16-key block are v_mfma_f32_16x16x32_{bf16,f16} products of the keys,
+//     loaded straight into operand layout (a lane holds 8 contiguous
+//     elements of one key), with the queries as three pieces of the cache's
+//     16-bit type (q*2^-e = p0 + p1 + p2 exactly, one power of two e per
+//     query), so every product is exact and sums are f32.  Softmax and P.V
+//     stay f32 on the VALU, V in the scalar form's row layout; P crosses
+//     from the score layout to the V layout through the wave's LDS.
+//   Loads are double-buffered in registers: the next tile's loads are issued
+//   before this tile's math.  The softmax is online (running max m, sum l,
+//   accumulator acc) per wave, in registers.
 //   The waves combine into one (m, l, o) partial per workgroup through
 //   per-wave LDS slots summed in a fixed order.  The last-arriving
-//   workgroup of each (query, KV head) merges the partials (log-sum-exp):
-//   the lanes of each float4 column of the result share the partials, load
-//   theirs in one batch of 16-byte buffer loads and combine by a DPP
-//   butterfly, then write out[h] = o/l.  It resets the arrival counter to
-//   zero, so no memset is needed between launches.
+//   workgroup of each (query, KV head) merges the partials: it loads every
+//   partial's (m, l) into LDS and its share of the o columns in one batch of
+//   16-byte loads, scales each by 2^(m - M) for the common max M, sums the
+//   lanes that share a column by DPP, and writes out[h] = o/l.  It resets
+//   the arrival counter to zero, so no memset is needed between launches.
 //   Partials travel through agent-coherent stores/loads and a relaxed
 //   counter; no device-wide fence (L2 writeback/invalidate) is executed.
 //
-// Numerics: all arithmetic is f32 on exactly-upcast K/V.  The 1/sqrt(D)
-// scale is folded with log2(e) into q once, and exp is evaluated as exp2.
+// Numerics: scores and P.V are f32 on exactly-upcast K/V (MFMA form: exact
+// products of the query pieces and the 16-bit keys, f32 sums).  The
+// 1/sqrt(D) scale is folded with log2(e) into q once, and exp is evaluated
+// as exp2.
 //
 // Multi-query form (n_q > 1): query b sits at absolute position pos0 + b and
 // attends [window_start(pos0+b), pos0+b] -- the row loop of
@@ -40,8 +50,6 @@
 #include "../tiles.h"
 
 namespace vtb {
-
-
 
 // RoPE of element i of one head x[0..D) (math.rope / math.ropeHalf,
 // src/kernels/math.zig:85-133): pair partner i^1 (interleaved) or i +- D/2
@@ -60,67 +68,301 @@ __device__ inline float rope_elem(const float* x, int i, const float* inv_freq, 
   return first ? x0 * cs - x1 * sn : x0 * sn + x1 * cs;
 }
 
-// Compile-time integer argument (merge batch size, DPP control) for lambdas.
-template <int N> struct merge_batch { static constexpr int value = N; };
+// Compile-time integer argument (DPP control) for lambdas.
+template <int N> struct ic { static constexpr int value = N; };
 
-template <typename KV, int D, int G, int NIT, int NW>
-__device__ __forceinline__ void decode_body(const DecodeArgs& a) {
-  constexpr int EPL = Unpack<KV>::N;           // elements per lane per load
-  constexpr int LPR = D / EPL;                 // lanes per row
-  constexpr int RPW = 64 / LPR;                // rows per load instruction
-  constexpr int TR = RPW * NIT;                // rows per wave tile
-  constexpr int NT = NW * 64;                  // threads per workgroup
-  static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "bad row split");
+// The (query, KV head, row split) a workgroup owns.
+struct DecodeUnit {
+  int b, kvh, split, h_lo, gs, n_act;
+  long long r0, r1;
+};
 
-  __shared__ float s_m[NW][G];
-  __shared__ float s_l[NW][G];
-  __shared__ float s_o[NW][G][D];
-  __shared__ int s_last;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
-
-  const long long qpos = a.pos0 + b;
+// False when this workgroup has no rows (its query needs fewer splits) or
+// its KV head no query heads.  With HG > 1 the workgroup owns KV heads
+// [HG*y, HG*y + HG) of a uniform GQA map (n_heads == n_kv * G): query slots
+// j = i*G + g are heads h_lo + j.
+template <int HG = 1, int G = 1>
+__device__ inline bool decode_unit(const DecodeArgs& a, DecodeUnit& u) {
+  u.split = blockIdx.x;
+  u.kvh = blockIdx.y;
+  u.b = blockIdx.z;
+  const long long qpos = a.pos0 + u.b;
   const long long wstart = (a.window <= 0 || qpos < a.window) ? 0 : qpos - a.window + 1;
   const long long L = qpos + 1 - wstart;
-  const long long r0 = wstart + (long long)split * a.rows_per_split;
-  const long long r1 = (r0 + a.rows_per_split < qpos + 1) ? r0 + a.rows_per_split : qpos + 1;
-  if (r0 >= r1) return;  // this query needs fewer splits; not counted below
-  const int n_act = (int)((L + a.rows_per_split - 1) / a.rows_per_split);
-
+  u.r0 = wstart + (long long)u.split * a.rows_per_split;
+  u.r1 = (u.r0 + a.rows_per_split < qpos + 1) ? u.r0 + a.rows_per_split : qpos + 1;
+  if (u.r0 >= u.r1) return false;
+  u.n_act = (int)((L + a.rows_per_split - 1) / a.rows_per_split);
+  if constexpr (HG > 1) {
+    u.h_lo = u.kvh * HG * G;
+    u.gs = HG * G;
+    return true;
+  }
   // GQA group of this KV head: h with (h*n_kv)/n_heads == kvh.
-  const int h_lo = (kvh * a.n_heads + a.n_kv - 1) / a.n_kv;
-  const int h_hi = ((kvh + 1) * a.n_heads + a.n_kv - 1) / a.n_kv;
-  const int gs = h_hi - h_lo;
-  if (gs <= 0) return;
+  u.h_lo = (u.kvh * a.n_heads + a.n_kv - 1) / a.n_kv;
+  const int h_hi = ((u.kvh + 1) * a.n_heads + a.n_kv - 1) / a.n_kv;
+  u.gs = h_hi - u.h_lo;
+  return u.gs > 0;
+}
 
-
-  // Fused KV-slot append (forward.zig:267-270): the workgroup whose rows
-  // include the new row pos0 writes this KV head's K and V slice of it,
-  // rounded to the cache dtype, before any of its waves reads it.  Only this
-  // workgroup reads that slice, and the stores complete (vmcnt 0) before the
-  // barrier, so the later loads from the same CU see them.
-  if (a.k_new != nullptr && a.pos0 >= r0 && a.pos0 < r1) {
-    const long long off = a.pos0 * (long long)a.n_kv * D + (long long)kvh * D;
-    const float* kn = a.k_new + (long long)kvh * D;
-    for (int i = threadIdx.x; i < D; i += NT) {
+// Fused KV-slot append (forward.zig:267-270): the workgroup whose rows
+// include the new row pos0 writes this KV head's K and V slice of it,
+// rounded to the cache dtype, before any of its waves reads it.  Only this
+// workgroup reads that slice, and the stores complete (vmcnt 0) before the
+// barrier, so the later loads from the same CU see them.
+template <typename KV, int D, int NT, int HG = 1>
+__device__ __forceinline__ void decode_append(const DecodeArgs& a, const DecodeUnit& u) {
+  if (a.k_new != nullptr && a.pos0 >= u.r0 && a.pos0 < u.r1) {
+    for (int t = threadIdx.x; t < HG * D; t += NT) {
+      const long long kvh = (long long)u.kvh * HG + t / D;
+      const int i = t % D;
+      const long long off = a.pos0 * (long long)a.n_kv * D + kvh * D;
+      const float* kn = a.k_new + kvh * D;
       const float kval = a.rope_inv_freq ? rope_elem<D>(kn, i, a.rope_inv_freq, (float)a.rope_pos, a.rope_half != 0)
                                          : kn[i];
       store_kv<KV>((void*)a.k, off + i, kval);
-      store_kv<KV>((void*)a.v, off + i, a.v_new[(long long)kvh * D + i]);
+      store_kv<KV>((void*)a.v, off + i, a.v_new[kvh * D + i]);
     }
     wait_stores();
     __syncthreads();
   }
+}
+
+// 16-byte agent-coherent (sc1) buffer load / store (whole-vector bit-casts:
+// a bit_cast of one ext-vector element reads element 0 with this compiler).
+__device__ inline f32x4 buffer_load_f4_coherent(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufSc1));
+}
+__device__ inline void buffer_store_f4_coherent(__amdgpu_buffer_rsrc_t r, int off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kBufSc1);
+}
+
+// Merge `count` (<= 32) partials [first, first + count) of src (o:
+// [slot][G][D], (m, l): [slot][G][2]) of this (query, KV head) into
+// out = O / L, or into slot dst of the group partials (O, M, L).
+//   Each float4 column of the result is shared by MP adjacent lanes, lane p
+//   loading slots p, p + MP, ... (SPL at most) in one batch of 16-byte loads.
+//   Alongside, 32 lanes per query g load the slots' (m, l), one slot each,
+//   and reduce them by DPP / permlane: M = max m, weights f = 2^(m - M) and
+//   L = sum l f go to LDS.  After one barrier every lane weights its loaded
+//   slots and the MP lanes of a column sum by DPP.  Slots past `count` load
+//   at an offset past the buffer's range: zeros, no memory access, no
+//   branch.  The order of every sum is fixed, so results are bit-reproducible.
+template <int G, int D, int NT, int MAXS>
+__device__ __forceinline__ void decode_merge(const DecodeArgs& a, const DecodeUnit& u, const float* src_o,
+                                             const float* src_ml, long long first, int count, bool to_out,
+                                             long long dst, float* sh_w, float* sh_ml) {
+  constexpr int C4 = D / 4;
+  constexpr int MC = G * C4;
+  constexpr int MP = NT >= 16 * MC ? 16 : (NT >= MC ? NT / MC : 1);
+  constexpr int CPT = MC > NT ? MC / NT : 1;  // columns per thread
+  constexpr int SPL = (MAXS + MP - 1) / MP;   // slots per lane
+  static_assert(MAXS <= 32, "merge slots");
+  const int tid = threadIdx.x, p = tid % MP;
+  const unsigned bytes_o = (unsigned)count * G * D * 4;
+  const auto ro = buffer_rsrc(src_o + first * G * D, bytes_o);
+  const auto rm = buffer_rsrc(src_ml + first * G * 2, (unsigned)count * G * 8);
+  f32x4 ov[CPT][SPL];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int col = tid / MP + c * (NT / MP);
+    const int g = col / C4, d4 = col % C4;
+#pragma unroll
+    for (int i = 0; i < SPL; ++i) {
+      const int s = p + MP * i;
+      const bool ok = col < MC && s < count;
+      ov[c][i] = buffer_load_f4_coherent(ro, ok ? ((s * G + g) * D + d4 * 4) * 4 : (int)bytes_o);
+    }
+  }
+  // (m, l) of slot s of query g in lane s of half-wave g (loop only when
+  // 32*G exceeds the workgroup).
+  for (int t0 = 0; t0 < 32 * G; t0 += NT) {
+    const int t = t0 + tid;
+    const int g = t >> 5, s = t & 31;
+    float m, l;
+    buffer_load8_coherent(rm, (s < count ? s * G + g : count * G) * 8, m, l);
+    m = s < count ? m : -INFINITY;
+    const float M = group_max<32>(m);
+    const float Ms = M == -INFINITY ? 0.0f : M;
+    const float f = m == -INFINITY ? 0.0f : exp2_fast(m - Ms);
+    const float L = group_sum<32>(l * f);
+    if (t < 32 * G) {
+      sh_w[g * 32 + s] = f;
+      if (s == 0) {
+        sh_ml[2 * g] = M;
+        sh_ml[2 * g + 1] = L;
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int col = tid / MP + c * (NT / MP);
+    const bool live = col < MC;
+    const int g = live ? col / C4 : 0, d4 = col % C4;
+    float O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < SPL; ++i) {
+      const float f = sh_w[g * 32 + ((p + MP * i) & 31)];  // slots past count weigh 0 and loaded 0
+      O[0] = fmaf(ov[c][i].x, f, O[0]);
+      O[1] = fmaf(ov[c][i].y, f, O[1]);
+      O[2] = fmaf(ov[c][i].z, f, O[2]);
+      O[3] = fmaf(ov[c][i].w, f, O[3]);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) O[k] = group_sum<MP>(O[k]);
+    if (live && p == 0 && g < u.gs) {
+      const float M = sh_ml[2 * g], L = sh_ml[2 * g + 1];
+      if (to_out) {
+        float* op = a.out + ((long long)u.b * a.n_heads + u.h_lo + g) * D + d4 * 4;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) op[k] = O[k] / L;
+      } else {
+        const auto rw = buffer_rsrc(a.wg_o + dst * G * D, G * D * 4);
+        buffer_store_f4_coherent(rw, (g * D + d4 * 4) * 4, f32x4{O[0], O[1], O[2], O[3]});
+        if (d4 == 0) {
+          store_coherent(&a.wg_ml[(dst * G + g) * 2 + 0], M);
+          store_coherent(&a.wg_ml[(dst * G + g) * 2 + 1], L);
+        }
+      }
+    }
+  }
+}
+
+// After the row loop: every wave has parked its (m, l, o) for the G slots in
+// LDS (sm, sl, so; a wave without rows has m = -inf).  The workgroup combines
+// them in wave order into its partial (or, with one split, the output) and
+// the last-arriving workgroup of each (query, KV head) merges the partials.
+//   Up to decode_merge_flat(G*D) active splits the merge is flat.  Beyond
+//   that splits form groups of decode_merge_group; the last workgroup of a
+//   group merges the group's partials into a group partial, and the last
+//   group merger merges the group partials.
+template <int G, int D, int NW>
+__device__ __forceinline__ void decode_finish(const DecodeArgs& a, const DecodeUnit& u, const float (*sm)[G],
+                                              const float (*sl)[G], const float (*so)[G][D]) {
+  constexpr int NT = NW * 64;
+  constexpr int C4 = D / 4;
+  constexpr int MC = G * C4;
+  constexpr int FLAT = decode_merge_flat(G * D);
+  constexpr int GS = decode_merge_group;
+  __shared__ float sh_w[32 * G];
+  __shared__ float sh_ml[2 * G];
+  __shared__ int s_last;
+  const bool single = (u.n_act == 1);
+  const long long units = gridDim.y;  // (query, KV head or head group) units per query
+  const long long part = ((long long)u.b * units + u.kvh) * a.n_splits + u.split;
+  const auto rw = buffer_rsrc(a.ws_o + part * G * D, G * D * 4);
+  for (int c = threadIdx.x; c < MC; c += NT) {
+    const int g = c / C4, d4 = c % C4;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm[w][g]);
+    float L = 0.0f;
+    f32x4 O = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      if (sm[w][g] == -INFINITY) continue;
+      const float f = exp2_fast(sm[w][g] - M);
+      L = fmaf(sl[w][g], f, L);
+      const f32x4 ow = *reinterpret_cast<const f32x4*>(&so[w][g][d4 * 4]);
+      O.x = fmaf(ow.x, f, O.x);
+      O.y = fmaf(ow.y, f, O.y);
+      O.z = fmaf(ow.z, f, O.z);
+      O.w = fmaf(ow.w, f, O.w);
+    }
+    if (g >= u.gs) continue;
+    if (single) {
+      float* op = a.out + ((long long)u.b * a.n_heads + u.h_lo + g) * D + d4 * 4;
+      op[0] = O.x / L;
+      op[1] = O.y / L;
+      op[2] = O.z / L;
+      op[3] = O.w / L;
+    } else {
+      // Agent-scope (sc1) stores are coherent across the XCDs' L2s, so the
+      // partials need no cache-wide writeback (a __threadfence() here costs
+      // a full L2 writeback + invalidate per workgroup on this chip).
+      buffer_store_f4_coherent(rw, (g * D + d4 * 4) * 4, O);
+      if (d4 == 0) {
+        store_coherent(&a.ws_ml[(part * G + g) * 2 + 0], M);
+        store_coherent(&a.ws_ml[(part * G + g) * 2 + 1], L);
+      }
+    }
+  }
+  if (single) return;
+
+  const bool two_level = u.n_act > FLAT;
+  const int n_groups = (a.n_splits + GS - 1) / GS;  // group slots per (query, KV head)
+  const int n_grp = two_level ? (u.n_act + GS - 1) / GS : 1;
+  const int grp = two_level ? u.split / GS : 0;
+  const int members = two_level ? ((u.n_act - grp * GS) < GS ? u.n_act - grp * GS : GS) : u.n_act;
+  unsigned* ctr0 = a.counters + ((long long)u.b * units + u.kvh) * (n_groups + 1) * decode_counter_stride;
+
+  // Arrival: every thread's coherent stores complete before the workgroup
+  // counts itself in.
+  auto arrive = [&](unsigned* ctr, int expect) -> bool {
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = (prev == (unsigned)(expect - 1));
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    return s_last != 0;
+  };
+
+  if (!arrive(ctr0 + (long long)grp * decode_counter_stride, members)) return;
+  const long long part0 = ((long long)u.b * units + u.kvh) * a.n_splits;
+  if (!two_level) {
+    decode_merge<G, D, NT, FLAT>(a, u, a.ws_o, a.ws_ml, part0, u.n_act, true, 0, sh_w, sh_ml);
+    return;
+  }
+  const long long gpart0 = ((long long)u.b * units + u.kvh) * n_groups;
+  decode_merge<G, D, NT, GS>(a, u, a.ws_o, a.ws_ml, part0 + (long long)grp * GS, members, false, gpart0 + grp,
+                             sh_w, sh_ml);
+  if (!arrive(ctr0 + (long long)n_groups * decode_counter_stride, n_grp)) return;
+  decode_merge<G, D, NT, GS>(a, u, a.wg_o, a.wg_ml, gpart0, n_grp, true, 0, sh_w, sh_ml);
+}
+
+// ----------------------------------------------------------------- scalar form
+// HG > 1: the workgroup owns HG adjacent KV heads (a uniform GQA map) and
+// one load instruction covers row t of all of them, HG*D contiguous
+// elements: lane l serves head (l / LPR) % HG.  Each workgroup then reads
+// every address class of the row alike; one head per workgroup left the
+// heads at 256-byte offsets 256 mod 1024 about 15% slower to stream (C2
+// shape), and the launch waited for them.
+template <typename KV, int D, int G, int NIT, int NW, int HG>
+__device__ __forceinline__ void decode_scalar_body(const DecodeArgs& a) {
+  constexpr int EPL = Unpack<KV>::N;           // elements per lane per load
+  constexpr int LPR = D / EPL;                 // lanes per head row
+  constexpr int LPH = LPR * HG;                // lanes per load-instruction row
+  constexpr int RPW = 64 / LPH;                // rows per load instruction
+  constexpr int TR = RPW * NIT;                // rows per wave tile
+  constexpr int NT = NW * 64;
+  constexpr int GS = HG * G;                   // query slots of the workgroup
+  static_assert(LPH >= 1 && LPH <= 64 && (64 % LPH) == 0, "bad row split");
+
+  __shared__ float s_m[NW][GS];
+  __shared__ float s_l[NW][GS];
+  __shared__ __attribute__((aligned(16))) float s_o[NW][GS][D];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  DecodeUnit u;
+  if (!decode_unit<HG, G>(a, u)) return;
+  const int b = u.b, h_lo = u.h_lo, gs = u.gs;
+  const long long r0 = u.r0, r1 = u.r1;
+  decode_append<KV, D, NT, HG>(a, u);
 
   const int col = lane % LPR;
-  const int rsub = lane / LPR;
+  const int hh = (lane / LPR) % HG;            // head of the group this lane serves
+  const int rsub = lane / LPH;
+  const long long kvh = (long long)u.kvh * HG + hh;
+  const int qh0 = HG > 1 ? h_lo + hh * G : h_lo;  // first query head of the lane's KV head
   const long long row_stride = (long long)a.n_kv * D;  // elements
-  const char* kbase = (const char*)a.k + ((long long)kvh * D + col * EPL) * KV::bytes;
-  const char* vbase = (const char*)a.v + ((long long)kvh * D + col * EPL) * KV::bytes;
+  const char* kbase = (const char*)a.k + (kvh * D + col * EPL) * KV::bytes;
+  const char* vbase = (const char*)a.v + (kvh * D + col * EPL) * KV::bytes;
 
   // This wave's contiguous rows [w0, w1): an equal share, rounded to RPW.
   const long long per_wave = ((r1 - r0 + NW - 1) / NW + RPW - 1) / RPW * RPW;
@@ -145,14 +387,26 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
   // scale: every load is valid, so none is predicated.  A predicated load per
   // element compiled to one dependent memory round trip each (~5 us of a
   // 17 us GQA launch).
+  // Without RoPE the query loads go out before the first tile's loads (a
+  // wave's loads return in order, so the q wait excludes the tile).
+  u32x4 ka[NIT], va[NIT], kb[NIT], vb[NIT];
+  long long t0 = w0;
   float qv[G][EPL];
   if (a.rope_inv_freq == nullptr) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float* qp = a.q + ((long long)b * a.n_heads + h_lo + (g < gs ? g : 0)) * D + col * EPL;
+      const float* qp = a.q + ((long long)b * a.n_heads + qh0 + (g < gs ? g : 0)) * D + col * EPL;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) qv[g][e] = qp[e];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    issue(t0, ka, va);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
       const float sc = g < gs ? a.scale_log2 : 0.0f;
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) qv[g][e] = qp[e] * sc;
+      for (int e = 0; e < EPL; ++e) qv[g][e] *= sc;
     }
   } else {
     // Fused RoPE of q (wave-uniform branch).  The lane's EPL elements hold
@@ -176,7 +430,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float* qp = a.q + ((long long)b * a.n_heads + h_lo + (g < gs ? g : 0)) * D + col * EPL;
+      const float* qp = a.q + ((long long)b * a.n_heads + qh0 + (g < gs ? g : 0)) * D + col * EPL;
       const float* pp = qp + (lower ? D / 2 : -(D / 2));
       const float sc = g < gs ? a.scale_log2 : 0.0f;
       float x[EPL], y[EPL];
@@ -199,6 +453,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
         qv[g][e] = r * sc;
       }
     }
+    issue(t0, ka, va);
   }
 
   float m[G], l[G], acc[G][EPL];
@@ -234,7 +489,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
         s[g][i] = v;
         mt = fmaxf(mt, v);
       }
-      mt = stride_max<LPR>(mt);
+      mt = stride_max<LPH>(mt);
       const float mn = fmaxf(m[g], mt);  // finite: row t0 is always in range
       const float corr = exp2_fast(m[g] - mn);
       m[g] = mn;
@@ -259,27 +514,30 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     }
   };
 
-  u32x4 ka[NIT], va[NIT], kb[NIT], vb[NIT];
-  long long t0 = w0;
-  if (t0 < w1) issue(t0, ka, va);
-  while (t0 < w1) {
-    if (t0 + TR < w1) issue(t0 + TR, kb, vb);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(t0, ka, va);
-    t0 += TR;
-    if (t0 >= w1) break;
-    if (t0 + TR < w1) issue(t0 + TR, ka, va);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(t0, kb, vb);
-    t0 += TR;
+  // Every issue is unconditional (rows past w1 clamp to row w1 - 1, a line
+  // already in flight): with no load under a branch the compiler's wait
+  // counts stay exact, so each tile waits only for its own loads.
+  if (t0 < w1) {
+    for (;;) {
+      issue(t0 + TR, kb, vb);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(t0, ka, va);
+      t0 += TR;
+      if (t0 >= w1) break;
+      issue(t0 + TR, ka, va);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(t0, kb, vb);
+      t0 += TR;
+      if (t0 >= w1) break;
+    }
   }
 
-  // Combine the row groups of the wave (lanes sharing `col`).
+  // Combine the row groups of the wave (lanes sharing head and `col`).
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    l[g] = stride_sum<LPR>(l[g]);
+    l[g] = stride_sum<LPH>(l[g]);
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[g][e] = stride_sum<LPR>(acc[g][e]);
+    for (int e = 0; e < EPL; ++e) acc[g][e] = stride_sum<LPH>(acc[g][e]);
   }
   // Each wave parks (m, l, acc) in its own LDS slot; the workgroup combine
   // then sums the waves in a fixed order, so results are bit-reproducible.
@@ -288,183 +546,320 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) s_o[wave][g][col * EPL + e] = acc[g][e];
+      for (int e = 0; e < EPL; ++e) s_o[wave][hh * G + g][col * EPL + e] = acc[g][e];
       if (col == 0) {
-        s_m[wave][g] = m[g];
-        s_l[wave][g] = l[g];
+        s_m[wave][hh * G + g] = m[g];
+        s_l[wave][hh * G + g] = l[g];
       }
     }
   }
   __syncthreads();
+  decode_finish<GS, D, NW>(a, u, s_m, s_l, s_o);
+}
 
-  const bool single = (n_act == 1);
-  const long long part = ((long long)b * a.n_kv + kvh) * a.n_splits + split;
-  for (int idx = threadIdx.x; idx < G * D; idx += NT) {
-    const int g = idx / D, d = idx % D;
-    if (g >= gs) continue;
-    float Mg = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) Mg = fmaxf(Mg, s_m[w][g]);
-    float Lg = 0.0f, Og = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      if (s_m[w][g] == -INFINITY) continue;
-      const float f = exp2_fast(s_m[w][g] - Mg);
-      Lg += s_l[w][g] * f;
-      Og += s_o[w][g][d] * f;
-    }
-    if (single) {
-      a.out[((long long)b * a.n_heads + h_lo + g) * D + d] = Og / Lg;
-    } else {
-      // Agent-scope atomic stores are coherent across the XCDs' L2s, so the
-      // partials need no cache-wide writeback (a __threadfence() here costs
-      // a full L2 writeback + invalidate per workgroup on this chip).
-      store_coherent(&a.ws_o[(part * G + g) * D + d], Og);
-      if (d == 0) {
-        store_coherent(&a.ws_ml[(part * G + g) * 2 + 0], Mg);
-        store_coherent(&a.ws_ml[(part * G + g) * 2 + 1], Lg);
-      }
-    }
+// ------------------------------------------------------------------ MFMA form
+template <typename KV> struct DecMfma;
+template <> struct DecMfma<kv_bf16> {
+  __device__ static inline f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
   }
-  if (single) return;
+  // x = piece + rest: piece the nearest bf16, rest exact in f32.
+  __device__ static inline uint16_t piece(float x, float& rest) {
+    const uint16_t h = f32_to_bf16_rne(x);
+    rest = x - __builtin_bit_cast(float, (uint32_t)h << 16);
+    return h;
+  }
+};
+template <> struct DecMfma<kv_f16> {
+  __device__ static inline f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  }
+  __device__ static inline uint16_t piece(float x, float& rest) {
+    const _Float16 h = (_Float16)x;  // v_cvt_f16_f32: round to nearest even
+    rest = x - (float)h;
+    return __builtin_bit_cast(uint16_t, h);
+  }
+};
 
-  // Merge.  Up to decode_merge_flat active splits, the last workgroup to
-  // arrive merges them all (batches of 8 independent loads, as many rounds
-  // as batches).  Beyond that the merge has two levels: splits form groups
-  // of decode_merge_group; the last workgroup of a group merges the group's
-  // partials in one batch into a group partial, and the last group merger
-  // merges the group partials.  A flat merge of a long MQA cache (C5: 256
-  // splits of one KV head) was ~100 us of dependent load rounds through one
-  // workgroup; the extra level costs ~1 us, so short split lists stay flat.
-  constexpr int GS = decode_merge_group;
-  const bool two_level = n_act > decode_merge_flat;
-  const int n_groups = (a.n_splits + GS - 1) / GS;  // group slots per (query, KV head)
-  const int n_grp = two_level ? (n_act + GS - 1) / GS : 1;
-  const int grp = two_level ? split / GS : 0;
-  const int members = two_level ? ((n_act - grp * GS) < GS ? n_act - grp * GS : GS) : n_act;
-  unsigned* ctr0 = a.counters + ((long long)b * a.n_kv + kvh) * (n_groups + 1) * decode_counter_stride;
+// Scores of a 16-key block on v_mfma_f32_16x16x32: A = Q' (16 rows
+// q' = 4*q + p, p = 0..2 the pieces of query q, p = 3 zero), B = K^T (16 key
+// columns), K = 32 head elements per instruction, D/32 instructions.  Lane l
+// supplies row / column l % 16 and elements 8*(l/16) .. +7 of each 32; it
+// receives rows 4*(l/16) .. +3 of column l % 16: the three pieces of query
+// l/16 (of its group of four) against key l % 16.
+template <typename KV, int D, int G, int NW, int NB>
+__device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a) {
+  static_assert(G % 4 == 0, "MFMA decode takes GQA groups of 4, 8, 16");
+  constexpr int NG = G / 4;          // MFMA row groups of four queries
+  constexpr int KM = D / 32;         // MFMAs per 16-key block
+  constexpr int TK = 16 * NB;        // keys per wave tile
+  constexpr int EPL = 8;             // V elements per lane per 16-byte load
+  constexpr int LPR = D / EPL;       // V lanes per row
+  constexpr int RPW = 64 / LPR;      // V rows per load instruction
+  constexpr int VI = TK / RPW;       // V load instructions per tile
+  constexpr int NT = NW * 64;
+  constexpr int QLD = D + 8;         // Q' row stride in LDS (16-byte pad)
+  static_assert(TK % RPW == 0, "V rows per tile");
 
-  // Arrival: every thread's coherent stores complete before the workgroup
-  // counts itself in.
-  auto arrive = [&](unsigned* ctr, int expect) -> bool {
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int last = (prev == (unsigned)(expect - 1));
-      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = last;
+  __shared__ float s_m[NW][G];
+  __shared__ float s_l[NW][G];
+  __shared__ __attribute__((aligned(16))) float s_o[NW][G][D];
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[4 * G][QLD];
+  __shared__ float s_qe[G];
+  __shared__ __attribute__((aligned(16))) float s_p[NW][TK * G + G];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  DecodeUnit u;
+  if (!decode_unit(a, u)) return;
+  const int b = u.b, kvh = u.kvh, h_lo = u.h_lo, gs = u.gs;
+  const long long r0 = u.r0, r1 = u.r1;
+  decode_append<KV, D, NT>(a, u);
+
+  const long long rs = (long long)a.n_kv * D * 2;  // row stride, bytes
+  const char* kbase = (const char*)a.k + (long long)kvh * D * 2 + (lane >> 4) * 16;
+  const char* vbase = (const char*)a.v + (long long)kvh * D * 2 + (lane % LPR) * 16;
+  const int kcol = lane & 15, vrow = lane / LPR, vcol = lane % LPR;
+
+  // This wave's contiguous rows [w0, w1): an equal share, rounded to 16.
+  const long long per_wave = ((r1 - r0 + NW - 1) / NW + 15) / 16 * 16;
+  const long long w0 = r0 + (long long)wave * per_wave;
+  const long long w1 = (w0 + per_wave < r1) ? w0 + per_wave : r1;
+
+  auto issue = [&](long long t0, u32x4 (&kr)[NB][KM], u32x4 (&vr)[VI]) {
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) {
+      const long long row = t0 + 16 * bb + kcol;
+      const long long rc = row < w1 ? row : w1 - 1;  // clamp: never read past the range
+#pragma unroll
+      for (int km = 0; km < KM; ++km) kr[bb][km] = load16(kbase + rc * rs + 64 * km);
     }
-    __syncthreads();
-    return s_last != 0;
-  };
-  // Merge `count` partials src[first .. first+count) of this (query, KV
-  // head) -- [slot][G][D] values, [slot][G][2] (m, l) -- into out = O / L,
-  // or into slot dst of the group partials.  A partial is MC float4 columns;
-  // MP adjacent lanes share a column and lane p takes slots p, p + MP, ...:
-  // MB slots per lane per batch, all loads of a batch in flight together,
-  // then a log-sum-exp butterfly over the MP lanes (DPP, within a row).
-  // Slots past `count`, and lanes without a live column, load at an offset
-  // past the buffer's range: zeros, no memory access, no branch.
-  constexpr int MC = G * D / 4;
-  constexpr int MP = NT >= 16 * MC ? 16 : (NT >= MC ? NT / MC : 1);
-  constexpr int MCP = NT / MP;  // columns per pass
-  auto merge = [&](auto batch, const float* src_o, const float* src_ml, long long first, int count, bool to_out,
-                   long long dst) {
-    constexpr int MB = decltype(batch)::value;
-    const int p = threadIdx.x % MP;
-    const auto ro = buffer_rsrc(src_o + first * G * D, (unsigned)count * G * D * 4);
-    const auto rm = buffer_rsrc(src_ml + first * G * 2, (unsigned)count * G * 8);
-    for (int c0 = 0; c0 < MC; c0 += MCP) {
-      const int c = c0 + (int)threadIdx.x / MP;
-      const int g = c / (D / 4), d4 = c % (D / 4);
-      const bool live = c < MC && g < gs;
-      float M = -INFINITY, L = 0.0f, O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int f0 = 0; f0 < count; f0 += MP * MB) {
-        float ov[MB][4], mv[MB], lv[MB];
 #pragma unroll
-        for (int i = 0; i < MB; ++i) {
-          const int sl = f0 + p + MP * i;
-          const int se = (live && sl < count) ? sl : count;
-          buffer_load16_coherent(ro, ((se * G + g) * D + d4 * 4) * 4, ov[i][0], ov[i][1], ov[i][2], ov[i][3]);
-          buffer_load8_coherent(rm, (se * G + g) * 8, mv[i], lv[i]);
-        }
-        float Mb = M;
-#pragma unroll
-        for (int i = 0; i < MB; ++i) {
-          const bool ok = live && f0 + p + MP * i < count;
-          mv[i] = ok ? mv[i] : -INFINITY;
-          Mb = fmaxf(Mb, mv[i]);
-        }
-        // Branch-free (a branch here lets the compiler split the loads and
-        // sink the parts used under it, a second round trip): with nothing
-        // attended yet Mb stays -inf and every factor is 0.
-        const float Ms = Mb == -INFINITY ? 0.0f : Mb;
-        const float cm = M == -INFINITY ? 0.0f : exp2_fast(M - Ms);
-        L *= cm;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) O[k] *= cm;
-#pragma unroll
-        for (int i = 0; i < MB; ++i) {
-          const float f = mv[i] == -INFINITY ? 0.0f : exp2_fast(mv[i] - Ms);
-          L = fmaf(lv[i], f, L);
-#pragma unroll
-          for (int k = 0; k < 4; ++k) O[k] = fmaf(ov[i][k], f, O[k]);
-        }
-        M = Mb;
-      }
-      // Butterfly over the MP lanes of the column (every lane active).
-      auto fold = [&](auto ctrl) {
-        constexpr int CTRL = decltype(ctrl)::value;
-        const float Mo = dpp<CTRL>(M), Lo = dpp<CTRL>(L);
-        float Oo[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) Oo[k] = dpp<CTRL>(O[k]);
-        const float Mn = fmaxf(M, Mo);
-        const float fa = M == -INFINITY ? 0.0f : exp2_fast(M - Mn);
-        const float fb = Mo == -INFINITY ? 0.0f : exp2_fast(Mo - Mn);
-        L = L * fa + Lo * fb;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) O[k] = O[k] * fa + Oo[k] * fb;
-        M = Mn;
-      };
-      if constexpr (MP >= 2) fold(merge_batch<DPP_XOR1>{});
-      if constexpr (MP >= 4) fold(merge_batch<DPP_XOR2>{});
-      if constexpr (MP >= 8) fold(merge_batch<DPP_HALF_MIRROR>{});
-      if constexpr (MP >= 16) fold(merge_batch<DPP_MIRROR>{});
-      if (live && p == 0) {
-        if (to_out) {
-          float* op = a.out + ((long long)b * a.n_heads + h_lo + g) * D + d4 * 4;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) op[k] = O[k] / L;
-        } else {
-          float* op = a.wg_o + (dst * G + g) * D + d4 * 4;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) store_coherent(op + k, O[k]);
-          store_coherent(&a.wg_ml[(dst * G + g) * 2 + 0], M);
-          store_coherent(&a.wg_ml[(dst * G + g) * 2 + 1], L);
-        }
-      }
+    for (int i = 0; i < VI; ++i) {
+      const long long row = t0 + i * RPW + vrow;
+      const long long rc = row < w1 ? row : w1 - 1;
+      vr[i] = load16(vbase + rc * rs);
     }
   };
 
-  if (!arrive(ctr0 + (long long)grp * decode_counter_stride, members)) return;
-  const long long part0 = ((long long)b * a.n_kv + kvh) * a.n_splits;
-  if (!two_level) {
-    // One slot per lane when the splits fit the column's lanes (C2's 8
-    // splits over 8 lanes); a batch of up to 16 slots per lane otherwise.
-    constexpr int MBF = (decode_merge_flat + MP - 1) / MP < 16 ? (decode_merge_flat + MP - 1) / MP : 16;
-    if (MBF > 1 && n_act <= MP)
-      merge(merge_batch<1>{}, a.ws_o, a.ws_ml, part0, n_act, true, 0);
-    else
-      merge(merge_batch<MBF>{}, a.ws_o, a.ws_ml, part0, n_act, true, 0);
-    return;
+  // Stage Q' in LDS: wave w takes queries w, w + NW, ...; lane l holds
+  // elements E*l .. +E-1.  Each query is scaled by the power of two 2^-e that
+  // brings its largest |x| into [2^14, 2^15) (exact), then split into three
+  // pieces of the cache's 16-bit type.  Slots past the group (gs < G) are
+  // zero.  The query loads are issued before the first K/V tile's: a wave's
+  // loads return in order, so the staging waits only for them while the tile
+  // stays in flight.
+  constexpr int E = D / 64;
+  constexpr int QPW = (G + NW - 1) / NW;  // queries staged per wave
+  const bool rope = a.rope_inv_freq != nullptr;
+  const bool rhalf = a.rope_half != 0;
+  float qx0[QPW][E], qx1[QPW][E], qfr[QPW][E];
+  // Every query load is unconditional (no branch between a load and its
+  // wait): without RoPE the pair loads read the element itself and the
+  // frequency load reads q.
+#pragma unroll
+  for (int j = 0; j < QPW; ++j) {
+    const int g = wave + j * NW;
+    const float* qp = a.q + ((long long)b * a.n_heads + h_lo + (g < gs ? g : 0)) * D;
+    const float* fr = rope ? a.rope_inv_freq : qp;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int i = lane * E + e;
+      const int jf = rhalf ? (i % (D / 2)) : (i >> 1);
+      qx0[j][e] = qp[!rope ? i : rhalf ? jf : (i & ~1)];
+      qx1[j][e] = qp[!rope ? i : rhalf ? jf + D / 2 : (i | 1)];
+      qfr[j][e] = fr[jf];
+    }
   }
-  const long long gpart0 = ((long long)b * a.n_kv + kvh) * n_groups;
-  constexpr int MBG = (GS + MP - 1) / MP;
-  merge(merge_batch<MBG>{}, a.ws_o, a.ws_ml, part0 + (long long)grp * GS, members, false, gpart0 + grp);
-  if (!arrive(ctr0 + (long long)n_groups * decode_counter_stride, n_grp)) return;
-  merge(merge_batch<MBG>{}, a.wg_o, a.wg_ml, gpart0, n_grp, true, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 ka[NB][KM], va[VI], kb[NB][KM], vb[VI];
+  long long t0 = w0;
+  issue(t0, ka, va);  // in flight while the queries are staged
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < QPW; ++j) {
+#pragma clang fp contract(off)
+    const int g = wave + j * NW;
+    float x[E];
+    float mx = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int i = lane * E + e;
+      float xv = qx0[j][e];
+      if (rope) {  // rope_elem's arithmetic on the loaded pair
+        float sn, cs;
+        rope_sincos((float)a.rope_pos * qfr[j][e], &sn, &cs);
+        const bool firstel = rhalf ? (i < D / 2) : ((i & 1) == 0);
+        xv = firstel ? qx0[j][e] * cs - qx1[j][e] * sn : qx0[j][e] * sn + qx1[j][e] * cs;
+      }
+      x[e] = g < gs ? xv * a.scale_log2 : 0.0f;
+      mx = fmaxf(mx, fabsf(x[e]));
+    }
+    const int ex = scale_exp(group_max<64>(mx));
+    const float down = pow2f(-ex);
+    if (g < G) {  // wave-uniform
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int i = lane * E + e;
+        float r1v, r2v, r3v;
+        s_q[4 * g + 0][i] = DecMfma<KV>::piece(x[e] * down, r1v);
+        s_q[4 * g + 1][i] = DecMfma<KV>::piece(r1v, r2v);
+        s_q[4 * g + 2][i] = DecMfma<KV>::piece(r2v, r3v);
+        s_q[4 * g + 3][i] = 0;
+      }
+      if (lane == 0) s_qe[g] = pow2f(ex);
+    }
+  }
+  __syncthreads();
+  u32x4 qa[NG][KM];
+  float qup[NG];
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) {
+#pragma unroll
+    for (int km = 0; km < KM; ++km)
+      qa[gi][km] = *reinterpret_cast<const u32x4*>(&s_q[16 * gi + kcol][32 * km + 8 * (lane >> 4)]);
+    qup[gi] = s_qe[4 * gi + (lane >> 4)];
+  }
+
+  // Online softmax state: lanes of 16-lane row r hold query 4*gi + r's
+  // running max m[gi] and their keys' share of its sum; acc is in V layout.
+  float m[NG], lsum[NG], acc[G][EPL];
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) {
+    m[gi] = -INFINITY;
+    lsum[gi] = 0.0f;
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
+  float* pw = &s_p[wave][0];  // [TK][G] probabilities, then [G] rescale factors
+
+  auto compute = [&](long long tt, const u32x4 (&kr)[NB][KM], const u32x4 (&vr)[VI]) {
+    float s[NB][NG];
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) {
+        f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int km = 0; km < KM; ++km) c = DecMfma<KV>::mma(qa[gi][km], kr[bb][km], c);
+        const float v = ((c.x + c.y) + c.z) * qup[gi];
+        s[bb][gi] = (tt + 16 * bb + kcol < w1) ? v : -INFINITY;
+      }
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+      float mt = s[0][gi];
+#pragma unroll
+      for (int bb = 1; bb < NB; ++bb) mt = fmaxf(mt, s[bb][gi]);
+      mt = group_max<16>(mt);
+      const float mn = fmaxf(m[gi], mt);  // finite: key tt is always in range
+      const float corr = exp2_fast(m[gi] - mn);
+      m[gi] = mn;
+      float ls = 0.0f;
+#pragma unroll
+      for (int bb = 0; bb < NB; ++bb) {
+        const float pv = exp2_fast(s[bb][gi] - mn);
+        ls += pv;
+        pw[(16 * bb + kcol) * G + 4 * gi + (lane >> 4)] = pv;
+      }
+      lsum[gi] = lsum[gi] * corr + ls;
+      if (kcol == 0) pw[TK * G + 4 * gi + (lane >> 4)] = corr;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float cr[G];
+#pragma unroll
+    for (int g4 = 0; g4 < G / 4; ++g4) {
+      const f32x4 c = *reinterpret_cast<const f32x4*>(&pw[TK * G + 4 * g4]);
+      cr[4 * g4 + 0] = c.x;
+      cr[4 * g4 + 1] = c.y;
+      cr[4 * g4 + 2] = c.z;
+      cr[4 * g4 + 3] = c.w;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[g][e] *= cr[g];
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+      float pr[G];
+#pragma unroll
+      for (int g4 = 0; g4 < G / 4; ++g4) {
+        const f32x4 c = *reinterpret_cast<const f32x4*>(&pw[(i * RPW + vrow) * G + 4 * g4]);
+        pr[4 * g4 + 0] = c.x;
+        pr[4 * g4 + 1] = c.y;
+        pr[4 * g4 + 2] = c.z;
+        pr[4 * g4 + 3] = c.w;
+      }
+      float vf[EPL];
+      Unpack<KV>::run(vr[i], vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(pr[g], vf[e], acc[g][e]);
+    }
+    // The next tile's LDS writes come after these reads in this wave's
+    // program order, and a wave's LDS operations complete in order.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  // Every issue is unconditional (rows past w1 clamp to row w1 - 1, a line
+  // already in flight): with no load under a branch the compiler's wait
+  // counts stay exact, so each tile waits only for its own loads.
+  if (t0 < w1) {
+    for (;;) {
+      issue(t0 + TK, kb, vb);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(t0, ka, va);
+      t0 += TK;
+      if (t0 >= w1) break;
+      issue(t0 + TK, ka, va);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(t0, kb, vb);
+      t0 += TK;
+      if (t0 >= w1) break;
+    }
+  }
+
+  // The wave's partial: l over the 16 lanes of each query's row, acc over
+  // the V lanes that share a column.
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) lsum[gi] = group_sum<16>(lsum[gi]);
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[g][e] = stride_sum<LPR>(acc[g][e]);
+  if (kcol == 0) {
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+      s_m[wave][4 * gi + (lane >> 4)] = m[gi];
+      s_l[wave][4 * gi + (lane >> 4)] = lsum[gi];
+    }
+  }
+  if (vrow == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e4 = 0; e4 < EPL / 4; ++e4)
+        *reinterpret_cast<f32x4*>(&s_o[wave][g][vcol * EPL + 4 * e4]) =
+            f32x4{acc[g][4 * e4], acc[g][4 * e4 + 1], acc[g][4 * e4 + 2], acc[g][4 * e4 + 3]};
+  }
+  __syncthreads();
+  decode_finish<G, D, NW>(a, u, s_m, s_l, s_o);
+}
+
+template <typename KV, int D, int G, int HG = 1>
+__device__ __forceinline__ void decode_body(const DecodeArgs& a) {
+  if constexpr (decode_uses_mfma(KV::bytes, G))
+    decode_mfma_body<KV, D, G, decode_waves(KV::bytes, D, G), decode_mfma_nb(D)>(a);
+  else
+    decode_scalar_body<KV, D, G, decode_nit(G), decode_waves(KV::bytes, D, G), HG>(a);
 }
 
 }  // namespace vtb
@@ -484,10 +879,10 @@ __device__ __attribute__((aligned(256), used)) unsigned char vtb_decode_scratch[
 
 // Kernel entry points, one per (KV dtype, head_dim, max GQA group).  Looked
 // up by name with hipModuleGetFunction: vtb_decode_<kv>_d<D>_g<G>.
-#define VTB_DECODE(KVN, KVT, D, G)                                                     \
-  extern "C" __global__ __launch_bounds__(vtb::decode_waves(G) * 64) void             \
-      vtb_decode_##KVN##_d##D##_g##G(vtb::DecodeArgs a) {                             \
-    vtb::decode_body<vtb::KVT, D, G, vtb::decode_nit(G), vtb::decode_waves(G)>(a);    \
+#define VTB_DECODE(KVN, KVT, D, G)                                                         \
+  extern "C" __global__ __launch_bounds__(vtb::decode_waves(vtb::KVT::bytes, D, G) * 64) void \
+      vtb_decode_##KVN##_d##D##_g##G(vtb::DecodeArgs a) {                                 \
+    vtb::decode_body<vtb::KVT, D, G>(a);                                                  \
   }
 
 #define VTB_DECODE_G(KVN, KVT, D) \
@@ -505,3 +900,22 @@ __device__ __attribute__((aligned(256), used)) unsigned char vtb_decode_scratch[
 VTB_DECODE_D(f32, kv_f32)
 VTB_DECODE_D(f16, kv_f16)
 VTB_DECODE_D(bf16, kv_bf16)
+
+// Head-group entry points (uniform GQA maps with groups of 1 or 2 and
+// n_kv a multiple of the group): vtb_decodeh_<kv>_d<D>_g<G>, HG =
+// decode_head_group(kv bytes, D) KV heads per workgroup.
+#define VTB_DECODEH(KVN, KVT, D, G)                                                        \
+  extern "C" __global__ __launch_bounds__(vtb::decode_waves(vtb::KVT::bytes, D, G) * 64) void \
+      vtb_decodeh_##KVN##_d##D##_g##G(vtb::DecodeArgs a) {                                \
+    vtb::decode_body<vtb::KVT, D, G, vtb::decode_head_group(vtb::KVT::bytes, D)>(a);      \
+  }
+#define VTB_DECODEH_D(KVN, KVT) \
+  VTB_DECODEH(KVN, KVT, 64, 1)  \
+  VTB_DECODEH(KVN, KVT, 64, 2)  \
+  VTB_DECODEH(KVN, KVT, 128, 1) \
+  VTB_DECODEH(KVN, KVT, 128, 2) \
+  VTB_DECODEH(KVN, KVT, 256, 1) \
+  VTB_DECODEH(KVN, KVT, 256, 2)
+VTB_DECODEH_D(f32, kv_f32)
+VTB_DECODEH_D(f16, kv_f16)
+VTB_DECODEH_D(bf16, kv_bf16)

@@ -95,17 +95,7 @@ __device__ inline void lane_halves(float v, float& lo_half, float& hi_half) {
 }
 
 // ---------------------------------------------------------------- pre-pass
-// Power-of-two scaling.  scale_exp(m) is the e for which m * 2^-e lies in
-// [2^14, 2^15), from the biased exponent of the magnitude m, clamped to
-// [-100, 114] (m = 0 or an f32 subnormal gives 0; NaN or inf give 114 and stay
-// NaN / inf); pow2f(e) = 2^e for -126 <= e <= 127.
-__device__ inline int scale_exp(float m) {
-  const int be = (int)((__builtin_bit_cast(uint32_t, m) >> 23) & 0xffu);
-  if (be == 0) return 0;
-  const int e = be - 127 - 14;
-  return e < -100 ? -100 : e;
-}
-__device__ inline float pow2f(int e) { return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23); }
+// Power-of-two scaling: scale_exp / pow2f (common.h).
 
 // Largest |x| of the eight bf16 values of w, as bf16 magnitude bits.
 __device__ inline uint32_t bf16x8_absmax(u32x4 w) {

@@ -4,9 +4,10 @@
 
 namespace vtb {
 
-// Decode: 16-byte loads per lane per wave tile (NIT), by GQA group width.
-// Tiles are double-buffered, so a wave keeps 2 x 2 x NIT loads in flight;
-// NIT shrinks as the group widens to keep the q/acc registers resident.
+// Decode, scalar form (f32 caches, and GQA groups of 1 or 2): 16-byte loads
+// per lane per wave tile (NIT), by GQA group width.  Tiles are
+// double-buffered, so a wave keeps 2 x 2 x NIT loads in flight; NIT shrinks
+// as the group widens to keep the q/acc registers resident.
 #ifndef VTB_DECODE_NIT1
 #define VTB_DECODE_NIT1 4
 #endif
@@ -23,30 +24,65 @@ constexpr int decode_nit(int g) {
   return g == 1 ? VTB_DECODE_NIT1 : g <= 4 ? VTB_DECODE_NIT4 : (g == 8 ? VTB_DECODE_NIT8 : 1);
 }
 
-// Waves per decode workgroup.  For g = 1 one wave per SIMD streams best:
-// 16-wave workgroups keep 4x the loads in flight per CU and measured ~1.6 us
-// slower per C2 launch at 8K context (deeper DRAM queues, 4x the waves to
-// dispatch), with the same bytes moved.
+// Decode, MFMA form: f16/bf16 caches with GQA groups of 4 or more compute
+// the G query-key dot products of each 16-key block on
+// v_mfma_f32_16x16x32_{bf16,f16} (queries as three exact pieces); the
+// softmax and P.V stay f32 on the VALU.
+constexpr bool decode_uses_mfma(int kv_bytes, int g) { return kv_bytes == 2 && g >= 4; }
+// 16-key blocks per wave tile (double-buffered), by head_dim.
+#ifndef VTB_DECODE_MFMA_NB
+#define VTB_DECODE_MFMA_NB 2
+#endif
+constexpr int decode_mfma_nb(int head_dim) { return head_dim >= 256 ? 1 : VTB_DECODE_MFMA_NB; }
+
+// Waves per decode workgroup.  Scalar form: for g = 1 one wave per SIMD
+// streams best: 16-wave workgroups keep 4x the loads in flight per CU and
+// measured ~1.6 us slower per C2 launch at 8K context (deeper DRAM queues,
+// 4x the waves to dispatch), with the same bytes moved.
 #ifndef VTB_DECODE_WAVES4
 #define VTB_DECODE_WAVES4 8
 #endif
 #ifndef VTB_DECODE_WAVES8
 #define VTB_DECODE_WAVES8 8
 #endif
-constexpr int decode_waves(int g) {
-  return g == 1 ? VTB_DECODE_WAVES1 : g <= 4 ? VTB_DECODE_WAVES4 : (g == 8 ? VTB_DECODE_WAVES8 : 4);
+// MFMA form: 8 waves (two per SIMD) for head_dim <= 128 with groups of 4;
+// 4 waves, with the register file of a whole SIMD each, for head_dim 256 or
+// groups of 8 or 16 (their query pieces, accumulators and double-buffered
+// tiles exceed 256 registers).
+#ifndef VTB_DECODE_MFMA_WAVES
+#define VTB_DECODE_MFMA_WAVES 8
+#endif
+#ifndef VTB_DECODE_MFMA_WAVES_D256
+#define VTB_DECODE_MFMA_WAVES_D256 4
+#endif
+constexpr int decode_waves(int kv_bytes, int head_dim, int g) {
+  return decode_uses_mfma(kv_bytes, g) ? (head_dim >= 256 || g >= 8 ? VTB_DECODE_MFMA_WAVES_D256 : VTB_DECODE_MFMA_WAVES)
+         : g == 1                      ? VTB_DECODE_WAVES1
+         : g <= 4                      ? VTB_DECODE_WAVES4
+                                       : (g == 8 ? VTB_DECODE_WAVES8 : 4);
+}
+
+// Scalar form, uniform GQA maps with groups of 1 or 2: KV heads per
+// workgroup, as many as fill one 64-lane load instruction with one row (at
+// most 4; 1 when a single head's row already fills it).
+constexpr int decode_head_group(int kv_bytes, int head_dim) {
+  return 64 / (head_dim * kv_bytes / 16) >= 4 ? 4 : 64 / (head_dim * kv_bytes / 16);
 }
 
 // Split-K arrival counters sit one per 128 bytes, so the atomics of
 // different (query, KV head) pairs never share a cache line.
 constexpr int decode_counter_stride = 32;
 
-// Split merge: up to decode_merge_flat active splits are merged by the
-// last workgroup alone; beyond that, groups of decode_merge_group splits are
-// merged by each group's last workgroup in one batch of loads, then the
-// group partials by the last group merger.
-constexpr int decode_merge_flat = 32;
+// Split merge: up to decode_merge_flat(G * head_dim) active splits are
+// merged by the last workgroup alone; beyond that, groups of
+// decode_merge_group splits are merged by each group's last workgroup, then
+// the group partials by the last group merger.  The flat limit keeps the
+// last workgroup's reads near 64 KiB.
+constexpr int decode_merge_flat(int partial_floats) { return partial_floats <= 512 ? 32 : 16; }
 constexpr int decode_merge_group = 16;
+// Splits per (query, KV head) are capped so the group partials fit one
+// merge: decode_merge_group groups of decode_merge_group splits.
+constexpr int decode_max_splits = decode_merge_group * decode_merge_group;
 
 // The decode code object's file-scope scratch (vtb_decode_scratch), used by
 // the no-allocation decode entry: arrival counters in the first
@@ -54,9 +90,10 @@ constexpr int decode_merge_group = 16;
 constexpr unsigned long long decode_scratch_bytes = 8ull << 20;
 constexpr unsigned long long decode_scratch_counter_bytes = 256ull << 10;
 
-// Rows read by one wave load instruction (the split granularity).
-constexpr int decode_rows_per_load(int head_dim, int kv_bytes) {
-  return 64 / (head_dim * kv_bytes / 16);
+// Rows per split are a multiple of this: the rows one wave load instruction
+// covers (scalar form) or one 16-key MFMA block.
+constexpr int decode_split_quantum(int head_dim, int kv_bytes, int g, int hg = 1) {
+  return decode_uses_mfma(kv_bytes, g) ? 16 : 64 / (head_dim * kv_bytes / 16 * hg);
 }
 
 // Prefill (MFMA): 4 waves x 32 queries per workgroup; keys per LDS tile by

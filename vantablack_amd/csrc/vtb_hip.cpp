@@ -81,6 +81,7 @@ struct VtbHipCtx {
   hipModule_t mod_decode = nullptr, mod_prefill = nullptr, mod_kvcopy = nullptr, mod_gemv = nullptr,
               mod_qgemm = nullptr;
   hipFunction_t f_decode[kNumKv][kNumD][kNumG] = {};
+  hipFunction_t f_decodeh[kNumKv][kNumD][2] = {};  // vtb_decodeh_<kv>_d<D>_g<1|2>: head-group form
   hipFunction_t f_prefill[kNumD] = {};
   hipFunction_t f_prefill8[kNumD] = {};  // wide (8-wave) variant, d <= 128
   hipFunction_t f_kvt[kNumKv][kNumD] = {};  // conversion pass per cache dtype (f16, bf16)
@@ -272,18 +273,20 @@ void decode_sizes(size_t n_q, size_t n_kv, size_t head_dim, int G, long long n_s
 long long decode_target_splits(VtbHipCtx* ctx, size_t n_q, size_t n_kv) {
   const long long target = env_int("VTB_DECODE_TARGET_WGS", std::max(ctx->cu_count, 1));
   const long long units = (long long)(n_kv * n_q);
-  return std::max(1LL, (target + units - 1) / units);
+  return std::min((long long)vtb::decode_max_splits, std::max(1LL, (target + units - 1) / units));
 }
-int plan_decode(VtbHipCtx* ctx, size_t n_q, size_t n_kv, size_t head_dim, long long Lmax, int dtype, int G,
-                DecodePlan* p) {
-  const long long quantum = vtb::decode_rows_per_load((int)head_dim, kKvBytes[dtype]);
-  const long long want = decode_target_splits(ctx, n_q, n_kv);
+// units: (query, KV head group) units per query; G: the kernel's group
+// width; HG: KV heads per workgroup (the partial has HG*G query slots).
+int plan_decode(VtbHipCtx* ctx, size_t n_q, size_t units, size_t head_dim, long long Lmax, int dtype, int G,
+                int HG, DecodePlan* p) {
+  const long long quantum = vtb::decode_split_quantum((int)head_dim, kKvBytes[dtype], G, HG);
+  const long long want = decode_target_splits(ctx, n_q, units);
   long long rps = (Lmax + want - 1) / want;
   rps = std::max(quantum, (rps + quantum - 1) / quantum * quantum);
   const long long n_splits = (Lmax + rps - 1) / rps;
   if (n_splits > 65535) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "too many splits");
   p->rps = rps;
-  decode_sizes(n_q, n_kv, head_dim, G, n_splits, p);
+  decode_sizes(n_q, units, head_dim, G * HG, n_splits, p);
   return VTB_HIP_OK;
 }
 
@@ -291,12 +294,25 @@ int plan_decode(VtbHipCtx* ctx, size_t n_q, size_t n_kv, size_t head_dim, long l
 // Lmax_hi: rows per split are at least ceil(L / want) and at least one
 // load quantum, so a launch has at most min(want, ceil(Lmax_hi / quantum))
 // splits, and the sizes grow with the split count.
-void decode_bound(VtbHipCtx* ctx, size_t n_q, size_t n_kv, size_t head_dim, long long Lmax_hi, int dtype, int G,
-                  DecodePlan* p) {
-  const long long quantum = vtb::decode_rows_per_load((int)head_dim, kKvBytes[dtype]);
-  const long long n_splits = std::min(decode_target_splits(ctx, n_q, n_kv), (Lmax_hi + quantum - 1) / quantum);
+void decode_bound(VtbHipCtx* ctx, size_t n_q, size_t units, size_t head_dim, long long Lmax_hi, int dtype, int G,
+                  int HG, DecodePlan* p) {
+  const long long quantum = vtb::decode_split_quantum((int)head_dim, kKvBytes[dtype], G, HG);
+  const long long n_splits = std::min(decode_target_splits(ctx, n_q, units), (Lmax_hi + quantum - 1) / quantum);
   p->rps = 0;
-  decode_sizes(n_q, n_kv, head_dim, G, std::max(1LL, n_splits), p);
+  decode_sizes(n_q, units, head_dim, G * HG, std::max(1LL, n_splits), p);
+}
+
+// KV heads per decode workgroup: the head-group form (decode_head_group
+// heads, one row of all of them per load instruction) for uniform GQA maps
+// with groups of 1 or 2 on the scalar path whose KV-head count it divides;
+// VTB_DECODE_HG=1 forces one head per workgroup.
+int decode_heads_per_wg(size_t n_heads, size_t n_kv, size_t head_dim, int dtype, int G) {
+  if (vtb::decode_uses_mfma(kKvBytes[dtype], G) || G > 2 || n_heads != n_kv * (size_t)G) return 1;
+  const int hg = vtb::decode_head_group(kKvBytes[dtype], (int)head_dim);
+  if (hg <= 1 || n_kv % (size_t)hg != 0) return 1;
+  const char* e = getenv("VTB_DECODE_HG");
+  if (e && atoi(e) == 1) return 1;
+  return hg;
 }
 
 // GQA group width the decode kernels are instantiated for (1, 2, 4, 8, 16),
@@ -341,8 +357,9 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
     long long ws = (window <= 0 || qp < window) ? 0 : qp - window + 1;
     Lmax = std::max(Lmax, qp + 1 - ws);
   }
+  const int HG = decode_heads_per_wg(n_heads, n_kv, head_dim, dtype, G);
   DecodePlan pl;
-  int rc0 = plan_decode(ctx, n_q, n_kv, head_dim, Lmax, dtype, G, &pl);
+  int rc0 = plan_decode(ctx, n_q, n_kv / HG, head_dim, Lmax, dtype, G, HG, &pl);
   if (rc0) return rc0;
   const long long rps = pl.rps, n_splits = pl.n_splits;
   const size_t n_part = pl.n_part, n_gpart = pl.n_gpart, ws_need = pl.ws_need, ctr_need = pl.ctr_need;
@@ -387,8 +404,9 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
   a.rope_inv_freq = rope.inv_freq;
   a.rope_pos = rope.pos;
   a.rope_half = rope.half;
-  return launch(ctx, ctx->f_decode[dtype][di][gi], (unsigned)n_splits, (unsigned)n_kv,
-                (unsigned)n_q, 64 * vtb::decode_waves(G), &a);
+  hipFunction_t f = HG > 1 ? ctx->f_decodeh[dtype][di][G - 1] : ctx->f_decode[dtype][di][gi];
+  return launch(ctx, f, (unsigned)n_splits, (unsigned)(n_kv / HG), (unsigned)n_q,
+                64 * vtb::decode_waves(kKvBytes[dtype], (int)head_dim, G), &a);
 }
 
 // Prefill scratch layout for keys [0, vt_ld) of n_kv heads: f16 V^T
@@ -793,6 +811,10 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
       for (int gi = 0; ok && gi < kNumG; ++gi) {
         snprintf(name, sizeof name, "vtb_decode_%s_d%d_g%d", kKvNames[kv], D, kGs[gi]);
         ok = hipModuleGetFunction(&ctx->f_decode[kv][di][gi], ctx->mod_decode, name) == hipSuccess;
+      }
+      for (int g = 1; ok && g <= 2; ++g) {
+        snprintf(name, sizeof name, "vtb_decodeh_%s_d%d_g%d", kKvNames[kv], D, g);
+        ok = hipModuleGetFunction(&ctx->f_decodeh[kv][di][g - 1], ctx->mod_decode, name) == hipSuccess;
       }
       if (kv != VTB_HIP_F32) {
         snprintf(name, sizeof name, "vtb_kvt_%s_d%d", kKvNames[kv], D);
@@ -1626,7 +1648,8 @@ extern "C" int vtb_hip_reserve(VtbHipCtx* ctx, const VtbHipAttnConfig* cfg, int 
   const size_t nq_scan = std::min(nq_hi, (size_t)decode_target_splits(ctx, 1, 1));
   for (size_t nq = 1; nq <= nq_scan + 1; ++nq) {
     DecodePlan p;
-    decode_bound(ctx, nq <= nq_scan ? nq : nq_hi, n_kv, D, L_hi, kv_dtype, G, &p);
+    const int HG = decode_heads_per_wg(n_heads, n_kv, D, kv_dtype, G);
+    decode_bound(ctx, nq <= nq_scan ? nq : nq_hi, n_kv / HG, D, L_hi, kv_dtype, G, HG, &p);
     ws = std::max(ws, p.ws_need);
     ctr = std::max(ctr, p.ctr_need);
   }
