@@ -328,10 +328,10 @@ __device__ __forceinline__ void decode_finish(const DecodeArgs& a, const DecodeU
 // ----------------------------------------------------------------- scalar form
 // HG > 1: the workgroup owns HG adjacent KV heads (a uniform GQA map) and
 // one load instruction covers row t of all of them, HG*D contiguous
-// elements: lane l serves head (l / LPR) % HG.  Each workgroup then reads
-// every address class of the row alike; one head per workgroup left the
-// heads at 256-byte offsets 256 mod 1024 about 15% slower to stream (C2
-// shape), and the launch waited for them.
+// elements: lane l serves head (l / LPR) % HG.  With one head per workgroup
+// the heads at 256-byte offsets 256 mod 1024 streamed about 15% slower than
+// the others (C2 shape: 21.8 against 19.0 us), and the launch waited for
+// them; with two heads per workgroup every workgroup mixes address classes.
 template <typename KV, int D, int G, int NIT, int NW, int HG>
 __device__ __forceinline__ void decode_scalar_body(const DecodeArgs& a) {
   constexpr int EPL = Unpack<KV>::N;           // elements per lane per load

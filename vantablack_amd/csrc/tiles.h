@@ -63,10 +63,12 @@ constexpr int decode_waves(int kv_bytes, int head_dim, int g) {
 }
 
 // Scalar form, uniform GQA maps with groups of 1 or 2: KV heads per
-// workgroup, as many as fill one 64-lane load instruction with one row (at
-// most 4; 1 when a single head's row already fills it).
+// workgroup (2 when two heads' rows fit one 64-lane load instruction).  At
+// the C2 shape two heads per workgroup measured 26.0 us per launch against
+// 26.2-26.4 for four (whose 32-way merge reads 4x the partials) and 27.1
+// for one.
 constexpr int decode_head_group(int kv_bytes, int head_dim) {
-  return 64 / (head_dim * kv_bytes / 16) >= 4 ? 4 : 64 / (head_dim * kv_bytes / 16);
+  return 64 / (head_dim * kv_bytes / 16) >= 2 ? 2 : 1;
 }
 
 // Split-K arrival counters sit one per 128 bytes, so the atomics of
