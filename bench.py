@@ -217,6 +217,21 @@ def bench_decode_cfg(ctx, torch, name, n_layers, n_heads, n_kv, d, kv, L, steps=
             "shape": f"{n_layers} layers, {n_heads}q/{n_kv}kv heads, d{d}, {kv} KV, attended L={L}"}
 
 
+def decode_kernel_name(n_heads, n_kv, d, kv):
+    """The decode kernel one launch runs, by the launcher's rule
+    (launch_decode / decode_heads_per_wg in vantablack_amd/csrc/vtb_hip.cpp):
+    the MFMA form for f16/bf16 caches with GQA groups of 4 or more, the
+    head-group form (two KV heads per workgroup) for uniform groups of 1-2
+    when a row of two heads fits one load instruction, else the one-head
+    scalar form; the group width rounds up to 1, 2, 4, 8 or 16."""
+    g = -(-n_heads // n_kv)
+    G = next(x for x in (1, 2, 4, 8, 16) if x >= g)
+    eb = {"f32": 4, "f16": 2, "bf16": 2}[kv]
+    hg = 2 if 64 // (d * eb // 16) >= 2 else 1
+    head_group = not (eb == 2 and G >= 4) and G <= 2 and n_heads == n_kv * G and hg > 1 and n_kv % hg == 0
+    return f"vtb_decode{'h' if head_group else ''}_{kv}_d{d}_g{G}"
+
+
 def prefill_flops(L, n_heads, d):
     return 4 * n_heads * d * L * (L + 1) // 2
 
@@ -644,7 +659,7 @@ PMC_PREFILL = [("C4", 32, 8, 128, 8192), ("C5", 8, 1, 256, 4096)]
 def pmc_workload():
     """The launches of every measured kernel shape, for rocprofv3 --pmc runs:
     the calibration copy (vtb_copy_f32); the fused append + decode launch of
-    C2 (vtb_decode_f16_d128_g1), C3 (vtb_decode_bf16_d128_g4) and C5
+    C2 (vtb_decodeh_f16_d128_g1), C3 (vtb_decode_bf16_d128_g4) and C5
     (vtb_decode_bf16_d256_g8), each over PMC_DECODE's layer count of distinct
     cache layers; and the C4 (8192 tokens) and C5 (4096 tokens) causal
     prefill calls: the statistics and conversion passes (vtb_kvstat_*,
@@ -924,7 +939,8 @@ def main():
     ctx.close()
     traffic = load_traffic()
     counters = load_counters()
-    dec_tr = traffic.get("vtb_decode_f16_d128_g1", {}).get("traffic_bytes")
+    dec_kernel = decode_kernel_name(32, 32, 128, "f16")
+    dec_tr = traffic.get(dec_kernel, {}).get("traffic_bytes")
     pre_kernel = pre["C4_L8192"]["kernel"] if pre else None
     pre_tr = traffic.get(pre_kernel, {}).get("traffic_bytes") if pre_kernel else None
 
@@ -954,13 +970,14 @@ def main():
             "frac": round(dec["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": dec_tr,
             "traffic_source": "profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-calibrated; L=8193)"
             if dec_tr else None,
-            "kernel": "vtb_decode_f16_d128_g1 (KV append fused)",
+            "kernel": f"{dec_kernel} (KV append fused)",
             "avg_launch_us": round(dec["avg_launch_s"] * 1e6, 3),
             "bytes_per_launch": int(dec["bytes_per_launch"]),
         },
     }
     if dec_more:
-        for cfg, kname in (("C3", "vtb_decode_bf16_d128_g4"), ("C5", "vtb_decode_bf16_d256_g8")):
+        for cfg, kname in (("C3", decode_kernel_name(32, 8, 128, "bf16")),
+                           ("C5", decode_kernel_name(8, 1, 256, "bf16"))):
             if cfg in dec_more:
                 dec_more[cfg]["counters"] = decode_counter_field(kname, traffic.get(kname), counters.get(kname))
         line["decode_other_configs"] = dec_more
