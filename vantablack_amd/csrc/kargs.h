@@ -18,10 +18,10 @@ struct DecodeArgs {
   const void* k;        // layer base: row t at k + t*n_kv*D elements
   const void* v;
   float* out;           // [n_q][n_heads][D] f32
-  float* ws_o;          // [n_q][n_kv][n_splits][G][D]
-  float* ws_ml;         // [n_q][n_kv][n_splits][G][2]
-  float* wg_o;          // [n_q][n_kv][n_groups][G][D] group partials
-  float* wg_ml;         // [n_q][n_kv][n_groups][G][2]
+  float* ws_o;          // [n_q][units][n_splits][G][D]
+  float* ws_ml;         // [n_q][units][n_splits][G][2]
+  float* wg_o;          // [n_q][units][n_groups][G][D] group partials
+  float* wg_ml;         // [n_q][units][n_groups][G][2]
   unsigned* counters;   // [n_q][n_kv][n_groups + 1] x decode_counter_stride, zero between launches
   int n_heads;
   int n_kv;

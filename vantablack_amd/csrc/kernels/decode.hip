@@ -137,41 +137,72 @@ __device__ inline void buffer_store_f4_coherent(__amdgpu_buffer_rsrc_t r, int of
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kBufSc1);
 }
 
-// Merge `count` (<= 32) partials [first, first + count) of src (o:
-// [slot][G][D], (m, l): [slot][G][2]) of this (query, KV head) into
-// out = O / L, or into slot dst of the group partials (O, M, L).
-//   Each float4 column of the result is shared by MP adjacent lanes, lane p
-//   loading slots p, p + MP, ... (SPL at most) in one batch of 16-byte loads.
+// Split-merge thread layout.  When the result has at least as many float4
+// columns as the workgroup has threads (WIDE), thread t takes columns
+// t, t + NT, ... of every slot: each load instruction reads 1 KB of one
+// slot.  Otherwise the columns form blocks of 16; a wave takes one block,
+// its four 16-lane quarters reading four different slots (256 bytes of one
+// slot each), and with more waves than blocks the extra waves take further
+// slots of the same block (WPB waves per block).  The segmented form costs
+// more instructions per loaded byte, which the one-wave-per-SIMD d256
+// kernels feel (C5: 2.9 us per launch), so it is used only where the wide
+// form would leave threads idle.
+template <int G, int D, int NT>
+struct MergeShape {
+  static constexpr int NW = NT / 64;
+  static constexpr int MC = G * D / 4;                    // float4 columns
+  static constexpr bool WIDE = MC >= NT;
+  static constexpr int NBLK = MC / 16;                    // 16-column blocks
+  static constexpr int WPB = WIDE || NBLK >= NW ? 1 : NW / NBLK;  // waves per block
+  static constexpr int CPT = WIDE ? MC / NT : (NBLK >= NW ? NBLK / NW : 1);  // columns (blocks) per thread
+  static constexpr int MP = WIDE ? 1 : 4 * WPB;          // threads per column
+};
+
+// Merge `count` (<= 32) partials [first, first + count) of one (query, KV
+// head) unit into out = O / L, or into a group partial (dst_o, dst_ml).
+// src_o: the unit's [slot][G][D]; src_ml: the unit's [slot][G][2].
+//   Every thread loads its column of slots p, p + MP, ... (MergeShape) in
+//   one batch of 16-byte loads; each lane quad reads one 64-byte line.
+//   (With the slots spread over adjacent lanes instead, a C3-sized merge of
+//   64 KB took 2.1 against 0.9 us: each quad touched four lines.)
 //   Alongside, 32 lanes per query g load the slots' (m, l), one slot each,
 //   and reduce them by DPP / permlane: M = max m, weights f = 2^(m - M) and
-//   L = sum l f go to LDS.  After one barrier every lane weights its loaded
-//   slots and the MP lanes of a column sum by DPP.  Slots past `count` load
-//   at an offset past the buffer's range: zeros, no memory access, no
-//   branch.  The order of every sum is fixed, so results are bit-reproducible.
+//   L = sum l f go to LDS.  After one barrier every thread weights its
+//   slots, the quarters of a wave add by permlane, and the WPB waves of a
+//   block through LDS, in a fixed order.  Slots past `count` load at an
+//   offset past the buffer's range: zeros, no memory access, no branch.
+//   Every sum has a fixed order, so results are bit-reproducible.
 template <int G, int D, int NT, int MAXS>
 __device__ __forceinline__ void decode_merge(const DecodeArgs& a, const DecodeUnit& u, const float* src_o,
                                              const float* src_ml, long long first, int count, bool to_out,
-                                             long long dst, float* sh_w, float* sh_ml) {
+                                             float* dst_o, float* dst_ml, float* sh_w, float* sh_ml,
+                                             f32x4* sh_red) {
+  using S = MergeShape<G, D, NT>;
   constexpr int C4 = D / 4;
   constexpr int MC = G * C4;
-  constexpr int MP = NT >= 16 * MC ? 16 : (NT >= MC ? NT / MC : 1);
-  constexpr int CPT = MC > NT ? MC / NT : 1;  // columns per thread
-  constexpr int SPL = (MAXS + MP - 1) / MP;   // slots per lane
-  static_assert(MAXS <= 32, "merge slots");
-  const int tid = threadIdx.x, p = tid % MP;
+  constexpr int MP = S::MP, CPT = S::CPT;
+  constexpr int SPL = (MAXS + MP - 1) / MP;  // slots per thread
+  static_assert(MAXS <= 32 && MC % 16 == 0, "merge shape");
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int p = S::WIDE ? 0 : S::WPB > 1 ? ((w / S::NBLK) << 2) | (lane >> 4) : lane >> 4;
+  const int blk0 = S::WPB > 1 ? w % S::NBLK : w;
+  // Column of pass c.
+  auto column = [&](int c) { return S::WIDE ? tid + c * NT : (blk0 + c * S::NW) * 16 + (lane & 15); };
+  // count is uniform; saying so keeps the buffer resources in SGPRs (the
+  // compiler otherwise wrapped every load of the d256 merge in a
+  // readfirstlane loop).
+  count = __builtin_amdgcn_readfirstlane(count);
   const unsigned bytes_o = (unsigned)count * G * D * 4;
   const auto ro = buffer_rsrc(src_o + first * G * D, bytes_o);
   const auto rm = buffer_rsrc(src_ml + first * G * 2, (unsigned)count * G * 8);
   f32x4 ov[CPT][SPL];
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
-    const int col = tid / MP + c * (NT / MP);
-    const int g = col / C4, d4 = col % C4;
+    const int col = column(c);
 #pragma unroll
     for (int i = 0; i < SPL; ++i) {
       const int s = p + MP * i;
-      const bool ok = col < MC && s < count;
-      ov[c][i] = buffer_load_f4_coherent(ro, ok ? ((s * G + g) * D + d4 * 4) * 4 : (int)bytes_o);
+      ov[c][i] = buffer_load_f4_coherent(ro, s < count ? (s * MC + col) * 16 : (int)bytes_o);
     }
   }
   // (m, l) of slot s of query g in lane s of half-wave g (loop only when
@@ -195,35 +226,54 @@ __device__ __forceinline__ void decode_merge(const DecodeArgs& a, const DecodeUn
     }
   }
   __syncthreads();
+  f32x4 O[CPT];
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
-    const int col = tid / MP + c * (NT / MP);
-    const bool live = col < MC;
-    const int g = live ? col / C4 : 0, d4 = col % C4;
-    float O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int col = column(c);
+    const int g = col / C4;
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < SPL; ++i) {
       const float f = sh_w[g * 32 + ((p + MP * i) & 31)];  // slots past count weigh 0 and loaded 0
-      O[0] = fmaf(ov[c][i].x, f, O[0]);
-      O[1] = fmaf(ov[c][i].y, f, O[1]);
-      O[2] = fmaf(ov[c][i].z, f, O[2]);
-      O[3] = fmaf(ov[c][i].w, f, O[3]);
+      o[0] = fmaf(ov[c][i].x, f, o[0]);
+      o[1] = fmaf(ov[c][i].y, f, o[1]);
+      o[2] = fmaf(ov[c][i].z, f, o[2]);
+      o[3] = fmaf(ov[c][i].w, f, o[3]);
     }
+    if constexpr (!S::WIDE) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) O[k] = group_sum<MP>(O[k]);
-    if (live && p == 0 && g < u.gs) {
-      const float M = sh_ml[2 * g], L = sh_ml[2 * g + 1];
-      if (to_out) {
-        float* op = a.out + ((long long)u.b * a.n_heads + u.h_lo + g) * D + d4 * 4;
+      for (int k = 0; k < 4; ++k) o[k] = stride_sum<16>(o[k]);
+    }
+    O[c] = f32x4{o[0], o[1], o[2], o[3]};
+  }
+  if constexpr (S::WPB > 1) {
+    if (lane < 16) sh_red[(w / S::NBLK) * MC + blk0 * 16 + lane] = O[0];
+    __syncthreads();
+    if (w >= S::NBLK) return;
+    f32x4 r = sh_red[blk0 * 16 + lane];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) op[k] = O[k] / L;
-      } else {
-        const auto rw = buffer_rsrc(a.wg_o + dst * G * D, G * D * 4);
-        buffer_store_f4_coherent(rw, (g * D + d4 * 4) * 4, f32x4{O[0], O[1], O[2], O[3]});
-        if (d4 == 0) {
-          store_coherent(&a.wg_ml[(dst * G + g) * 2 + 0], M);
-          store_coherent(&a.wg_ml[(dst * G + g) * 2 + 1], L);
-        }
+    for (int q = 1; q < S::WPB; ++q) r += sh_red[q * MC + blk0 * 16 + lane];
+    O[0] = r;
+  }
+  if (!S::WIDE && lane >= 16) return;
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int col = column(c);
+    const int g = col / C4, d4 = col % C4;
+    if (g >= u.gs) continue;
+    const float M = sh_ml[2 * g], L = sh_ml[2 * g + 1];
+    if (to_out) {
+      float* op = a.out + ((long long)u.b * a.n_heads + u.h_lo + g) * D + d4 * 4;
+      op[0] = O[c].x / L;
+      op[1] = O[c].y / L;
+      op[2] = O[c].z / L;
+      op[3] = O[c].w / L;
+    } else {
+      const auto rw = buffer_rsrc(dst_o, G * D * 4);
+      buffer_store_f4_coherent(rw, col * 16, O[c]);
+      if (d4 == 0) {
+        store_coherent(&dst_ml[g * 2 + 0], M);
+        store_coherent(&dst_ml[g * 2 + 1], L);
       }
     }
   }
@@ -237,6 +287,11 @@ __device__ __forceinline__ void decode_merge(const DecodeArgs& a, const DecodeUn
 //   that splits form groups of decode_merge_group; the last workgroup of a
 //   group merges the group's partials into a group partial, and the last
 //   group merger merges the group partials.
+//   Partials of a unit ub: o at ws_o[ub][split][G][D], (m, l) at
+//   ws_ml[ub][split][G][2]; group partials likewise with n_groups slots.
+//   A workgroup's (m, l) values stay in one piece: with one query's slots
+//   adjacent instead ([G][split][2]), eight workgroups wrote 8-byte pieces
+//   of each 64-byte line and C5 took 1.3 us longer.
 template <int G, int D, int NW>
 __device__ __forceinline__ void decode_finish(const DecodeArgs& a, const DecodeUnit& u, const float (*sm)[G],
                                               const float (*sl)[G], const float (*so)[G][D]) {
@@ -245,12 +300,17 @@ __device__ __forceinline__ void decode_finish(const DecodeArgs& a, const DecodeU
   constexpr int MC = G * C4;
   constexpr int FLAT = decode_merge_flat(G * D);
   constexpr int GS = decode_merge_group;
+  constexpr int WPB = MergeShape<G, D, NT>::WPB;
   __shared__ float sh_w[32 * G];
   __shared__ float sh_ml[2 * G];
+  __shared__ f32x4 sh_red[WPB > 1 ? WPB * MC : 1];
   __shared__ int s_last;
   const bool single = (u.n_act == 1);
   const long long units = gridDim.y;  // (query, KV head or head group) units per query
-  const long long part = ((long long)u.b * units + u.kvh) * a.n_splits + u.split;
+  const long long ub = (long long)u.b * units + u.kvh;
+  const long long part = ub * a.n_splits + u.split;
+  const int n_groups = (a.n_splits + GS - 1) / GS;  // group slots per (query, KV head)
+  float* ml_unit = a.ws_ml + ub * a.n_splits * G * 2;
   const auto rw = buffer_rsrc(a.ws_o + part * G * D, G * D * 4);
   for (int c = threadIdx.x; c < MC; c += NT) {
     const int g = c / C4, d4 = c % C4;
@@ -283,19 +343,18 @@ __device__ __forceinline__ void decode_finish(const DecodeArgs& a, const DecodeU
       // a full L2 writeback + invalidate per workgroup on this chip).
       buffer_store_f4_coherent(rw, (g * D + d4 * 4) * 4, O);
       if (d4 == 0) {
-        store_coherent(&a.ws_ml[(part * G + g) * 2 + 0], M);
-        store_coherent(&a.ws_ml[(part * G + g) * 2 + 1], L);
+        store_coherent(&ml_unit[((long long)u.split * G + g) * 2 + 0], M);
+        store_coherent(&ml_unit[((long long)u.split * G + g) * 2 + 1], L);
       }
     }
   }
   if (single) return;
 
   const bool two_level = u.n_act > FLAT;
-  const int n_groups = (a.n_splits + GS - 1) / GS;  // group slots per (query, KV head)
   const int n_grp = two_level ? (u.n_act + GS - 1) / GS : 1;
   const int grp = two_level ? u.split / GS : 0;
   const int members = two_level ? ((u.n_act - grp * GS) < GS ? u.n_act - grp * GS : GS) : u.n_act;
-  unsigned* ctr0 = a.counters + ((long long)u.b * units + u.kvh) * (n_groups + 1) * decode_counter_stride;
+  unsigned* ctr0 = a.counters + ub * (n_groups + 1) * decode_counter_stride;
 
   // Arrival: every thread's coherent stores complete before the workgroup
   // counts itself in.
@@ -313,16 +372,22 @@ __device__ __forceinline__ void decode_finish(const DecodeArgs& a, const DecodeU
   };
 
   if (!arrive(ctr0 + (long long)grp * decode_counter_stride, members)) return;
-  const long long part0 = ((long long)u.b * units + u.kvh) * a.n_splits;
+  const float* o_unit = a.ws_o + ub * a.n_splits * G * D;
   if (!two_level) {
-    decode_merge<G, D, NT, FLAT>(a, u, a.ws_o, a.ws_ml, part0, u.n_act, true, 0, sh_w, sh_ml);
+    // Up to 16 splits the merge issues loads for 16 slots only (slots past
+    // the count still pass through the load pipeline).
+    if (FLAT > GS && u.n_act <= GS)
+      decode_merge<G, D, NT, GS>(a, u, o_unit, ml_unit, 0, u.n_act, true, nullptr, nullptr, sh_w, sh_ml, sh_red);
+    else
+      decode_merge<G, D, NT, FLAT>(a, u, o_unit, ml_unit, 0, u.n_act, true, nullptr, nullptr, sh_w, sh_ml, sh_red);
     return;
   }
-  const long long gpart0 = ((long long)u.b * units + u.kvh) * n_groups;
-  decode_merge<G, D, NT, GS>(a, u, a.ws_o, a.ws_ml, part0 + (long long)grp * GS, members, false, gpart0 + grp,
-                             sh_w, sh_ml);
+  float* go_unit = a.wg_o + ub * n_groups * G * D;
+  float* gml_unit = a.wg_ml + ub * n_groups * G * 2;
+  decode_merge<G, D, NT, GS>(a, u, o_unit, ml_unit, (long long)grp * GS, members, false,
+                             go_unit + (long long)grp * G * D, gml_unit + (long long)grp * G * 2, sh_w, sh_ml, sh_red);
   if (!arrive(ctr0 + (long long)n_groups * decode_counter_stride, n_grp)) return;
-  decode_merge<G, D, NT, GS>(a, u, a.wg_o, a.wg_ml, gpart0, n_grp, true, 0, sh_w, sh_ml);
+  decode_merge<G, D, NT, GS>(a, u, go_unit, gml_unit, 0, n_grp, true, nullptr, nullptr, sh_w, sh_ml, sh_red);
 }
 
 // ----------------------------------------------------------------- scalar form
