@@ -249,6 +249,23 @@ def test_c5_gemma_prefill_full_size(ctx, orc):
     prefill_case(ctx, orc, 8, 1, 256, "bf16", 4096, seed=500, rows=_dense_rows(4096, 4), pooled=True)
 
 
+# Balanced pairs of query blocks (the d256 kernel): blocks b and c = nblk-1-b
+# pair up, block c's keys are cut at the pair's midpoint over two
+# workgroups and merged by whichever arrives second, and the first
+# workgroup of the pair also takes block b whole.  Each shape runs paired
+# (the default) and unpaired against the oracle: prompt offsets, a partial
+# last block, one pair, and the two-piece precision path (large scores).
+@pytest.mark.parametrize("balance", ["1", "0"])
+@pytest.mark.parametrize("n_heads,B,pos0,q_scale", [
+    (2, 512, 0, 1.0), (3, 1024, 0, 1.0), (2, 768, 300, 1.0), (1, 256, 37, 1.0), (2, 1000, 0, 1.0),
+    (2, 512, 0, 8.0),
+])
+def test_prefill_d256_balanced_pairs(ctx, orc, monkeypatch, balance, n_heads, B, pos0, q_scale):
+    monkeypatch.setenv("VTB_PREFILL_BALANCE", balance)
+    err = prefill_case(ctx, orc, n_heads, 1, 256, "bf16", B, pos0=pos0, seed=900 + B, q_scale=q_scale)
+    print(f"d256 balance={balance} h{n_heads} B{B} pos0 {pos0} q x{q_scale}: rel err {err:.2e}")
+
+
 # Ranges beyond f16's: the pre-pass scales each bf16 head by a power of two
 # (keys / values) and each wave's queries likewise, so magnitudes above 65504
 # or below f16's normal range keep 11 significant bits.  Scores stay O(1)

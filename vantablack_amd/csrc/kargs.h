@@ -70,9 +70,14 @@ struct PrefillArgs {
   int n_kv;
   int vt_ld;                 // keys per V^T row (multiple of 64, >= pos0 + n_q)
   float scale_log2;          // (1/sqrt(D)) * log2(e)
-  int pad1;
+  int balance;               // 1: paired key ranges (prefill_entry); nblk even
+  float* part_o;             // balance: split-block partials [n_heads][nblk / 2][2][threads][D / 2] f32
+  float* part_ml;            // [n_heads][nblk / 2][2][threads][2]: (m, l)
+  unsigned* part_ctr;        // [n_heads][nblk / 2] x 32 arrival counters, zero between launches
 };
-static_assert(sizeof(PrefillArgs) == 120, "PrefillArgs layout");
+static_assert(sizeof(PrefillArgs) == 144 && offsetof(PrefillArgs, balance) == 116 &&
+                  offsetof(PrefillArgs, part_o) == 120 && offsetof(PrefillArgs, part_ctr) == 136,
+              "PrefillArgs layout");
 static_assert(offsetof(PrefillArgs, kexp) == 32 && offsetof(PrefillArgs, hflag) == 48 &&
                   offsetof(PrefillArgs, knorm) == 56 && offsetof(PrefillArgs, k_row_stride) == 64 &&
                   offsetof(PrefillArgs, pos0) == 80 && offsetof(PrefillArgs, n_q) == 96 &&

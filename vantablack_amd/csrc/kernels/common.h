@@ -229,6 +229,14 @@ __device__ inline void buffer_load8_coherent(__amdgpu_buffer_rsrc_t r, int off, 
   x = buffer_load_coherent(r, off);
   y = buffer_load_coherent(r, off + 4);
 }
+// 16-byte agent-coherent (sc1) buffer load / store (whole-vector bit-casts:
+// a bit_cast of one ext-vector element reads element 0 with this compiler).
+__device__ inline f32x4 buffer_load_f4_coherent(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufSc1));
+}
+__device__ inline void buffer_store_f4_coherent(__amdgpu_buffer_rsrc_t r, int off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kBufSc1);
+}
 
 // Wait for all of this wave's vector-memory loads, including buffer->LDS
 // transfers (their LDS writes have landed when vmcnt reaches zero).

@@ -128,15 +128,6 @@ __device__ __forceinline__ void decode_append(const DecodeArgs& a, const DecodeU
   }
 }
 
-// 16-byte agent-coherent (sc1) buffer load / store (whole-vector bit-casts:
-// a bit_cast of one ext-vector element reads element 0 with this compiler).
-__device__ inline f32x4 buffer_load_f4_coherent(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufSc1));
-}
-__device__ inline void buffer_store_f4_coherent(__amdgpu_buffer_rsrc_t r, int off, f32x4 v) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kBufSc1);
-}
-
 // Split-merge thread layout.  When the result has at least as many float4
 // columns as the workgroup has threads (WIDE), thread t takes columns
 // t, t + NT, ... of every slot: each load instruction reads 1 KB of one

@@ -330,10 +330,88 @@ struct PrefillLds {
   __attribute__((aligned(16))) char v1[D * (BN / 8 + 1) * 16];
 };
 
+// Kernels built with balanced pairs of query blocks (prefill_entry).  Only
+// d256, whose one-wave-per-SIMD workgroups fill the CUs once (C5: 256
+// workgroups): there the longest causal block set the launch time.  The
+// d <= 128 kernels spilled 21-28 VGPRs with the extra work-item state; the
+// 4-wave d128 kernel measured 34-35 against 31 us at 512 tokens balanced.
+template <int D>
+constexpr bool kBalanced = D >= 256;
+
+// A piece of a split query block (balanced launches): publish this
+// workgroup's unnormalised partial (o, m, l per thread) with coherent
+// stores and count it in; the second piece to arrive loads the first's and
+// merges them, always as piece 0's terms plus piece 1's, so the result does
+// not depend on the arrival order.  Returns true in the workgroup that then
+// writes the block's output.  Layout: part_o[slot][piece][j][thread] float4
+// (j < D/8: the thread's o, consecutive threads adjacent), part_ml[slot]
+// [piece][thread] (m, l); slot = head * nblk/2 + pair.
+template <int D, int NW>
+__device__ __forceinline__ bool prefill_merge_pieces(const PrefillArgs& a, int h, int qb, int piece,
+                                                    f32x16 (&o)[D / 32], float& m_ref, float& l_run) {
+  constexpr int NT = 64 * NW, ND = D / 32, J = D / 8;
+  __shared__ int s_last;
+  const int tid = threadIdx.x;
+  const int nblk = gridDim.y;
+  const long long slot = (long long)h * (nblk / 2) + (nblk - 1 - qb);
+  const long long mine = slot * 2 + piece, other = slot * 2 + (1 - piece);
+  {
+    const auto rw = buffer_rsrc(a.part_o + mine * J * NT * 4, J * NT * 16);
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        buffer_store_f4_coherent(rw, ((4 * dt + q4) * NT + tid) * 16,
+                                 f32x4{o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]});
+    store_coherent(&a.part_ml[(mine * NT + tid) * 2 + 0], m_ref);
+    store_coherent(&a.part_ml[(mine * NT + tid) * 2 + 1], l_run);
+  }
+  wait_stores();
+  __syncthreads();
+  if (tid == 0) {
+    unsigned* ctr = a.part_ctr + slot * 32;
+    const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev == 1u;
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return false;
+  const auto rr = buffer_rsrc(a.part_o + other * J * NT * 4, J * NT * 16);
+  const float mo = load_coherent(&a.part_ml[(other * NT + tid) * 2 + 0]);
+  const float lo = load_coherent(&a.part_ml[(other * NT + tid) * 2 + 1]);
+  const float M = fmaxf(m_ref, mo);
+  const float fm = m_ref == -INFINITY ? 0.0f : exp2_fast(m_ref - M);
+  const float fo = mo == -INFINITY ? 0.0f : exp2_fast(mo - M);
+  const float f0 = piece == 0 ? fm : fo, f1 = piece == 0 ? fo : fm;
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) {
+    f32x4 ov[4];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) ov[q4] = buffer_load_f4_coherent(rr, ((4 * dt + q4) * NT + tid) * 16);
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float mv = o[dt][4 * q4 + e], xv = ov[q4][e];
+        const float v0 = piece == 0 ? mv : xv, v1 = piece == 0 ? xv : mv;
+        o[dt][4 * q4 + e] = v0 * f0 + v1 * f1;
+      }
+  }
+  const float l0v = piece == 0 ? l_run : lo, l1v = piece == 0 ? lo : l_run;
+  l_run = l0v * f0 + l1v * f1;
+  m_ref = M;
+  return true;
+}
+
+// One work item: queries of block qb against keys [k_lo, k_hi) (intersected
+// with each query's causal and window range); piece < 0: the whole block
+// (write the output), else a piece of a split block (prefill_merge_pieces).
 template <int D, int NW, bool X2>
 __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, const int qb, const int kvh,
                                              const f16x8 (&qf)[D / 16], const f16x8 (&ql)[D / 16],
-                                             const int eq, PrefillLds<D>& lds) {
+                                             const int eq, PrefillLds<D>& lds, const long long k_lo,
+                                             const long long k_hi, const int piece) {
   constexpr int NT = 64 * NW;                 // threads per workgroup
   constexpr int BM = 32 * NW;                 // queries per workgroup (NW waves x 32)
   constexpr int BN = prefill_block_n(D);      // keys per tile
@@ -378,9 +456,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   const long long qpos = a.pos0 + mq;
   const long long q_lo = a.pos0 + m0;  // first query position of the workgroup
   const int m_last = (m0 + BM < a.n_q ? m0 + BM : a.n_q) - 1;
-  const long long kend = a.pos0 + m_last + 1;  // keys [.., kend) may be attended
-  long long kbeg = 0;
-  if (a.window > 0 && q_lo >= a.window) kbeg = q_lo - a.window + 1;
+  long long kend = a.pos0 + m_last + 1;  // keys [.., kend) may be attended
+  if (k_hi < kend) kend = k_hi;
+  long long kbeg = k_lo;
+  if (a.window > 0 && q_lo >= a.window && q_lo - a.window + 1 > kbeg) kbeg = q_lo - a.window + 1;
   const long long kt_first = kbeg / BN * BN;
 
   // Wave-level query range, for tile skipping.
@@ -626,6 +705,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
     stage(k_lds0, v_lds0);
   }
 
+  if constexpr (kBalanced<D>) {
+    if (piece >= 0 && !prefill_merge_pieces<D, NW>(a, h, qb, piece, o, m_ref, l_run)) return;
+  }
+
   // out[mq][h][d] = O^T[d][mq] / l.  The lane holds d = 32dt + 8(r/4) +
   // 4hi + (r%4): four consecutive dims per r/4, written as one 16-byte store.
   float l0, l1;
@@ -656,9 +739,12 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
 template <int D, int NW>
 __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
   constexpr int KS = D / 16;
+  constexpr int BM = 32 * NW;
+  constexpr int BN = prefill_block_n(D);
   __shared__ float s_qn[NW];
+  __shared__ PrefillLds<D> lds;
   const int nblk = gridDim.y;
-  int h, qb;
+  int h, w;
   {
     // Workgroups are dispatched round-robin over the 8 XCDs in linear order.
     // When the heads split evenly, XCD x gets heads [x*hpx, (x+1)*hpx) --
@@ -668,75 +754,106 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
     if (a.n_heads % 8 == 0) {
       const int hpx = a.n_heads / 8, j = i / 8;
       h = (i % 8) * hpx + j % hpx;
-      qb = nblk - 1 - j / hpx;
+      w = nblk - 1 - j / hpx;
     } else {
       h = blockIdx.x;
-      qb = nblk - 1 - (int)blockIdx.y;
+      w = nblk - 1 - (int)blockIdx.y;
+    }
+  }
+  // Work items.  Plain launches: block w, all its keys.  Balanced launches
+  // (a.balance, nblk even): causal blocks b = p and c = nblk - 1 - p pair up
+  // (their key counts sum to the same for every p) and the pair's keys are
+  // cut in two equal halves at S: workgroup 2p takes block c's keys [0, S),
+  // workgroup 2p + 1 the rest of block c and then all of block b.  Every
+  // workgroup then has the same work, where the plain grid's longest block
+  // has twice the average (a one-workgroup-per-CU grid waits for it).
+  auto kend_of = [&](int q) -> long long {
+    const int ml = ((q + 1) * BM < a.n_q ? (q + 1) * BM : a.n_q);
+    return a.pos0 + ml;
+  };
+  int n_items = 1, qb0 = w, qb1 = 0, pc0 = -1;
+  long long lo0 = 0, hi0 = 1LL << 62;
+  if (kBalanced<D> && a.balance) {
+    const int p = w >> 1, c = nblk - 1 - p, b = p;
+    const long long kc = kend_of(c), kb = kend_of(b);
+    const long long S = (kb + kc) / 2 / BN * BN;
+    if (S >= kc) {  // no split
+      qb0 = (w & 1) ? b : c;
+    } else if ((w & 1) == 0) {
+      qb0 = c, pc0 = 0, hi0 = S;
+    } else {
+      qb0 = c, pc0 = 1, lo0 = S;
+      qb1 = b, n_items = 2;
     }
   }
   const int kvh = (int)(((long long)h * a.n_kv) / a.n_heads);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hi = lane >> 5, lc = lane & 31;
-  const int mq = qb * 32 * NW + wave * 32 + lc;
-  const int mr = mq < a.n_q ? mq : a.n_q - 1;  // padding lanes reuse the last query
-  const float* qp = a.q + ((long long)mr * a.n_heads + h) * D + 8 * hi;
-  // Q^T fragments (B operand): lane holds Q[mq][16ks + 8hi .. +8], read as
-  // f32 and rounded to f16 after scaling by 2^-eq, eq from the largest |q|
-  // of the wave's 32 (query, head) rows (wave-uniform); the score
-  // multiplier takes 2^eq back.  A power-of-two scale is exact for every
-  // value it keeps in f16's normal range.  The second piece lo = f16(x - hi)
-  // makes 22 significant bits for the two-piece form.
-  f16x8 qf[KS], ql[KS];
-  int eq;
-  float n2 = 0.0f;  // |q|^2 of the lane's half row
-  {
-    f32x4 qv[KS][2];
+  for (int it = 0; it < n_items; ++it) {
+    const int qb = it == 0 ? qb0 : qb1;
+    const int piece = it == 0 ? pc0 : -1;
+    const long long k_lo = it == 0 ? lo0 : 0, k_hi = it == 0 ? hi0 : (1LL << 62);
+    if (it > 0) __syncthreads();  // the previous item's LDS reads are done
+    const int mq = qb * 32 * NW + wave * 32 + lc;
+    const int mr = mq < a.n_q ? mq : a.n_q - 1;  // padding lanes reuse the last query
+    const float* qp = a.q + ((long long)mr * a.n_heads + h) * D + 8 * hi;
+    // Q^T fragments (B operand): lane holds Q[mq][16ks + 8hi .. +8], read as
+    // f32 and rounded to f16 after scaling by 2^-eq, eq from the largest |q|
+    // of the wave's 32 (query, head) rows (wave-uniform); the score
+    // multiplier takes 2^eq back.  A power-of-two scale is exact for every
+    // value it keeps in f16's normal range.  The second piece lo = f16(x - hi)
+    // makes 22 significant bits for the two-piece form.
+    f16x8 qf[KS], ql[KS];
+    int eq;
+    float n2 = 0.0f;  // |q|^2 of the lane's half row
+    {
+      f32x4 qv[KS][2];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qv[ks][0] = *reinterpret_cast<const f32x4*>(qp + 16 * ks);
-      qv[ks][1] = *reinterpret_cast<const f32x4*>(qp + 16 * ks + 4);
+      for (int ks = 0; ks < KS; ++ks) {
+        qv[ks][0] = *reinterpret_cast<const f32x4*>(qp + 16 * ks);
+        qv[ks][1] = *reinterpret_cast<const f32x4*>(qp + 16 * ks + 4);
+      }
+      float mx = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            mx = fmaxf(mx, fabsf(qv[ks][j][e]));
+            n2 = fmaf(qv[ks][j][e], qv[ks][j][e], n2);
+          }
+      eq = __builtin_amdgcn_readfirstlane(scale_exp(wave_max(mx)));
+      const float qscale = pow2f(-eq);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float x = qv[ks][j][e] * qscale;
+            qf[ks][4 * j + e] = (_Float16)x;
+            ql[ks][4 * j + e] = (_Float16)(x - (float)qf[ks][4 * j + e]);
+          }
     }
-    float mx = 0.0f;
+    // |q|^2 of the lane's row (the lane pair hi = 0, 1 holds it), max over
+    // the workgroup.
+    float n2lo, n2hi;
+    lane_halves(n2, n2lo, n2hi);
+    const float wn2 = wave_max(n2lo + n2hi);
+    if (lane == 0) s_qn[wave] = wn2;
+    __syncthreads();
+    float qn2 = s_qn[0];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          mx = fmaxf(mx, fabsf(qv[ks][j][e]));
-          n2 = fmaf(qv[ks][j][e], qv[ks][j][e], n2);
-        }
-    eq = __builtin_amdgcn_readfirstlane(scale_exp(wave_max(mx)));
-    const float qscale = pow2f(-eq);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float x = qv[ks][j][e] * qscale;
-          qf[ks][4 * j + e] = (_Float16)x;
-          ql[ks][4 * j + e] = (_Float16)(x - (float)qf[ks][4 * j + e]);
-        }
+    for (int ww = 1; ww < NW; ++ww) qn2 = fmaxf(qn2, s_qn[ww]);
+    const bool x2 = (a.hflag && a.hflag[kvh] != 0) ||
+                    (a.knorm && sqrtf(qn2) * a.knorm[kvh] * a.scale_log2 > 32.0f);
+    if (x2)
+      prefill_body<D, NW, true>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece);
+    else
+      prefill_body<D, NW, false>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece);
   }
-  // |q|^2 of the lane's row (the lane pair hi = 0, 1 holds it), max over
-  // the workgroup.
-  float n2lo, n2hi;
-  lane_halves(n2, n2lo, n2hi);
-  const float wn2 = wave_max(n2lo + n2hi);
-  if (lane == 0) s_qn[wave] = wn2;
-  __syncthreads();
-  float qn2 = s_qn[0];
-#pragma unroll
-  for (int w = 1; w < NW; ++w) qn2 = fmaxf(qn2, s_qn[w]);
-  const bool x2 = (a.hflag && a.hflag[kvh] != 0) ||
-                  (a.knorm && sqrtf(qn2) * a.knorm[kvh] * a.scale_log2 > 32.0f);
-  __shared__ PrefillLds<D> lds;
-  if (x2)
-    prefill_body<D, NW, true>(a, h, qb, kvh, qf, ql, eq, lds);
-  else
-    prefill_body<D, NW, false>(a, h, qb, kvh, qf, ql, eq, lds);
 }
 
 }  // namespace vtb

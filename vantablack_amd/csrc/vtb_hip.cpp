@@ -216,6 +216,12 @@ int env_int(const char* name, int dflt) {
   int v = atoi(s);
   return v > 0 ? v : dflt;
 }
+// An on/off switch: "0" turns it off, any other value on.
+bool env_flag(const char* name, bool dflt) {
+  const char* s = getenv(name);
+  if (!s || !*s) return dflt;
+  return atoi(s) != 0;
+}
 
 // Split-K decode / f32 prefill launcher.  Queries b in [0, n_q) sit at
 // pos0 + b and attend [window_start, pos0 + b] of the layer rows at k/v.
@@ -416,9 +422,15 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
 // 256-byte aligned.
 constexpr int kPrefillMaxParts = 64;
 struct PrefillScratch {
-  size_t vt = 0, part = 0, hflag = 0, knorm = 0, k16 = 0, kexp = 0, vexp = 0, bytes = 0;
+  size_t vt = 0, part = 0, hflag = 0, knorm = 0, k16 = 0, kexp = 0, vexp = 0, bal_o = 0, bal_ml = 0, bytes = 0;
 };
-PrefillScratch prefill_scratch(size_t n_kv, size_t head_dim, long long vt_ld, int dtype) {
+// Balanced launches (4-wave kernel): split-block partials for n_heads heads
+// of nblk query blocks, threads per workgroup nt.
+size_t prefill_balance_floats(size_t n_heads, size_t nblk, size_t head_dim, size_t nt) {
+  return n_heads * nblk * nt * (head_dim / 2);
+}
+PrefillScratch prefill_scratch(size_t n_kv, size_t head_dim, long long vt_ld, int dtype, size_t bal_floats = 0,
+                               size_t bal_ml_floats = 0) {
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   PrefillScratch p;
   const size_t plane = n_kv * head_dim * (size_t)vt_ld * 2;
@@ -432,6 +444,11 @@ PrefillScratch prefill_scratch(size_t n_kv, size_t head_dim, long long vt_ld, in
     p.kexp = p.k16 + up(plane);
     p.vexp = p.kexp + up(n_kv * (size_t)(vt_ld / 64) * sizeof(int));
     p.bytes = p.vexp + up(n_kv * sizeof(int));
+  }
+  if (bal_floats) {
+    p.bal_o = p.bytes;
+    p.bal_ml = p.bal_o + up(bal_floats * sizeof(float));
+    p.bytes = p.bal_ml + up(bal_ml_floats * sizeof(float));
   }
   return p;
 }
@@ -474,15 +491,29 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
   const size_t bm = wide ? bm_wide : (size_t)vtb::prefill_block_m((int)head_dim);
   const size_t nblk = (n_q + bm - 1) / bm;
   if (nblk > 65535 || n_heads > 0x7fffffff) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "grid too large");
+  // Balanced pairs of query blocks (prefill_entry; the d256 kernel, whose
+  // one-wave-per-SIMD workgroups fill the CUs once at the shapes it takes):
+  // an even block count and causal ranges not cut by a window.  C5 (4096
+  // tokens, 8/1 heads): 140 against 214 us per call.  VTB_PREFILL_BALANCE=0
+  // turns it off.
+  const bool balance = env_flag("VTB_PREFILL_BALANCE", true) && !wide && head_dim >= 256 && nblk >= 2 &&
+                       nblk % 2 == 0 && (window <= 0 || window >= pos0 + (long long)n_q);
+  const size_t nt = wide ? 512 : 256;
   // Pre-pass over keys [0, pos0 + n_q), padded to whole 64-key tiles.
   const long long n_rows = pos0 + (long long)n_q;
   const long long bn = vtb::prefill_block_n((int)head_dim);
   const long long vt_ld = (n_rows + 63) / 64 * 64;  // multiple of the pre-pass tile and of bn
   // The kernels compare positions in 32-bit arithmetic.
   if (vt_ld % bn != 0 || vt_ld >= (1LL << 30)) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prompt too long");
-  const PrefillScratch ps = prefill_scratch(n_kv, head_dim, vt_ld, dtype);
+  const PrefillScratch ps =
+      prefill_scratch(n_kv, head_dim, vt_ld, dtype, balance ? prefill_balance_floats(n_heads, nblk, head_dim, nt) : 0,
+                      balance ? n_heads * nblk * nt * 2 : 0);
   int rc = ensure_scratch(ctx, &ctx->pf, &ctx->pf_bytes, ps.bytes, "hipMalloc(prefill scratch)");
   if (rc) return rc;
+  if (balance) {
+    rc = ensure_workspace(ctx, 0, n_heads * (nblk / 2) * vtb::decode_counter_stride);
+    if (rc) return rc;
+  }
   char* base = (char*)ctx->pf;
   const bool bf = dtype == VTB_HIP_BF16;
   KvtArgs ka;
@@ -544,6 +575,12 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
   a.pos0 = pos0;
   a.window = window;
   a.scale_log2 = inv_sqrt_hd * 1.4426950408889634f;
+  if (balance) {
+    a.balance = 1;
+    a.part_o = (float*)(base + ps.bal_o);
+    a.part_ml = (float*)(base + ps.bal_ml);
+    a.part_ctr = ctx->counters;
+  }
   // x = head (fastest), y = query block: the longest (causal) blocks of every
   // head are dispatched first.
   return launch(ctx, wide ? ctx->f_prefill8[di] : ctx->f_prefill[di], (unsigned)n_heads, (unsigned)nblk, 1,
@@ -1657,9 +1694,21 @@ extern "C" int vtb_hip_reserve(VtbHipCtx* ctx, const VtbHipAttnConfig* cfg, int 
   if (rc) return rc;
   if (kv_dtype != VTB_HIP_F32 && max_batch > 0) {
     const long long vt_ld = ((long long)max_seq + 63) / 64 * 64;
-    rc = ensure_scratch(ctx, &ctx->pf, &ctx->pf_bytes, prefill_scratch(n_kv, D, vt_ld, kv_dtype).bytes,
+    // With balanced pairs enabled, the d256 kernel's partials for up to
+    // max_batch queries.
+    const bool bal = env_flag("VTB_PREFILL_BALANCE", true) && D >= 256;
+    const size_t bm4 = (size_t)vtb::prefill_block_m((int)D);
+    const size_t nblk4 = (max_batch + bm4 - 1) / bm4 + 1;
+    rc = ensure_scratch(ctx, &ctx->pf, &ctx->pf_bytes,
+                        prefill_scratch(n_kv, D, vt_ld, kv_dtype, bal ? prefill_balance_floats(n_heads, nblk4, D, 256) : 0,
+                                        bal ? n_heads * nblk4 * 256 * 2 : 0)
+                            .bytes,
                         "hipMalloc(prefill scratch)");
     if (rc) return rc;
+    if (bal) {
+      rc = ensure_workspace(ctx, 0, n_heads * (nblk4 / 2 + 1) * vtb::decode_counter_stride);
+      if (rc) return rc;
+    }
   }
   if (max_matmul_k > 0 && max_batch > 0) {
     if (max_matmul_k > 32768) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "reserve: matmul k above 32768");
