@@ -237,15 +237,9 @@ def prefill_flops(L, n_heads, d):
 
 
 def prefill_kernel_name(torch, n_heads, n_q, d):
-    """The attention kernel one attn_prefill call runs, by the launcher's rule
-    (launch_prefill_mfma in vantablack_amd/csrc/vtb_hip.cpp): the 8-wave
-    kernel (256 queries per workgroup, d <= 128) when it still yields at
-    least VTB_PREFILL_WIDE_MIN_WGS workgroups (default two per CU), else the
-    4-wave kernel."""
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    wide_min = int(os.environ.get("VTB_PREFILL_WIDE_MIN_WGS", 2 * max(cus, 1)))
-    wide = d <= 128 and n_heads * -(-n_q // 256) >= wide_min
-    return f"vtb_prefill{'8' if wide else ''}_d{d}"
+    """The attention kernel one attn_prefill call runs (launch_prefill_mfma in
+    vantablack_amd/csrc/vtb_hip.cpp): one per head_dim."""
+    return f"vtb_prefill_d{d}"
 
 
 def bench_prefill(ctx, torch, n_heads, n_kv, d, L, reps=5, warmup=2):

@@ -25,7 +25,8 @@ def prefill_case(ctx, orc, n_heads, n_kv, d, dtype, B, pos0=0, window=None, seed
     """Prefill B queries at positions pos0..pos0+B-1 over a cache of
     pos0 + B (+ extra_rows unwritten) rows, via vtb_hip_segment_attn_prefill.
     k_scale / v_scale / q_scale multiply the seeded N(0,1) inputs (a scalar,
-    or an array broadcast over [rows, n_kv, d] / [B, n_heads*d])."""
+    or an array broadcast over [rows, n_kv, d] / [B, n_heads*d]).  Returns
+    the relative error against the oracle."""
     import vantablack_amd as vb
     n_rows = pos0 + B
     k = (orc.normal(seed * 10 + 1, n_rows * n_kv * d).reshape(n_rows, n_kv, d) * k_scale).astype(np.float32)
@@ -283,7 +284,7 @@ def test_prefill_range_beyond_f16(ctx, orc, what, ks, vs, qs):
 
 def test_prefill_v_outlier_rows_beyond_f16(ctx, orc):
     # A few V rows at ~1e6 among N(0,1) rows of the same heads (a per-head
-    # scale keeps both within f16's 2^29 normal range); wide kernel too.
+    # scale keeps both within f16's 2^29 normal range).
     n_rows = 400
     scale = np.ones((n_rows, 2, 1), np.float32)
     scale[[5, 77, 301]] = 7.0e5
@@ -295,43 +296,34 @@ def test_prefill_v_outlier_rows_beyond_f16(ctx, orc):
 # scores (max |q| * max |k_t| * scale_log2) exceeds 32: with one piece, x20
 # channel outliers (the C3 recipe) measured 6.9e-3 against the oracle.  Every
 # kernel shape holds both paths.
-@pytest.mark.parametrize("n_heads,n_kv,d,B,wide", [
-    (8, 2, 128, 333, False),   # 4-wave d128 (two-piece path with the late tile fetch)
-    (8, 2, 128, 333, True),    # 8-wave d128, both paths in one kernel
-    (8, 2, 64, 300, False),    # 4-wave d64
-    (4, 1, 256, 200, False),   # d256 (one wave per SIMD)
+@pytest.mark.parametrize("n_heads,n_kv,d,B", [
+    (8, 2, 128, 333),   # d128 (two-piece path with K fragments read in halves)
+    (8, 2, 64, 300),    # d64
+    (4, 1, 256, 200),   # d256 (one wave per SIMD)
 ])
-def test_prefill_channel_outliers_c3_style(ctx, orc, monkeypatch, n_heads, n_kv, d, B, wide):
-    if wide:
-        monkeypatch.setenv("VTB_PREFILL_WIDE_MIN_WGS", "1")
+def test_prefill_channel_outliers_c3_style(ctx, orc, n_heads, n_kv, d, B):
     ch = np.ones((1, n_kv, d), np.float32)
     n_out = max(1, n_kv * d // 100)
     ch.reshape(-1)[np.random.default_rng(3).choice(n_kv * d, n_out, replace=False)] = 20.0
     err = prefill_case(ctx, orc, n_heads, n_kv, d, "bf16", B, seed=79, k_scale=ch, v_scale=ch)
-    print(f"channel outliers h{n_heads}/{n_kv} d{d} wide={wide}: rel err {err:.2e}")
+    print(f"channel outliers h{n_heads}/{n_kv} d{d}: rel err {err:.2e}")
 
 
-def test_prefill_mixed_heads_outliers_in_one_kv_head(ctx, orc, monkeypatch):
+def test_prefill_mixed_heads_outliers_in_one_kv_head(ctx, orc):
     # One KV head with x20 channels, the other N(0,1): both paths in one
     # launch; f16 cache (no value scaling, the flags still apply).
     ch = np.ones((1, 2, 128), np.float32)
     ch[0, 1, [3, 77]] = 20.0
-    for wide in ("0", "1"):
-        monkeypatch.setenv("VTB_PREFILL_WIDE_MIN_WGS", "1" if wide == "1" else "100000")
-        prefill_case(ctx, orc, 8, 2, 128, "f16", 290, seed=81, k_scale=ch, v_scale=ch)
+    prefill_case(ctx, orc, 8, 2, 128, "f16", 290, seed=81, k_scale=ch, v_scale=ch)
 
 
-def test_prefill_wide_kernel_range_beyond_f16(ctx, orc, monkeypatch):
-    # The 8-wave kernel shares the body; the same per-head / per-wave scales.
-    monkeypatch.setenv("VTB_PREFILL_WIDE_MIN_WGS", "1")
+def test_prefill_range_beyond_f16_several_blocks(ctx, orc):
+    # Five query blocks, the same per-head / per-wave scales.
     prefill_case(ctx, orc, 8, 2, 128, "bf16", 520, seed=80, v_scale=3.0e5, k_scale=2.0e5, q_scale=5.0e-6)
 
 
-@pytest.mark.parametrize("wide", [False, True])
-def test_prefill_large_scores_take_two_pieces(ctx, orc, monkeypatch, wide):
+def test_prefill_large_scores_take_two_pieces(ctx, orc):
     # q and k of rms ~40: scores of ~1e3 (a one-hot softmax), where q's 11-bit
     # rounding alone would move a score by ~0.5; the score bound selects the
     # two-piece form.
-    if wide:
-        monkeypatch.setenv("VTB_PREFILL_WIDE_MIN_WGS", "1")
     prefill_case(ctx, orc, 8, 2, 64, "bf16", 280, seed=82, k_scale=40.0, q_scale=40.0)

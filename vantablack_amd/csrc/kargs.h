@@ -44,7 +44,7 @@ static_assert(offsetof(DecodeArgs, n_heads) == 72 && offsetof(DecodeArgs, pos0) 
                   offsetof(DecodeArgs, rope_pos) == 136 && offsetof(DecodeArgs, rope_half) == 144,
               "DecodeArgs layout");
 
-// Causal prefill attention (vtb_prefill_d*, vtb_prefill8_d*).  Every MFMA
+// Causal prefill attention (vtb_prefill_d*).  Every MFMA
 // operand is f16: the f32 queries are converted in registers with a
 // power-of-two scale per wave (32 queries of one head); keys come from the
 // conversion pass (or straight from an f16 cache) with a power-of-two
@@ -70,12 +70,15 @@ struct PrefillArgs {
   int n_kv;
   int vt_ld;                 // keys per V^T row (multiple of 64, >= pos0 + n_q)
   float scale_log2;          // (1/sqrt(D)) * log2(e)
-  int balance;               // 1: paired key ranges (prefill_entry); nblk even
+  int flags;                 // kPrefillBalance
   float* part_o;             // balance: split-block partials [n_heads][nblk / 2][2][threads][D / 2] f32
   float* part_ml;            // [n_heads][nblk / 2][2][threads][2]: (m, l)
   unsigned* part_ctr;        // [n_heads][nblk / 2] x 32 arrival counters, zero between launches
 };
-static_assert(sizeof(PrefillArgs) == 144 && offsetof(PrefillArgs, balance) == 116 &&
+// PrefillArgs::flags.  kPrefillBalance: paired key ranges (prefill_entry;
+// d256, nblk even).
+constexpr int kPrefillBalance = 1;
+static_assert(sizeof(PrefillArgs) == 144 && offsetof(PrefillArgs, flags) == 116 &&
                   offsetof(PrefillArgs, part_o) == 120 && offsetof(PrefillArgs, part_ctr) == 136,
               "PrefillArgs layout");
 static_assert(offsetof(PrefillArgs, kexp) == 32 && offsetof(PrefillArgs, hflag) == 48 &&

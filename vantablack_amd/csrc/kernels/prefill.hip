@@ -58,9 +58,9 @@
 //
 // Workgroup = 4 waves x 32 queries = 128 queries of one head; key tiles of BN
 // rows stream through LDS (K row-major, V^T row-major, both padded so the
-// 16-byte MFMA operand reads and the tile stores are bank-conflict free),
-// with the next tile prefetched into registers.  Tiles entirely above a
-// wave's diagonal or before its window are skipped.
+// 16-byte MFMA operand reads are bank-conflict free), the next tile written
+// by LDS DMA (buffer_load ... lds) while the current one is computed.  Tiles
+// entirely above a wave's diagonal or before its window are skipped.
 #include "common.h"
 #include "../tiles.h"
 
@@ -320,14 +320,92 @@ __device__ __forceinline__ void kvt_body(const KvtArgs& a) {
 // from stage j%2 while tile j+1 is written into the other and one barrier
 // per tile suffices.  K rows are padded by one 16-byte chunk, V^T rows
 // likewise (bank spread).  Declared once per kernel in the entry and shared
-// by both precision paths, so a workgroup holds one set.
+// by both precision paths, so a workgroup holds one set.  Four separate
+// __shared__ arrays rather than one object: the compiler then knows a DMA
+// into one stage cannot write the stage being read, and does not wait for
+// the DMA before those reads.
+// LDS-typed bytes: stage pointers stay in the local address space, so
+// reads are ds_reads and DMA targets need no address-space conversion.
+typedef __attribute__((address_space(3))) char lchar;
+template <typename T>
+__device__ __forceinline__ T lds_load(const lchar* p) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) T*>(p);
+}
+
 template <int D>
 struct PrefillLds {
   static constexpr int BN = prefill_block_n(D);
-  __attribute__((aligned(16))) char k0[BN * (D / 8 + 1) * 16];
-  __attribute__((aligned(16))) char k1[BN * (D / 8 + 1) * 16];
-  __attribute__((aligned(16))) char v0[D * (BN / 8 + 1) * 16];
-  __attribute__((aligned(16))) char v1[D * (BN / 8 + 1) * 16];
+  static constexpr int KBYTES = BN * (D / 8 + 1) * 16;
+  static constexpr int VBYTES = D * (BN / 8 + 1) * 16;
+  lchar* k0;
+  lchar* k1;
+  lchar* v0;
+  lchar* v1;
+};
+
+// Tile staging by LDS DMA (buffer_load_dwordx4 ... lds): a stage is filled
+// in 1 KB blocks, each one instruction of one wave whose 64 lanes write 16
+// bytes each, in lane order, from the block's LDS offset on.  Slot s = 64 b +
+// lane of a stage is 16-byte chunk s % (C + 1) of row s / (C + 1) of the
+// padded layout (C chunks per row, one pad chunk); the pad slot's lane loads
+// chunk 0 of its row (never read).  Block b belongs to wave b % NW.  K rows
+// at or past kend lie outside the tile's buffer resource and read as zero
+// (those keys are masked for every query here); V^T tiles are whole (the
+// conversion pass zero-pads the last).  No registers hold a tile in flight;
+// completion is counted by vmcnt (wait_loads() before the barrier that
+// publishes a stage).  Offsets are 32-bit: the host keeps a K tile and a
+// V^T head below 2 GiB.
+template <int D, int NW>
+struct TileDma {
+  static constexpr int BN = prefill_block_n(D);
+  static constexpr int KCH = D / 8;
+  static constexpr int VCH = BN / 8;
+  static constexpr int KSL = BN * (KCH + 1);   // 16-byte slots per K stage
+  static constexpr int VSL = D * (VCH + 1);    // per V^T stage
+  static constexpr int KBL = (KSL + 63) / 64;  // 1 KB blocks
+  static constexpr int VBL = (VSL + 63) / 64;
+  static constexpr int KPW = (KBL + NW - 1) / NW;
+  static constexpr int VPW = (VBL + NW - 1) / NW;
+  int wave, lane;
+  int koff[KPW], voff[VPW];  // this lane's source byte offsets inside a tile
+  __device__ __forceinline__ TileDma(int wave_, int lane_, int krow_bytes, int vrow_bytes) : wave(wave_), lane(lane_) {
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      const int sl = 64 * (wave + NW * i) + lane, row = sl / (KCH + 1), ch = sl % (KCH + 1);
+      koff[i] = row * krow_bytes + 16 * (ch == KCH ? 0 : ch);
+    }
+#pragma unroll
+    for (int i = 0; i < VPW; ++i) {
+      const int sl = 64 * (wave + NW * i) + lane, row = sl / (VCH + 1), ch = sl % (VCH + 1);
+      voff[i] = row * vrow_bytes + 16 * (ch == VCH ? 0 : ch);
+    }
+  }
+  // Keys [kt0, kt0 + BN) of a head's K rows (kbase, krow_bytes apart; rows
+  // from kend on excluded) into the K stage kl.
+  __device__ __forceinline__ void issue_k(const char* kbase, long long krow_bytes, long long kend, long long kt0,
+                                          lchar* kl) const {
+    const long long rows = kend - kt0 < BN ? kend - kt0 : BN;
+    const auto r = buffer_rsrc(kbase + kt0 * krow_bytes, (unsigned)(rows * krow_bytes));
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      const int blk = wave + NW * i;
+      if (blk < KBL && (KSL % 64 == 0 || 64 * blk + lane < KSL))
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, reinterpret_cast<__attribute__((address_space(3))) void*>(kl + 1024 * blk), 16,
+                                                 koff[i], 0, 0, 0);
+    }
+  }
+  // Keys [kt0, kt0 + BN) of a head's V^T (vbase; rows of vrow_bytes) into the
+  // V^T stage vl.
+  __device__ __forceinline__ void issue_v(const char* vbase, int vrow_bytes, long long kt0, lchar* vl) const {
+    const auto r = buffer_rsrc(vbase + kt0 * 2, (unsigned)((D - 1) * vrow_bytes + BN * 2));
+#pragma unroll
+    for (int i = 0; i < VPW; ++i) {
+      const int blk = wave + NW * i;
+      if (blk < VBL && (VSL % 64 == 0 || 64 * blk + lane < VSL))
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, reinterpret_cast<__attribute__((address_space(3))) void*>(vl + 1024 * blk), 16,
+                                                 voff[i], 0, 0, 0);
+    }
+  }
 };
 
 // Kernels built with balanced pairs of query blocks (prefill_entry).  Only
@@ -404,6 +482,32 @@ __device__ __forceinline__ bool prefill_merge_pieces(const PrefillArgs& a, int h
   return true;
 }
 
+// out[mq][h][d] = O^T[d][mq] / l.  The lane holds d = 32dt + 8(r/4) + 4hi +
+// (r%4): four consecutive dims per r/4, written as one 16-byte store.  The
+// row sum is split over the lane pair (hi = 0, 1); ev is the head's value
+// exponent.
+template <int D>
+__device__ __forceinline__ void prefill_write_out(const PrefillArgs& a, int h, int mq, int hi,
+                                                  const f32x16 (&o)[D / 32], float l_run, int ev) {
+  float l0, l1;
+  lane_halves(l_run, l0, l1);
+  const float l_tot = l0 + l1;
+  if (mq < a.n_q) {
+    const float inv = (1.0f / l_tot) * pow2f(ev);
+    float* op = a.out + ((long long)mq * a.n_heads + h) * D + 4 * hi;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f32x4 w;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = o[dt][4 * g + j] * inv;
+        *reinterpret_cast<f32x4*>(op + 32 * dt + 8 * g) = w;
+      }
+    }
+  }
+}
+
 // One work item: queries of block qb against keys [k_lo, k_hi) (intersected
 // with each query's causal and window range); piece < 0: the whole block
 // (write the output), else a piece of a split block (prefill_merge_pieces).
@@ -419,8 +523,6 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   constexpr int VCH = BN / 8;                 // 16-byte chunks per V^T row
   constexpr int KPB = (KCH + 1) * 16;         // LDS pitch of a K row: one pad chunk
   constexpr int VPB = (VCH + 1) * 16;         // LDS pitch of a V^T row
-  constexpr int CPT = BN * KCH / NT;          // 16-byte chunks per thread per tile (K; V^T alike)
-  static_assert(BN * KCH % NT == 0 && D * (BN / 8) == BN * KCH, "tile does not match the workgroup");
   constexpr int NS = BN / 32;                 // 32-key S^T tiles per key tile
   constexpr int ND = D / 32;                  // 32-dim O^T tiles
   constexpr int KS = D / 16;                  // k-steps of the QK product
@@ -439,11 +541,11 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   // The register-tight case: the two-piece form of the 4-wave d128 kernel.
   constexpr bool LATE = X2 && NW == 4 && D == 128;
 
-  static_assert(sizeof(lds.k0) == BN * KPB && sizeof(lds.v0) == D * VPB, "LDS stage size");
-  char* const k_lds0 = lds.k0;
-  char* const k_lds1 = lds.k1;
-  char* const v_lds0 = lds.v0;
-  char* const v_lds1 = lds.v1;
+  static_assert(PrefillLds<D>::KBYTES == BN * KPB && PrefillLds<D>::VBYTES == D * VPB, "LDS stage size");
+  lchar* const k_lds0 = lds.k0;
+  lchar* const k_lds1 = lds.k1;
+  lchar* const v_lds0 = lds.v0;
+  lchar* const v_lds1 = lds.v1;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -467,39 +569,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   const long long wq_hi = a.pos0 + (m0 + wave * 32 + 31 < a.n_q ? m0 + wave * 32 + 31 : a.n_q - 1);
   const bool wave_live = m0 + wave * 32 < a.n_q;
 
-  const _Float16* kg = (const _Float16*)a.k + (long long)kvh * a.k_head_stride;
-  const _Float16* vtg = (const _Float16*)a.vt + (long long)kvh * D * a.vt_ld;
-
-  // Tile staging through registers: thread chunk i of a tile is K row
-  // (tid + NT i) / KCH, chunk (tid + NT i) % KCH, and V^T row (tid + NT i) /
-  // VCH, chunk (tid + NT i) % VCH.  K rows at or past kend are clamped to
-  // kend - 1 (those keys are masked for every query here).
-  u32x4 kpre[CPT], vpre[CPT];
-  auto fetch = [&](long long kt0) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + NT * i;
-      long long row = kt0 + c / KCH;
-      row = row < kend ? row : kend - 1;
-      kpre[i] = load16_cached(kg + row * a.k_row_stride + 8 * (c % KCH));
-    }
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + NT * i;
-      vpre[i] = load16_cached(vtg + (long long)(c / VCH) * a.vt_ld + kt0 + 8 * (c % VCH));
-    }
-  };
-  auto stage = [&](char* kl, char* vl) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + NT * i;
-      *reinterpret_cast<u32x4*>(kl + (c / KCH) * KPB + 16 * (c % KCH)) = kpre[i];
-    }
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + NT * i;
-      *reinterpret_cast<u32x4*>(vl + (c / VCH) * VPB + 16 * (c % VCH)) = vpre[i];
-    }
+  const char* kbase = (const char*)((const _Float16*)a.k + (long long)kvh * a.k_head_stride);
+  const char* vbase = (const char*)((const _Float16*)a.vt + (long long)kvh * D * a.vt_ld);
+  const long long krow_bytes = a.k_row_stride * 2;
+  const int vrow_bytes = a.vt_ld * 2;
+  const TileDma<D, NW> dma(wave, lane, (int)krow_bytes, vrow_bytes);
+  auto fetch = [&](long long kt0, lchar* kl, lchar* vl) {
+    dma.issue_k(kbase, krow_bytes, kend, kt0, kl);
+    dma.issue_v(vbase, vrow_bytes, kt0, vl);
   };
 
   // Q^T fragments (B operand) from the entry: qf (and the second pieces ql,
@@ -520,12 +597,12 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   // absent window keeps every causal key).
   const int wcap = (a.window > 0 && a.window < (1 << 30)) ? (int)a.window : (1 << 30);
 
-  auto compute = [&](const char* kl, const char* vl, long long kt0) {
+  auto compute = [&](const lchar* kl, const lchar* vl, long long kt0, int ek) {
     // Skip tiles entirely above this wave's diagonal or before its windows.
     bool live = wave_live && kt0 <= wq_hi;
     if (a.window > 0 && kt0 + BN - 1 < wq_lo - a.window + 1) live = false;
     if (!live) return;
-    int es = eq + (kexp_h ? kexp_h[kt0 >> 6] : 0);
+    int es = eq + ek;
     es = es < -120 ? -120 : (es > 120 ? 120 : es);
     const float sl = a.scale_log2 * pow2f(es);
 
@@ -535,7 +612,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
     // KH parts of the k-steps in the register-tight two-piece form).
     constexpr int KH = LATE ? 2 : 1;
     constexpr int KSH = KS / KH;
-    const char* kr = kl + lc * KPB + 16 * hi;
+    const lchar* kr = kl + lc * KPB + 16 * hi;
     f32x16 s[NS];
 #pragma unroll
     for (int nt = 0; nt < NS; ++nt) s[nt] = f32x16{};
@@ -548,7 +625,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
         for (int ks = 0; ks < KSH; ++ks)
 #pragma unroll
           for (int nb = 0; nb < KB; ++nb)
-            kf[ks][nb] = *reinterpret_cast<const u32x4*>(kr + 32 * (n0 + nb) * KPB + 32 * (k0 + ks));
+            kf[ks][nb] = lds_load<u32x4>(kr + 32 * (n0 + nb) * KPB + 32 * (k0 + ks));
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -570,12 +647,12 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
 
     // First V^T batch (dims 0 .. 32VB) for the PV product, in flight during
     // the softmax.
-    const char* vr = vl + lc * VPB + 16 * hi;
+    const lchar* vr = vl + lc * VPB + 16 * hi;
     u32x4 vf[PS][VB];
 #pragma unroll
     for (int ks = 0; ks < PS; ++ks)
 #pragma unroll
-      for (int db = 0; db < VB; ++db) vf[ks][db] = *reinterpret_cast<const u32x4*>(vr + 32 * db * VPB + 32 * ks);
+      for (int db = 0; db < VB; ++db) vf[ks][db] = lds_load<u32x4>(vr + 32 * db * VPB + 32 * ks);
 
     // Mask (diagonal / window tiles only: a wave-uniform branch).  Key
     // 32nt + 8(r/4) + 4hi + r%4 of the tile is kept iff it lies in
@@ -657,7 +734,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
         for (int ks = 0; ks < PS; ++ks)
 #pragma unroll
           for (int db = 0; db < VB; ++db)
-            vf[ks][db] = *reinterpret_cast<const u32x4*>(vr + 32 * (d0 + db) * VPB + 32 * ks);
+            vf[ks][db] = lds_load<u32x4>(vr + 32 * (d0 + db) * VPB + 32 * ks);
       }
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(1);
@@ -680,54 +757,48 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
 
   // Key loop, two tiles per trip so each stage is a fixed LDS object.  Per
   // tile: barrier (the stage to read is complete; every wave is done with the
-  // other stage), fetch the next tile into registers, compute, then store the
-  // fetched tile into the other stage.  The two-piece form of the 4-wave
-  // d128 kernel fetches after the compute instead (its registers do not
-  // hold the next tile during it), the same barriers in the same order.
+  // other stage), DMA of the next tile into the other stage, compute, wait
+  // for this wave's DMA.  The next tile's key exponent is read with its DMA,
+  // as a vector load that the same wait covers: a scalar load would be
+  // waited for together with the tile's LDS fragment reads (one counter).
+  // (Moved to a scalar register right after that wait, so no later
+  // instruction waits on it.)
+  auto kexp_of = [&](long long kt0) -> int { return kexp_h ? kexp_h[kt0 >> 6] : 0; };
+  int ek0 = 0, ek1 = 0;
   if (kt_first < kend) {
-    fetch(kt_first);
-    stage(k_lds0, v_lds0);
+    fetch(kt_first, k_lds0, v_lds0);
+    ek0 = kexp_of(kt_first);
+    wait_loads();
+    ek0 = __builtin_amdgcn_readfirstlane(ek0);
   }
   for (long long kt0 = kt_first; kt0 < kend; kt0 += 2 * BN) {
     __syncthreads();
     const bool more1 = kt0 + BN < kend;
-    if (!LATE && more1) fetch(kt0 + BN);
-    compute(k_lds0, v_lds0, kt0);
+    if (more1) {
+      fetch(kt0 + BN, k_lds1, v_lds1);
+      ek1 = kexp_of(kt0 + BN);
+    }
+    compute(k_lds0, v_lds0, kt0, ek0);
     if (!more1) break;
-    if (LATE) fetch(kt0 + BN);
-    stage(k_lds1, v_lds1);
+    wait_loads();
+    ek1 = __builtin_amdgcn_readfirstlane(ek1);
     __syncthreads();
     const bool more2 = kt0 + 2 * BN < kend;
-    if (!LATE && more2) fetch(kt0 + 2 * BN);
-    compute(k_lds1, v_lds1, kt0 + BN);
+    if (more2) {
+      fetch(kt0 + 2 * BN, k_lds0, v_lds0);
+      ek0 = kexp_of(kt0 + 2 * BN);
+    }
+    compute(k_lds1, v_lds1, kt0 + BN, ek1);
     if (!more2) break;
-    if (LATE) fetch(kt0 + 2 * BN);
-    stage(k_lds0, v_lds0);
+    wait_loads();
+    ek0 = __builtin_amdgcn_readfirstlane(ek0);
   }
 
   if constexpr (kBalanced<D>) {
     if (piece >= 0 && !prefill_merge_pieces<D, NW>(a, h, qb, piece, o, m_ref, l_run)) return;
   }
 
-  // out[mq][h][d] = O^T[d][mq] / l.  The lane holds d = 32dt + 8(r/4) +
-  // 4hi + (r%4): four consecutive dims per r/4, written as one 16-byte store.
-  float l0, l1;
-  lane_halves(l_run, l0, l1);
-  const float l_tot = l0 + l1;
-  if (mq < a.n_q) {
-    const float inv = (1.0f / l_tot) * pow2f(ev);
-    float* op = a.out + ((long long)mq * a.n_heads + h) * D + 4 * hi;
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        f32x4 w;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w[j] = o[dt][4 * g + j] * inv;
-        *reinterpret_cast<f32x4*>(op + 32 * dt + 8 * g) = w;
-      }
-    }
-  }
+  prefill_write_out<D>(a, h, mq, hi, o, l_run, ev);
 }
 
 // Entry: the workgroup's (head, query block), its queries in registers
@@ -742,7 +813,11 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
   constexpr int BM = 32 * NW;
   constexpr int BN = prefill_block_n(D);
   __shared__ float s_qn[NW];
-  __shared__ PrefillLds<D> lds;
+  __shared__ __attribute__((aligned(16))) char s_k0[PrefillLds<D>::KBYTES];
+  __shared__ __attribute__((aligned(16))) char s_k1[PrefillLds<D>::KBYTES];
+  __shared__ __attribute__((aligned(16))) char s_v0[PrefillLds<D>::VBYTES];
+  __shared__ __attribute__((aligned(16))) char s_v1[PrefillLds<D>::VBYTES];
+  PrefillLds<D> lds{(lchar*)s_k0, (lchar*)s_k1, (lchar*)s_v0, (lchar*)s_v1};
   const int nblk = gridDim.y;
   int h, w;
   {
@@ -773,7 +848,7 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
   };
   int n_items = 1, qb0 = w, qb1 = 0, pc0 = -1;
   long long lo0 = 0, hi0 = 1LL << 62;
-  if (kBalanced<D> && a.balance) {
+  if (kBalanced<D> && (a.flags & kPrefillBalance)) {
     const int p = w >> 1, c = nblk - 1 - p, b = p;
     const long long kc = kend_of(c), kb = kend_of(b);
     const long long S = (kb + kc) / 2 / BN * BN;
@@ -873,18 +948,6 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
     vtb::kvstat_body<vtb::DTT, D>(a);                                                      \
   }
 
-// Wide variant (d <= 128): 8 waves x 32 queries share one set of staged
-// K / V^T tiles.  The body needs ~214 VGPRs, so a CU holds one such
-// workgroup: the same 8 waves (2 per SIMD) as two 4-wave workgroups, with
-// each staged byte feeding twice the queries.
-#define VTB_PREFILL_WIDE(D)                                                                \
-  extern "C" __global__ __launch_bounds__(512, 2)                                          \
-  void vtb_prefill8_d##D(vtb::PrefillArgs a) {                                             \
-    vtb::prefill_entry<D, 8>(a);                                                           \
-  }
-
-VTB_PREFILL_WIDE(64)
-VTB_PREFILL_WIDE(128)
 VTB_PREFILL(64)
 VTB_PREFILL(128)
 VTB_PREFILL(256)

@@ -103,8 +103,6 @@ constexpr int decode_split_quantum(int head_dim, int kv_bytes, int g, int hg = 1
 // Prefill (MFMA): 4 waves x 32 queries per workgroup; keys per LDS tile by
 // head_dim (the K and V^T tiles stay near 36 KiB of LDS).
 constexpr int prefill_block_m(int) { return 128; }
-// Queries per workgroup of the wide (8-wave, d <= 128) prefill kernels.
-constexpr int prefill_block_m_wide = 256;
 constexpr int prefill_block_n(int head_dim) { return head_dim <= 128 ? 64 : 32; }
 // Minimum resident waves per SIMD the prefill kernel is compiled for: two
 // waves let one wave's softmax and LDS waits hide behind the other's MFMAs

@@ -83,7 +83,6 @@ struct VtbHipCtx {
   hipFunction_t f_decode[kNumKv][kNumD][kNumG] = {};
   hipFunction_t f_decodeh[kNumKv][kNumD][2] = {};  // vtb_decodeh_<kv>_d<D>_g<1|2>: head-group form
   hipFunction_t f_prefill[kNumD] = {};
-  hipFunction_t f_prefill8[kNumD] = {};  // wide (8-wave) variant, d <= 128
   hipFunction_t f_kvt[kNumKv][kNumD] = {};  // conversion pass per cache dtype (f16, bf16)
   hipFunction_t f_kvstat[kNumKv][kNumD] = {};  // statistics pass per cache dtype
   hipFunction_t f_append[kNumKv] = {};
@@ -481,14 +480,7 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
     return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prefill kernel not built for this shape");
   if (!aligned16(k) || !aligned16(v) || !aligned16(q))
     return set_err(ctx, VTB_HIP_EINVAL, "q/K/V not 16-byte aligned");
-  // The wide kernel (8 waves, 256 queries per workgroup) when it still gives
-  // at least VTB_PREFILL_WIDE_MIN_WGS workgroups (default 2 per CU); short
-  // prompts keep the 4-wave kernel's parallelism.
-  const size_t bm_wide = (size_t)vtb::prefill_block_m_wide;
-  const long long wide_min = env_int("VTB_PREFILL_WIDE_MIN_WGS", 2LL * std::max(ctx->cu_count, 1));
-  const bool wide = ctx->f_prefill8[di] != nullptr &&
-                    (long long)(n_heads * ((n_q + bm_wide - 1) / bm_wide)) >= wide_min;
-  const size_t bm = wide ? bm_wide : (size_t)vtb::prefill_block_m((int)head_dim);
+  const size_t bm = (size_t)vtb::prefill_block_m((int)head_dim);
   const size_t nblk = (n_q + bm - 1) / bm;
   if (nblk > 65535 || n_heads > 0x7fffffff) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "grid too large");
   // Balanced pairs of query blocks (prefill_entry; the d256 kernel, whose
@@ -496,15 +488,18 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
   // an even block count and causal ranges not cut by a window.  C5 (4096
   // tokens, 8/1 heads): 140 against 214 us per call.  VTB_PREFILL_BALANCE=0
   // turns it off.
-  const bool balance = env_flag("VTB_PREFILL_BALANCE", true) && !wide && head_dim >= 256 && nblk >= 2 &&
+  const bool balance = env_flag("VTB_PREFILL_BALANCE", true) && head_dim >= 256 && nblk >= 2 &&
                        nblk % 2 == 0 && (window <= 0 || window >= pos0 + (long long)n_q);
-  const size_t nt = wide ? 512 : 256;
+  const size_t nt = 256;
   // Pre-pass over keys [0, pos0 + n_q), padded to whole 64-key tiles.
   const long long n_rows = pos0 + (long long)n_q;
   const long long bn = vtb::prefill_block_n((int)head_dim);
   const long long vt_ld = (n_rows + 63) / 64 * 64;  // multiple of the pre-pass tile and of bn
-  // The kernels compare positions in 32-bit arithmetic.
-  if (vt_ld % bn != 0 || vt_ld >= (1LL << 30)) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prompt too long");
+  // The kernels compare positions in 32-bit arithmetic, and their tile DMA
+  // uses 32-bit offsets within a head's V^T and within a K tile.
+  if (vt_ld % bn != 0 || vt_ld >= (1LL << 30) || (long long)head_dim * vt_ld * 2 >= (1LL << 31) ||
+      (long long)(n_kv * head_dim) * 2 * bn >= (1LL << 31))
+    return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prompt too long");
   const PrefillScratch ps =
       prefill_scratch(n_kv, head_dim, vt_ld, dtype, balance ? prefill_balance_floats(n_heads, nblk, head_dim, nt) : 0,
                       balance ? n_heads * nblk * nt * 2 : 0);
@@ -576,15 +571,14 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
   a.window = window;
   a.scale_log2 = inv_sqrt_hd * 1.4426950408889634f;
   if (balance) {
-    a.balance = 1;
+    a.flags |= vtb::kPrefillBalance;
     a.part_o = (float*)(base + ps.bal_o);
     a.part_ml = (float*)(base + ps.bal_ml);
     a.part_ctr = ctx->counters;
   }
   // x = head (fastest), y = query block: the longest (causal) blocks of every
   // head are dispatched first.
-  return launch(ctx, wide ? ctx->f_prefill8[di] : ctx->f_prefill[di], (unsigned)n_heads, (unsigned)nblk, 1,
-                wide ? 512 : 256, &a);
+  return launch(ctx, ctx->f_prefill[di], (unsigned)n_heads, (unsigned)nblk, 1, (unsigned)nt, &a);
 }
 
 // Quantised GEMV launcher: out[m] = W[m, k] . x.  One workgroup per R rows
@@ -865,9 +859,6 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
         snprintf(name, sizeof name, "vtb_prefill_d%d", D);
         if (hipModuleGetFunction(&ctx->f_prefill[di], ctx->mod_prefill, name) != hipSuccess)
           ctx->f_prefill[di] = nullptr;
-        snprintf(name, sizeof name, "vtb_prefill8_d%d", D);
-        if (D > 128 || hipModuleGetFunction(&ctx->f_prefill8[di], ctx->mod_prefill, name) != hipSuccess)
-          ctx->f_prefill8[di] = nullptr;  // not built for d256: the 4-wave kernel runs
       }
     }
     if (ok) {
