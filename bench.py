@@ -657,7 +657,7 @@ def pmc_workload():
     (vtb_decode_bf16_d256_g8), each over PMC_DECODE's layer count of distinct
     cache layers; and the C4 (8192 tokens) and C5 (4096 tokens) causal
     prefill calls: the statistics and conversion passes (vtb_kvstat_*,
-    vtb_kvt_*) and the attention kernel the launcher picks (vtb_prefill8_d128,
+    vtb_kvt_*) and the attention kernels (vtb_prefill_d128,
     vtb_prefill_d256)."""
     import numpy as np
     import torch
