@@ -596,11 +596,20 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   // The window as a 32-bit bound (positions stay below 2^30; a larger or
   // absent window keeps every causal key).
   const int wcap = (a.window > 0 && a.window < (1 << 30)) ? (int)a.window : (1 << 30);
+  // The per-tile checks in 32-bit scalar arithmetic (positions stay below
+  // 2^30; a window of 2^30 or more excludes no key, like none): wave-uniform
+  // values in SGPRs, so the checks are SALU compares rather than 64-bit
+  // vector ones.
+  const int iwin = __builtin_amdgcn_readfirstlane(wcap < (1 << 30) ? wcap : 0);
+  const int iwq_lo = __builtin_amdgcn_readfirstlane((int)wq_lo);
+  const int iwq_hi = __builtin_amdgcn_readfirstlane((int)wq_hi);
+  const int iqpos = (int)qpos;
 
   auto compute = [&](const lchar* kl, const lchar* vl, long long kt0, int ek) {
     // Skip tiles entirely above this wave's diagonal or before its windows.
-    bool live = wave_live && kt0 <= wq_hi;
-    if (a.window > 0 && kt0 + BN - 1 < wq_lo - a.window + 1) live = false;
+    const int t0 = __builtin_amdgcn_readfirstlane((int)kt0);
+    bool live = wave_live && t0 <= iwq_hi;
+    if (iwin > 0 && t0 + BN - 1 < iwq_lo - iwin + 1) live = false;
     if (!live) return;
     int es = eq + ek;
     es = es < -120 ? -120 : (es > 120 ? 120 : es);
@@ -657,9 +666,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
     // Mask (diagonal / window tiles only: a wave-uniform branch).  Key
     // 32nt + 8(r/4) + 4hi + r%4 of the tile is kept iff it lies in
     // (qpos - window, qpos]; lim is qpos relative to this lane's first key.
-    const bool need_mask = (kt0 + BN - 1 > wq_lo) || (a.window > 0 && kt0 < wq_hi - a.window + 1);
+    const bool need_mask = (t0 + BN - 1 > iwq_lo) || (iwin > 0 && t0 < iwq_hi - iwin + 1);
     if (need_mask) {
-      const int lim = (int)(qpos - kt0) - 4 * hi;
+      const int lim = iqpos - t0 - 4 * hi;
 #pragma unroll
       for (int nt = 0; nt < NS; ++nt) {
 #pragma unroll
@@ -765,15 +774,17 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   // instruction waits on it.)
   auto kexp_of = [&](long long kt0) -> int { return kexp_h ? kexp_h[kt0 >> 6] : 0; };
   int ek0 = 0, ek1 = 0;
-  if (kt_first < kend) {
+  const int ikend = __builtin_amdgcn_readfirstlane((int)kend);
+  const int ikt_first = __builtin_amdgcn_readfirstlane((int)kt_first);
+  if (ikt_first < ikend) {
     fetch(kt_first, k_lds0, v_lds0);
     ek0 = kexp_of(kt_first);
     wait_loads();
     ek0 = __builtin_amdgcn_readfirstlane(ek0);
   }
-  for (long long kt0 = kt_first; kt0 < kend; kt0 += 2 * BN) {
+  for (int kt0 = ikt_first; kt0 < ikend; kt0 += 2 * BN) {
     __syncthreads();
-    const bool more1 = kt0 + BN < kend;
+    const bool more1 = kt0 + BN < ikend;
     if (more1) {
       fetch(kt0 + BN, k_lds1, v_lds1);
       ek1 = kexp_of(kt0 + BN);
@@ -783,7 +794,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
     wait_loads();
     ek1 = __builtin_amdgcn_readfirstlane(ek1);
     __syncthreads();
-    const bool more2 = kt0 + 2 * BN < kend;
+    const bool more2 = kt0 + 2 * BN < ikend;
     if (more2) {
       fetch(kt0 + 2 * BN, k_lds0, v_lds0);
       ek0 = kexp_of(kt0 + 2 * BN);
