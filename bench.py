@@ -40,6 +40,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
@@ -215,6 +217,72 @@ def bench_decode_cfg(ctx, torch, name, n_layers, n_heads, n_kv, d, kv, L, steps=
     return {"us_per_launch": round(t * 1e6, 3), "gbs": round(per / t / 1e9, 1),
             "pct_of_hbm_peak": round(100.0 * per / t / 1e9 / HBM_PEAK_GBS, 2), "bytes_per_launch": per,
             "shape": f"{n_layers} layers, {n_heads}q/{n_kv}kv heads, d{d}, {kv} KV, attended L={L}"}
+
+
+def bench_decode_c2_run(ctx, torch, n_layers=32, L0=4096, steps=256):
+    """BASELINE config 2 as written: Llama-2-7B shapes (32 layers, 32/32
+    heads, d128, f16 KV) with the cache holding 4096 rows, then 256 decode
+    steps, each appending the token's K/V row and attending every row so far
+    in every layer (L = 4097 .. 4352).  One untimed pass of the 256 steps,
+    then a timed pass of the same launches (each step rewrites its row with
+    the same values).  Returns the run's time from HIP events on the context
+    stream and its algorithmic GB/s."""
+    import vantablack_amd as vb
+    n_heads, n_kv, d = 32, 32, 128
+    max_seq = L0 + steps
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(4352)
+    kc = torch.empty((n_layers, max_seq, n_kv, d), dtype=torch.float16, device=dev)
+    vc = torch.empty_like(kc)
+    kc.normal_(generator=g)
+    vc.normal_(generator=g)
+    q = (torch.randn((n_layers, n_heads * d), generator=g, device=dev) / np.sqrt(d)).contiguous()
+    kcur = torch.randn((n_layers, steps, n_kv * d), generator=g, device=dev)
+    vcur = torch.randn((n_layers, steps, n_kv * d), generator=g, device=dev)
+    out = torch.empty((n_layers, n_heads * d), device=dev)
+    torch.cuda.synchronize()
+    kb, vbuf = ctx.wrap_tensor(kc), ctx.wrap_tensor(vc)
+    qbs = [ctx.wrap_tensor(q[l]) for l in range(n_layers)]
+    obs = [ctx.wrap_tensor(out[l]) for l in range(n_layers)]
+    kcs = [[ctx.wrap_tensor(kcur[l, s]) for s in range(steps)] for l in range(n_layers)]
+    vcs = [[ctx.wrap_tensor(vcur[l, s]) for s in range(steps)] for l in range(n_layers)]
+    layer_bytes = max_seq * n_kv * d * 2
+    inv = 1.0 / np.sqrt(d)
+    stream = torch.cuda.ExternalStream(ctx.stream)
+
+    def run(seg):
+        for s in range(steps):
+            for l in range(n_layers):
+                seg.attn_decode_append(obs[l], qbs[l], kb, l * layer_bytes, vbuf, l * layer_bytes, kcs[l][s],
+                                       vcs[l][s], n_heads, n_kv, d, L0 + s + 1, inv, vb.F16)
+
+    with ctx.segment() as seg:
+        run(seg)
+    ctx.wait_idle()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    with ctx.segment() as seg:
+        run(seg)
+    e1.record(stream)
+    ctx.wait_idle()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    t = e0.elapsed_time(e1) * 1e-3
+    alg = sum(n_layers * decode_bytes(L0 + s + 1, n_heads, n_kv, d, 2) for s in range(steps))
+    for b in qbs + obs + [kb, vbuf] + [x for r in kcs + vcs for x in r]:
+        b.release()
+    del kc, vc, kcur, vcur
+    torch.cuda.empty_cache()
+    log(f"decode C2 run: {steps} steps x {n_layers} layers, L {L0 + 1}->{L0 + steps}: {t * 1e3:.2f} ms "
+        f"({t / steps * 1e3:.4f} ms/step, wall {wall * 1e3:.1f} ms) -> {alg / t / 1e9:.1f} GB/s")
+    return {"ms_total": round(t * 1e3, 3), "ms_per_step": round(t / steps * 1e3, 4),
+            "us_per_launch": round(t / (steps * n_layers) * 1e6, 3), "wall_ms": round(wall * 1e3, 2),
+            "gbs": round(alg / t / 1e9, 1), "pct_of_hbm_peak": round(100.0 * alg / t / 1e9 / HBM_PEAK_GBS, 2),
+            "bytes_total": alg,
+            "shape": f"{n_layers} layers, {n_heads}q/{n_kv}kv heads, d{d}, f16 KV, {steps} steps, "
+                     f"L {L0 + 1}->{L0 + steps} (BASELINE config 2 as written)"}
 
 
 def decode_kernel_name(n_heads, n_kv, d, kv):
@@ -588,11 +656,41 @@ def bench_full_prefill(ctx, torch, B=8192, reps=2):
             "tflops_reference": round((proj_flops + attn_flops) / t / 1e12, 1)}
 
 
-def cpu_baseline(seconds_budget=18.0):
-    """Time the CPU oracle on a bounded sample of the decode workload: one
-    C2 layer at L=8192 (f32 values of the f16 cache, as vantablack's f32
-    cache would hold them), repeated until ~seconds_budget is spent."""
-    import numpy as np
+def _timed(fn, budget_s):
+    """Seconds per call of fn, repeated until budget_s is spent (at least once)."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s:
+            return el / n, n
+
+
+def _cpu_workers():
+    # Workers: the CPUs this process may run on, capped at the GPU box's CPU
+    # share (16); pool.zig's own default is (ncpu + 1) / 2 workers
+    # (pool.zig:53), timed as well.
+    affinity = len(os.sched_getaffinity(0))
+    workers = min(affinity, int(os.environ.get("VTB_CPU_WORKERS", "16")))
+    return affinity, (("faithful_1t", 1), ("pool", workers), ("pool_default", (workers + 1) // 2))
+
+
+def _oracle_cache(orc, rng, n_kv, d, rows, kv):
+    """One-layer oracle cache of `rows` rows holding exactly-upcast values of
+    the KV dtype (f32 storage, as vantablack's cache holds them)."""
+    cache = orc.OracleKvCache(1, n_kv, d, rows)
+    for arr in (cache.k, cache.v):
+        x = rng.standard_normal(arr.size, dtype=np.float32)
+        arr[:] = x if kv == "f32" else orc.to_dtype(x, kv)[1]
+    return cache
+
+
+def cpu_baseline(seconds_budget=6.0):
+    """Time the CPU oracle on a bounded sample of the headline decode
+    workload: one C2 layer at L=8192 (f32 values of the f16 cache, as
+    vantablack's f32 cache would hold them), each line repeated for about
+    seconds_budget / 3."""
     from oracle import oracle as orc
     n_heads, n_kv, d, L = 32, 32, 128, 8192
     rng = np.random.default_rng(0)
@@ -607,29 +705,109 @@ def cpu_baseline(seconds_budget=18.0):
     per = decode_bytes(L, n_heads, n_kv, d, 4)
     per16 = decode_bytes(L, n_heads, n_kv, d, 2)
     res = {}
-    # Workers: the CPUs this process may run on, capped at the GPU box's CPU
-    # share (16); pool.zig's own default is (ncpu + 1) / 2 workers
-    # (pool.zig:53), timed as well.
-    affinity = len(os.sched_getaffinity(0))
-    workers = min(affinity, int(os.environ.get("VTB_CPU_WORKERS", "16")))
-    for label, nw in (("faithful_1t", 1), ("pool", workers), ("pool_default", (workers + 1) // 2)):
+    affinity, lines = _cpu_workers()
+    for label, nw in lines:
         pool = orc.Pool(nw)
         try:
-            n, t0 = 0, time.perf_counter()
-            while True:
-                pool.attention(q, cache, c, 0, L - 1)
-                n += 1
-                el = time.perf_counter() - t0
-                if el > seconds_budget / 3:
-                    break
+            t, n = _timed(lambda: pool.attention(q, cache, c, 0, L - 1), seconds_budget / 3)
         finally:
             pool.close()
-        res[label] = {"gbs": n * per / el / 1e9, "gbs_f16_equiv": n * per16 / el / 1e9,
-                      "ms_per_layer": el / n * 1e3, "layers": n, "workers": nw}
+        res[label] = {"gbs": per / t / 1e9, "gbs_f16_equiv": per16 / t / 1e9,
+                      "ms_per_layer": t * 1e3, "layers": n, "workers": nw}
         log(f"cpu {label}: {res[label]['ms_per_layer']:.2f} ms per layer-step ({n} runs)")
     res["affinity_cpus"] = affinity
     res["cpu_model"] = cpu_model()
     return res
+
+
+# The BASELINE configs as the CPU oracle runs them (forward.zig:187-228 per
+# decode layer, prefill.zig:237-287 per prompt row).  Decode: (name, n_heads,
+# n_kv, d, KV dtype, layers per step, [(cur_pos, window)] sampled layer
+# calls, steps, note).  Prefill: (name, n_heads, n_kv, d, KV dtype, prompt
+# tokens, every k-th row sampled).
+CPU_DECODE_CFGS = (
+    ("C1", 32, 4, 64, "f32", 1, [(511, 0)], 1, "one layer at L=512, the whole config"),
+    ("C2_256", 32, 32, 128, "f16", 32, [(4096, 0), (4351, 0)], 256,
+     "one layer at the first (L=4097) and last (L=4352) step; a step is 32 layers, the run 256 steps, "
+     "extrapolated linearly in L from the two"),
+    ("C3", 32, 8, 128, "bf16", 32, [(16383, 4096)], 1,
+     "one layer at pos 16383 with window 4096 (L=4096); a step is 32 layers"),
+    ("C5_decode", 8, 1, 256, "bf16", 26, [(32767, 0)], 1, "one layer at L=32768; a step is 26 layers"),
+)
+CPU_PREFILL_CFGS = (
+    ("C4_L512", 32, 8, 128, "bf16", 512, 1),
+    ("C4_L2048", 32, 8, 128, "bf16", 2048, 8),
+    ("C4_L8192", 32, 8, 128, "bf16", 8192, 64),
+    ("C5_prefill", 8, 1, 256, "bf16", 4096, 32),
+)
+
+
+def cpu_baseline_configs(seconds_per_line=1.5):
+    """The CPU oracle on every BASELINE config, three lines each: faithful
+    (one thread, as vantablack runs attention), and split over heads on a
+    pool.zig-style pool at the box's CPU share and at pool.zig's default
+    worker count.  Each line times a bounded sample of the config (named in
+    its `sample`) for about seconds_per_line and extrapolates to the whole
+    config's work: decode steps from per-layer calls, a prefill from every
+    k-th prompt row (row b attends b + 1 keys, so the sample's share of the
+    L(L+1)/2 causal pairs scales it up exactly)."""
+    from oracle import oracle as orc
+    rng = np.random.default_rng(11)
+    _, lines = _cpu_workers()
+    out = {}
+    for name, nh, nkv, d, kv, layers, calls, steps, note in CPU_DECODE_CFGS:
+        rows = max(p for p, _ in calls) + 1
+        cache = _oracle_cache(orc, rng, nkv, d, rows, kv)
+        q = rng.standard_normal(nh * d, dtype=np.float32) / np.float32(np.sqrt(d))
+        scores = np.zeros(nh * rows, np.float32)
+        o = np.zeros(nh * d, np.float32)
+        cfgs = [(pos, orc.config(nh, nkv, d, rows, w if w else orc.NO_WINDOW)) for pos, w in calls]
+        attended = [pos + 1 - orc.window_start(pos, w if w else orc.NO_WINDOW) for pos, w in calls]
+        step_bytes = layers * sum(decode_bytes(a, nh, nkv, d, 4) for a in attended) / len(attended)
+        e = {"workload": f"{nh}q/{nkv}kv heads, d{d}, {kv} values as f32, {layers} layers per step, "
+                         f"{steps} step(s)", "sample": note}
+        for label, nw in lines:
+            pool = orc.Pool(nw)
+            try:
+                t, n = _timed(lambda: [pool.attention(q, cache, cf, 0, pos, scores=scores, out=o)
+                                       for pos, cf in cfgs], seconds_per_line)
+            finally:
+                pool.close()
+            t_layer = t / len(cfgs)
+            e[label] = {"cores": nw, "ms_per_layer": round(t_layer * 1e3, 4),
+                        "ms_per_step": round(t_layer * layers * 1e3, 3),
+                        "ms_total": round(t_layer * layers * steps * 1e3, 3),
+                        "gbs_f32": round(step_bytes / (t_layer * layers) / 1e9, 3), "runs": n}
+            log(f"cpu {name} {label}: {t_layer * 1e3:.3f} ms per layer ({n} runs)")
+        out[name] = e
+        del cache
+    for name, nh, nkv, d, kv, B, k in CPU_PREFILL_CFGS:
+        cache = _oracle_cache(orc, rng, nkv, d, B, kv)
+        c = orc.config(nh, nkv, d, B)
+        sample = list(range(k - 1, B, k))
+        qs = rng.standard_normal((len(sample), nh * d), dtype=np.float32)
+        scores = np.zeros(nh * B, np.float32)
+        o = np.zeros(nh * d, np.float32)
+        work_all = B * (B + 1) // 2
+        work_sample = sum(b + 1 for b in sample)
+        flops = prefill_flops(B, nh, d)
+        e = {"workload": f"{nh}q/{nkv}kv heads, d{d}, {kv} values as f32, {B}-token causal prompt (pos0 0)",
+             "sample": (f"every {k}-th prompt row ({len(sample)} rows, {work_sample} of {work_all} causal "
+                        f"pairs), scaled by {work_all / work_sample:.3f}" if k > 1 else "every prompt row")}
+        for label, nw in lines:
+            pool = orc.Pool(nw)
+            try:
+                t, n = _timed(lambda: [pool.attention(qs[i], cache, c, 0, b, scores=scores, out=o)
+                                       for i, b in enumerate(sample)], seconds_per_line)
+            finally:
+                pool.close()
+            t_all = t * work_all / work_sample
+            e[label] = {"cores": nw, "ms_per_call": round(t_all * 1e3, 2),
+                        "tflops": round(flops / t_all / 1e12, 5), "runs": n}
+            log(f"cpu {name} {label}: {t_all * 1e3:.1f} ms per call (extrapolated; {n} sample runs)")
+        out[name] = e
+        del cache
+    return out
 
 
 def cpu_model():
@@ -913,6 +1091,8 @@ def main():
         # C2's shape at 8K with the layer's RoPE of q and k_cur fused into
         # the same launch (the next-row prologue), to price the rotation.
         "C2_rope_fused": bench_decode_cfg(ctx, torch, "C2+RoPE", 32, 32, 32, 128, "f16", 8192, rope=True),
+        # C2 as BASELINE.json writes it: 256 steps, L 4097 -> 4352.
+        "C2_256": bench_decode_c2_run(ctx, torch),
     }
     pre = {} if args.no_prefill else {
         "C4_L512": bench_prefill(ctx, torch, 32, 8, 128, 512),
@@ -930,6 +1110,7 @@ def main():
     full = None if args.no_gemv else bench_full_decode(ctx, torch, ctx_rows=args.ctx)
     fullp = None if (args.no_gemv or args.no_prefill) else bench_full_prefill(ctx, torch)
     cpu = None if args.no_cpu else cpu_baseline()
+    cpu_cfg = None if args.no_cpu else cpu_baseline_configs()
     ctx.close()
     traffic = load_traffic()
     counters = load_counters()
@@ -1033,6 +1214,32 @@ def main():
                              "ms_per_layer": round(cpu["pool_default"]["ms_per_layer"], 3),
                              "note": "pool.zig's default worker count, (workers + 1) / 2"},
         }
+    if cpu_cfg:
+        # The same GPU run's figure beside each CPU config line.
+        gpu = {}
+        if dec_more:
+            layers = {"C1": 1, "C3": 32, "C5_decode": 26}
+            for name, key in (("C1", "C1"), ("C3", "C3"), ("C5_decode", "C5")):
+                if key in dec_more:
+                    gpu[name] = {"ms_per_step": round(dec_more[key]["us_per_launch"] * layers[name] / 1e3, 4)}
+            if "C2_256" in dec_more:
+                gpu["C2_256"] = {"ms_total": dec_more["C2_256"]["ms_total"],
+                                 "ms_per_step": dec_more["C2_256"]["ms_per_step"]}
+        if pre:
+            for name, key in (("C4_L512", "C4_L512"), ("C4_L2048", "C4_L2048"), ("C4_L8192", "C4_L8192"),
+                              ("C5_prefill", "C5_L4096")):
+                gpu[name] = {"ms_per_call": round(pre[key]["avg_launch_s"] * 1e3, 4)}
+        for name, e in cpu_cfg.items():
+            if name in gpu:
+                e["gpu"] = gpu[name]
+                k = "ms_per_call" if "ms_per_call" in gpu[name] else "ms_per_step"
+                e["gpu"]["speedup_vs_pool"] = round(e["pool"][k] / gpu[name][k], 1)
+        line.setdefault("cpu_baseline", {})["configs"] = cpu_cfg
+        line["cpu_baseline"]["configs_note"] = (
+            "every BASELINE config on the CPU oracle (C restatement of cpuAttention / attentionCausal, "
+            "f32 values of the KV dtype): faithful_1t = one thread, as vantablack runs attention; pool / "
+            "pool_default = heads split over a pool.zig-style pool at the box's CPU share and at pool.zig's "
+            "default worker count; each line a bounded sample (see `sample`) extrapolated to the config")
     print(json.dumps(line), flush=True)
 
 

@@ -239,8 +239,15 @@ void vtb_hip_segment_attn_decode_append(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbH
  * (256 KiB of counters, the rest partials; each context holds its own copy
  * until it is destroyed), not in the context's growable workspace.  A shape
  * whose workspace would exceed it is rejected with 5 (EUNSUPPORTED) at
- * commit; every n_q = 1 shape of the default one-workgroup-per-CU plan fits
- * (partials about n_kv * n_splits * G * (head_dim + 2) * 4 bytes).  Calls
+ * commit.  A shape fits when its split plan keeps
+ * (n_part + n_gpart) * (head_dim + 2) * 4 <= 8 MiB - 256 KiB and its
+ * arrival counters within 256 KiB, where n_part = units * n_splits * G and
+ * n_gpart = units * ceil(n_splits / 16) * G (units: KV heads, or head pairs
+ * for the head-group kernels; G: the kernel's query slots per unit).  The
+ * split count depends on the CU count and VTB_DECODE_TARGET_WGS, so this is
+ * not a fixed set of shapes; the BASELINE decode shapes (C1, C2, C3, C5)
+ * fit on a 256-CU MI355X with the default plan, and wider ones can be
+ * rejected (e.g. 200 KV heads with 16-query groups at head_dim 256).  Calls
  * that overlap on one context race on the array; calls on one stream do
  * not (each launch leaves its counters at zero for the next). */
 void vtb_hip_segment_attn_decode_append_noalloc(VtbHipSeg *seg, VtbHipBuf *out_buf, VtbHipBuf *q_buf,

@@ -16,6 +16,9 @@ a 2.6e-4 relative output error flipping it).  Such a row may pick a different
 index only if that index's reference logit is within TIE_REL (1e-3, half the
 output tolerance) of max|reference logit| from the best; at most 1% of the
 rows (at least one) may do so, and every other row must match exactly.
+Every checked case records how many rows such a tie flipped (FLIPS); the
+GPU run prints the per-case counts at the end of the session
+(tests/conftest.py), so "identical argmax" is visible case by case.
 """
 from __future__ import annotations
 
@@ -29,6 +32,10 @@ TIE_REL = 1e-3
 
 
 _W = {}
+
+# (case, rows checked, tie-flipped rows) of every f16/bf16 check in this
+# process, in order.
+FLIPS = []
 
 
 def _projection(orc, seed, dim):
@@ -70,6 +77,7 @@ def check(orc, got, ref, n_heads, dtype, n_queries=1, what=""):
     assert err <= TOL[dtype], f"{what}: rel err {err:.3e} > {TOL[dtype]:.0e}"
     if dtype != "f32":
         rows, not_tie = argmax_mismatches(orc, got, ref, n_queries)
+        FLIPS.append((what, n_queries, len(rows)))
         assert not not_tie, f"{what}: downstream argmax differs on rows {not_tie[:10]}"
         assert len(rows) <= max(1, n_queries // 100), \
             f"{what}: downstream argmax tie-flips on {len(rows)} of {n_queries} rows"

@@ -3,6 +3,10 @@ against the allocating one (vtb_hip_segment_attn_decode_append) through the C
 ABI: two calls in a row on the fixed scratch, the second with a smaller
 input, each bit-identical to the existing entry on the same inputs (the same
 kernels and split plan; only where the split-K workspace lives differs).
+The no-allocation calls run first, on a fresh context, and the context's
+growable scratch (split-K workspace, counters, prefill and matmul scratch)
+must read zero bytes before and after them: a path that fell back on the
+context workspace would grow it.
 Also: a shape whose workspace exceeds the fixed scratch is rejected at commit."""
 import numpy as np
 import pytest
@@ -10,8 +14,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 
-def _case(ctx, orc, n_heads, n_kv, d, L, dtype, seed):
-    import vantablack_amd as vb
+def _inputs(orc, n_heads, n_kv, d, L, dtype, seed):
     rng = np.random.default_rng(seed)
     rows = L
     k = rng.standard_normal((rows, n_kv, d)).astype(np.float32)
@@ -21,25 +24,39 @@ def _case(ctx, orc, n_heads, n_kv, d, L, dtype, seed):
     q = (rng.standard_normal(n_heads * d) / np.sqrt(d)).astype(np.float32)
     kc = rng.standard_normal(n_kv * d).astype(np.float32)
     vc = rng.standard_normal(n_kv * d).astype(np.float32)
-    dt = vb.hip.DTYPES[dtype]
-    outs = []
-    for noalloc in (False, True):
-        kb, vbuf = ctx.to_device(ks), ctx.to_device(vs)  # fresh caches: the fused append writes row L-1
-        qb, kcb, vcb = ctx.to_device(q), ctx.to_device(kc), ctx.to_device(vc)
-        ob = ctx.alloc(n_heads * d * 4)
-        with ctx.segment() as seg:
-            f = seg.attn_decode_append_noalloc if noalloc else seg.attn_decode_append
-            f(ob, qb, kb, 0, vbuf, 0, kcb, vcb, n_heads, n_kv, d, L, 1.0 / np.sqrt(d), dt)
-        ctx.wait_idle()
-        outs.append(ctx.download(ob, np.float32, n_heads * d))
-    return outs
+    return ks, vs, q, kc, vc
+
+
+def _run(c, inputs, n_heads, n_kv, d, L, dtype, noalloc):
+    import vantablack_amd as vb
+    ks, vs, q, kc, vc = inputs
+    kb, vbuf = c.to_device(ks), c.to_device(vs)  # fresh caches: the fused append writes row L-1
+    qb, kcb, vcb = c.to_device(q), c.to_device(kc), c.to_device(vc)
+    ob = c.alloc(n_heads * d * 4)
+    with c.segment() as seg:
+        f = seg.attn_decode_append_noalloc if noalloc else seg.attn_decode_append
+        f(ob, qb, kb, 0, vbuf, 0, kcb, vcb, n_heads, n_kv, d, L, 1.0 / np.sqrt(d), vb.hip.DTYPES[dtype])
+    c.wait_idle()
+    return c.download(ob, np.float32, n_heads * d)
+
+
+# C2's head shape at 8K rows (8 splits per head), then a smaller GQA d256
+# case (more splits, two-level merge) on the same fixed scratch.
+CASES = ((32, 32, 128, 8193, "f16", 1), (8, 1, 256, 20000, "bf16", 2))
 
 
 def test_noalloc_decode_matches_the_allocating_entry_twice(ctx, orc):
-    # C2's head shape at 8K rows (8 splits per head), then a smaller GQA
-    # d256 case (more splits, two-level merge) on the same fixed scratch.
-    for args in ((32, 32, 128, 8193, "f16", 1), (8, 1, 256, 20000, "bf16", 2)):
-        a, b = _case(ctx, orc, *args)
+    import vantablack_amd as vb
+    inputs = [_inputs(orc, *args) for args in CASES]
+    fresh = vb.Context()
+    try:
+        assert fresh.scratch_bytes == 0
+        got = [_run(fresh, inp, *args[:5], noalloc=True) for inp, args in zip(inputs, CASES)]
+        assert fresh.scratch_bytes == 0, "the no-allocation entry grew the context's workspace"
+    finally:
+        fresh.close()
+    for inp, args, b in zip(inputs, CASES, got):
+        a = _run(ctx, inp, *args[:5], noalloc=False)
         assert np.isfinite(b).all()
         assert np.array_equal(a, b), f"noalloc differs from the allocating entry for {args}"
 
