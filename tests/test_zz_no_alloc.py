@@ -45,7 +45,10 @@ def _run(c, inputs, n_heads, n_kv, d, L, dtype, noalloc):
 CASES = ((32, 32, 128, 8193, "f16", 1), (8, 1, 256, 20000, "bf16", 2))
 
 
-def test_noalloc_decode_matches_the_allocating_entry_twice(ctx, orc):
+def test_noalloc_decode_matches_the_allocating_entry_twice(orc):
+    # One fresh context for both entries: a context's split plan (its
+    # per-XCD row weights, measured at init) fixes the summation order, so
+    # the two entries agree bit for bit only on the same context.
     import vantablack_amd as vb
     inputs = [_inputs(orc, *args) for args in CASES]
     fresh = vb.Context()
@@ -53,12 +56,12 @@ def test_noalloc_decode_matches_the_allocating_entry_twice(ctx, orc):
         assert fresh.scratch_bytes == 0
         got = [_run(fresh, inp, *args[:5], noalloc=True) for inp, args in zip(inputs, CASES)]
         assert fresh.scratch_bytes == 0, "the no-allocation entry grew the context's workspace"
+        for inp, args, b in zip(inputs, CASES, got):
+            a = _run(fresh, inp, *args[:5], noalloc=False)
+            assert np.isfinite(b).all()
+            assert np.array_equal(a, b), f"noalloc differs from the allocating entry for {args}"
     finally:
         fresh.close()
-    for inp, args, b in zip(inputs, CASES, got):
-        a = _run(ctx, inp, *args[:5], noalloc=False)
-        assert np.isfinite(b).all()
-        assert np.array_equal(a, b), f"noalloc differs from the allocating entry for {args}"
 
 
 def test_noalloc_decode_rejects_a_workspace_beyond_the_scratch(ctx, orc, monkeypatch):

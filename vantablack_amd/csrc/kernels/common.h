@@ -14,6 +14,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 // Storage tags for the KV cache element type.
 struct kv_f32 { static constexpr int bytes = 4; };
@@ -241,6 +242,15 @@ __device__ inline void buffer_store_f4_coherent(__amdgpu_buffer_rsrc_t r, int of
 // Wait for all of this wave's vector-memory loads, including buffer->LDS
 // transfers (their LDS writes have landed when vmcnt reaches zero).
 __device__ inline void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Wait until at most N of this wave's vector-memory operations are
+// outstanding (they complete in issue order for loads).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Wait for all of this wave's LDS operations.
+__device__ inline void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // Gated activations of the FFN (math.zig:154-175): silu(z) * u and the
 // tanh-approximate gelu(z) * u, in the reference's operation order with no

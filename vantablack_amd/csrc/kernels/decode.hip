@@ -68,6 +68,13 @@ __device__ inline float rope_elem(const float* x, int i, const float* inv_freq, 
   return first ? x0 * cs - x1 * sn : x0 * sn + x1 * cs;
 }
 
+// Cache policy of the MFMA form's K/V tile DMA (buffer intrinsic aux bits:
+// 2 = non-temporal; K/V rows are streamed once per launch).
+#ifndef VTB_DECODE_DMA_AUX
+#define VTB_DECODE_DMA_AUX 2
+#endif
+constexpr int kDecodeDmaAux = VTB_DECODE_DMA_AUX;
+
 // Compile-time integer argument (DPP control) for lambdas.
 template <int N> struct ic { static constexpr int value = N; };
 
@@ -283,9 +290,9 @@ __device__ __forceinline__ void decode_merge(const DecodeArgs& a, const DecodeUn
 //   A workgroup's (m, l) values stay in one piece: with one query's slots
 //   adjacent instead ([G][split][2]), eight workgroups wrote 8-byte pieces
 //   of each 64-byte line and C5 took 1.3 us longer.
-template <int G, int D, int NW>
+template <int G, int D, int NW, int SOS = G * D>
 __device__ __forceinline__ void decode_finish(const DecodeArgs& a, const DecodeUnit& u, const float (*sm)[G],
-                                              const float (*sl)[G], const float (*so)[G][D]) {
+                                              const float (*sl)[G], const float* so) {
   constexpr int NT = NW * 64;
   constexpr int C4 = D / 4;
   constexpr int MC = G * C4;
@@ -315,7 +322,7 @@ __device__ __forceinline__ void decode_finish(const DecodeArgs& a, const DecodeU
       if (sm[w][g] == -INFINITY) continue;
       const float f = exp2_fast(sm[w][g] - M);
       L = fmaf(sl[w][g], f, L);
-      const f32x4 ow = *reinterpret_cast<const f32x4*>(&so[w][g][d4 * 4]);
+      const f32x4 ow = *reinterpret_cast<const f32x4*>(&so[w * SOS + g * D + d4 * 4]);
       O.x = fmaf(ow.x, f, O.x);
       O.y = fmaf(ow.y, f, O.y);
       O.z = fmaf(ow.z, f, O.z);
@@ -610,15 +617,54 @@ __device__ __forceinline__ void decode_scalar_body(const DecodeArgs& a) {
     }
   }
   __syncthreads();
-  decode_finish<GS, D, NW>(a, u, s_m, s_l, s_o);
+  decode_finish<GS, D, NW>(a, u, s_m, s_l, &s_o[0][0][0]);
 }
 
 // ------------------------------------------------------------------ MFMA form
+// f16/bf16 caches with GQA groups of 4, 8 or 16: both products of a 16-key
+// block run on the matrix cores, with K and V staged in LDS by DMA.
+//
+// Staging.  Each wave streams its own contiguous rows, 16 keys per block,
+// through two LDS stages of its own (K rows, then V rows, 2*D bytes each).
+// A block is filled by buffer_load_dwordx4 ... lds (16 bytes per lane, the
+// lanes' LDS writes contiguous in lane order); lane slots pick their source
+// chunk so that chunk c of row r lands in slot c ^ f(r) of the row
+// (f = kswz / vswz), which spreads the later 16-byte K reads and 8-byte V^T
+// reads over all LDS banks.  Rows past the wave's range lie outside the
+// block's buffer descriptor and read as zero (their scores are masked).
+// Both stages' blocks are in flight while a block is computed.
+//
+// Scores.  v_mfma_f32_16x16x32_{bf16,f16}: A = Q' (rows 4q + p of a row
+// group of four queries, p = 0..2 the three exact 16-bit pieces of query q
+// scaled by 2^-e, p = 3 zero), B = K^T from LDS (lane l: key l % 16, 8
+// contiguous head elements), D/32 instructions per row group.  Lane l gets
+// query l/16's three piece products against key l % 16 and adds them.
+//
+// P.V.  v_mfma_f32_16x16x16_{bf16,f16}: A = P' (rows: SL slots per query,
+// QPR queries per row group; the first NPC slots hold the exact 16-bit
+// pieces of P, the rest zero), B = V (16 keys x 16 head columns), read from
+// the row-major V stage with ds_read_b64_tr_b16, which hands lane l of each
+// 16-lane group g column l % 16 of keys 4g .. 4g + 3.  P crosses from the
+// score layout (one key, one query per lane) to the A layout through a
+// 512-byte LDS tile per wave.  O accumulates in f32, D/16 instructions per
+// row group.  With SL = 2 (groups of 8 or 16) P enters as two pieces, 16
+// significant bits for bf16 (relative error <= 2^-17 per weight) and 22 for
+// f16; with SL = 4 (groups of 4) as three, exact.  For f16 P is scaled by
+// 2^7 first (P <= 2^8 stays inside f16's range; the scale leaves at the end).
+//
+// Softmax.  Online, with a lazy reference: a query's running max m is only
+// raised when a block's max exceeds it by more than 8 (log2 units), so
+// P <= 2^8 and most blocks skip the O rescale.  l sums the f32 P before
+// rounding.  The rescale factors cross to the P.V layout through LDS.
 template <typename KV> struct DecMfma;
 template <> struct DecMfma<kv_bf16> {
   __device__ static inline f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
+  }
+  __device__ static inline f32x4 mma16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
+                                                     0, 0, 0);
   }
   // x = piece + rest: piece the nearest bf16, rest exact in f32.
   __device__ static inline uint16_t piece(float x, float& rest) {
@@ -626,48 +672,70 @@ template <> struct DecMfma<kv_bf16> {
     rest = x - __builtin_bit_cast(float, (uint32_t)h << 16);
     return h;
   }
+  // P enters unscaled: bf16 has f32's exponent range.
+  static constexpr float kPScale = 1.0f;
 };
 template <> struct DecMfma<kv_f16> {
   __device__ static inline f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
                                                   0, 0);
   }
+  __device__ static inline f32x4 mma16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0,
+                                                 0);
+  }
   __device__ static inline uint16_t piece(float x, float& rest) {
     const _Float16 h = (_Float16)x;  // v_cvt_f16_f32: round to nearest even
     rest = x - (float)h;
     return __builtin_bit_cast(uint16_t, h);
   }
+  // P <= 2^8 (lazy reference); times 2^7 stays below f16's largest finite
+  // value, and weights down to 2^-21 stay normal.
+  static constexpr float kPScale = 128.0f;
 };
 
-// Scores of a 16-key block on v_mfma_f32_16x16x32: A = Q' (16 rows
-// q' = 4*q + p, p = 0..2 the pieces of query q, p = 3 zero), B = K^T (16 key
-// columns), K = 32 head elements per instruction, D/32 instructions.  Lane l
-// supplies row / column l % 16 and elements 8*(l/16) .. +7 of each 32; it
-// receives rows 4*(l/16) .. +3 of column l % 16: the three pieces of query
-// l/16 (of its group of four) against key l % 16.
-template <typename KV, int D, int G, int NW, int NB>
+// Slot of chunk c of staged row r: c ^ kswz(r) for K, c ^ vswz(r) for V
+// (C = D/8 chunks per row).  K is read 16 rows x one chunk per 16 lanes,
+// V^T 4 rows x two chunks per 16 lanes; the XOR spreads both over the banks.
+template <int D>
+__device__ constexpr int kswz(int r) { return r % (D / 8); }
+template <int D>
+__device__ constexpr int vswz(int r) { return (2 * r) % (D / 8); }
+
+typedef __attribute__((address_space(3))) char dchar;
+
+template <typename KV, int D, int G, int NW>
 __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a) {
   static_assert(G % 4 == 0, "MFMA decode takes GQA groups of 4, 8, 16");
-  constexpr int NG = G / 4;          // MFMA row groups of four queries
-  constexpr int KM = D / 32;         // MFMAs per 16-key block
-  constexpr int TK = 16 * NB;        // keys per wave tile
-  constexpr int EPL = 8;             // V elements per lane per 16-byte load
-  constexpr int LPR = D / EPL;       // V lanes per row
-  constexpr int RPW = 64 / LPR;      // V rows per load instruction
-  constexpr int VI = TK / RPW;       // V load instructions per tile
+  constexpr int NG = G / 4;            // score row groups (four queries each)
+  constexpr int KM = D / 32;           // score MFMAs per 16-key block and row group
+  constexpr int C = D / 8;             // 16-byte chunks per K or V row
+  constexpr int RB = 2 * D;            // bytes per staged row
+  constexpr int VOFF = 16 * RB;        // the V rows follow the K rows in a stage
+  constexpr int SB = 2 * 16 * RB;      // bytes per wave per stage
+  constexpr int NI = 16 * C / 64;      // DMA instructions per 16-row K (or V) block
+  constexpr int QPR = G >= 8 ? 8 : 4;  // queries per P.V row group
+  constexpr int SL = 16 / QPR;         // P' rows per query
+  constexpr int NPC = SL < 3 ? SL : 3; // P pieces per query
+  constexpr int NPG = G / QPR;         // P.V row groups
+  constexpr int ND = D / 16;           // P.V MFMAs per row group (16-column blocks)
   constexpr int NT = NW * 64;
-  constexpr int QLD = D + 8;         // Q' row stride in LDS (16-byte pad)
-  static_assert(TK % RPW == 0, "V rows per tile");
+  constexpr int QLD = D + 8;           // Q' row stride in LDS (16-byte pad)
+  constexpr bool QREG = NG * KM <= 8;  // Q' operands held in registers (else read per block)
+  static_assert(NI * 64 == 16 * C && NI >= 1, "DMA block");
+  static_assert((long long)G * D * 4 <= SB, "a wave's partial must fit its stage");
 
+  __shared__ __attribute__((aligned(16))) char s_stg0[NW * SB];
+  __shared__ __attribute__((aligned(16))) char s_stg1[NW * SB];
   __shared__ float s_m[NW][G];
   __shared__ float s_l[NW][G];
-  __shared__ __attribute__((aligned(16))) float s_o[NW][G][D];
   __shared__ __attribute__((aligned(16))) uint16_t s_q[4 * G][QLD];
   __shared__ float s_qe[G];
-  __shared__ __attribute__((aligned(16))) float s_p[NW][TK * G + G];
+  __shared__ __attribute__((aligned(16))) uint16_t s_p[NW][NPG][16 * 16];
+  __shared__ float s_cr[NW][G];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   DecodeUnit u;
   if (!decode_unit(a, u)) return;
   const int b = u.b, kvh = u.kvh, h_lo = u.h_lo, gs = u.gs;
@@ -675,38 +743,49 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a) {
   decode_append<KV, D, NT>(a, u);
 
   const long long rs = (long long)a.n_kv * D * 2;  // row stride, bytes
-  const char* kbase = (const char*)a.k + (long long)kvh * D * 2 + (lane >> 4) * 16;
-  const char* vbase = (const char*)a.v + (long long)kvh * D * 2 + (lane % LPR) * 16;
-  const int kcol = lane & 15, vrow = lane / LPR, vcol = lane % LPR;
+  const char* kbase = (const char*)a.k + (long long)kvh * D * 2;
+  const char* vbase = (const char*)a.v + (long long)kvh * D * 2;
+  const int kcol = lane & 15, grp = lane >> 4;
 
   // This wave's contiguous rows [w0, w1): an equal share, rounded to 16.
   const long long per_wave = ((r1 - r0 + NW - 1) / NW + 15) / 16 * 16;
   const long long w0 = r0 + (long long)wave * per_wave;
   const long long w1 = (w0 + per_wave < r1) ? w0 + per_wave : r1;
+  const int n_blk = w0 < w1 ? (int)((w1 - w0 + 15) / 16) : 0;
 
-  auto issue = [&](long long t0, u32x4 (&kr)[NB][KM], u32x4 (&vr)[VI]) {
+  // DMA source offsets of this lane inside a block (the same for every
+  // block): slot s = 64 i + lane is chunk (s % C) ^ f(row) of row s / C.
+  int koff[NI], voff[NI];
 #pragma unroll
-    for (int bb = 0; bb < NB; ++bb) {
-      const long long row = t0 + 16 * bb + kcol;
-      const long long rc = row < w1 ? row : w1 - 1;  // clamp: never read past the range
+  for (int i = 0; i < NI; ++i) {
+    const int s = 64 * i + lane, r = s / C, cs = s % C;
+    koff[i] = (int)(r * rs) + 16 * (cs ^ kswz<D>(r));
+    voff[i] = (int)(r * rs) + 16 * (cs ^ vswz<D>(r));
+  }
+  dchar* const stg0 = (dchar*)s_stg0 + wave * SB;
+  dchar* const stg1 = (dchar*)s_stg1 + wave * SB;
+  // Block j (rows w0 + 16 j ...) of K and V into a stage.
+  auto issue = [&](int j, dchar* st) {
+    const long long t0 = w0 + 16LL * j;
+    const long long nr = w1 - t0 < 16 ? w1 - t0 : 16;
+    const auto rk = buffer_rsrc(kbase + t0 * rs, (unsigned)(nr * rs));
+    const auto rv = buffer_rsrc(vbase + t0 * rs, (unsigned)(nr * rs));
 #pragma unroll
-      for (int km = 0; km < KM; ++km) kr[bb][km] = load16(kbase + rc * rs + 64 * km);
-    }
+    for (int i = 0; i < NI; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(st + 1024 * i), 16,
+                                               koff[i], 0, 0, kDecodeDmaAux);
 #pragma unroll
-    for (int i = 0; i < VI; ++i) {
-      const long long row = t0 + i * RPW + vrow;
-      const long long rc = row < w1 ? row : w1 - 1;
-      vr[i] = load16(vbase + rc * rs);
-    }
+    for (int i = 0; i < NI; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(st + VOFF + 1024 * i),
+                                               16, voff[i], 0, 0, kDecodeDmaAux);
   };
 
   // Stage Q' in LDS: wave w takes queries w, w + NW, ...; lane l holds
   // elements E*l .. +E-1.  Each query is scaled by the power of two 2^-e that
   // brings its largest |x| into [2^14, 2^15) (exact), then split into three
   // pieces of the cache's 16-bit type.  Slots past the group (gs < G) are
-  // zero.  The query loads are issued before the first K/V tile's: a wave's
-  // loads return in order, so the staging waits only for them while the tile
-  // stays in flight.
+  // zero.  The query loads are issued before the first blocks' DMA: a wave's
+  // loads return in order, so the staging waits only for them.
   constexpr int E = D / 64;
   constexpr int QPW = (G + NW - 1) / NW;  // queries staged per wave
   const bool rope = a.rope_inv_freq != nullptr;
@@ -730,9 +809,8 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a) {
     }
   }
   __builtin_amdgcn_sched_barrier(0);
-  u32x4 ka[NB][KM], va[VI], kb[NB][KM], vb[VI];
-  long long t0 = w0;
-  issue(t0, ka, va);  // in flight while the queries are staged
+  if (n_blk > 0) issue(0, stg0);
+  if (n_blk > 1) issue(1, stg1);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < QPW; ++j) {
@@ -768,152 +846,197 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a) {
       if (lane == 0) s_qe[g] = pow2f(ex);
     }
   }
+  // The P' tile's zero slots (rows NPC .. SL-1 of every query) stay zero.
+  if constexpr (NPC < SL) {
+    for (int i = lane; i < NPG * 16 * 16; i += 64) {
+      const int row = (i >> 4) & 15;
+      if (row % SL >= NPC) s_p[wave][i >> 8][i & 255] = 0;
+    }
+  }
   __syncthreads();
-  u32x4 qa[NG][KM];
+  auto qfrag = [&](int gi, int km) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(&s_q[16 * gi + kcol][32 * km + 8 * grp]);
+  };
+  u32x4 qa[QREG ? NG : 1][QREG ? KM : 1];
+  if constexpr (QREG) {
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi)
+#pragma unroll
+      for (int km = 0; km < KM; ++km) qa[gi][km] = qfrag(gi, km);
+  }
   float qup[NG];
 #pragma unroll
-  for (int gi = 0; gi < NG; ++gi) {
-#pragma unroll
-    for (int km = 0; km < KM; ++km)
-      qa[gi][km] = *reinterpret_cast<const u32x4*>(&s_q[16 * gi + kcol][32 * km + 8 * (lane >> 4)]);
-    qup[gi] = s_qe[4 * gi + (lane >> 4)];
-  }
+  for (int gi = 0; gi < NG; ++gi) qup[gi] = s_qe[4 * gi + grp];
 
-  // Online softmax state: lanes of 16-lane row r hold query 4*gi + r's
-  // running max m[gi] and their keys' share of its sum; acc is in V layout.
-  float m[NG], lsum[NG], acc[G][EPL];
+  // Online softmax state.  Score layout: lanes of group grp in row group gi
+  // hold query 4 gi + grp: its reference max m and their keys' share of its
+  // sum.  P.V layout: lane l holds rows 4 grp .. +3 of every 16-column O
+  // tile of each P.V row group.
+  float m[NG], lsum[NG];
 #pragma unroll
   for (int gi = 0; gi < NG; ++gi) {
     m[gi] = -INFINITY;
     lsum[gi] = 0.0f;
   }
+  f32x4 o[NPG][ND];
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+  for (int pg = 0; pg < NPG; ++pg)
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
-  float* pw = &s_p[wave][0];  // [TK][G] probabilities, then [G] rescale factors
+    for (int nd = 0; nd < ND; ++nd) o[pg][nd] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  uint16_t* const pt = &s_p[wave][0][0];
+  float* const crw = &s_cr[wave][0];
+  // V^T operand read of lane l = 16 g + 4 j + c: row 4 g + j, columns
+  // n0 + 4 c .. + 3 (chunk n0/8 + c/2, half c % 2).
+  const int vrow = 4 * grp + ((lane >> 2) & 3), vc = lane & 3;
 
-  auto compute = [&](long long tt, const u32x4 (&kr)[NB][KM], const u32x4 (&vr)[VI]) {
-    float s[NB][NG];
+  auto compute = [&](const dchar* st, int j) {
+    const long long t0 = w0 + 16LL * j;
+    // Scores of the 16 keys for every row group.
+    u32x4 kb[KM];
 #pragma unroll
-    for (int bb = 0; bb < NB; ++bb)
-#pragma unroll
-      for (int gi = 0; gi < NG; ++gi) {
-        f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int km = 0; km < KM; ++km) c = DecMfma<KV>::mma(qa[gi][km], kr[bb][km], c);
-        const float v = ((c.x + c.y) + c.z) * qup[gi];
-        s[bb][gi] = (tt + 16 * bb + kcol < w1) ? v : -INFINITY;
-      }
+    for (int km = 0; km < KM; ++km) {
+      const int ch = grp + 4 * km;
+      kb[km] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+          st + kcol * RB + 16 * (ch ^ kswz<D>(kcol)));
+    }
+    float s[NG];
 #pragma unroll
     for (int gi = 0; gi < NG; ++gi) {
-      float mt = s[0][gi];
+      f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int bb = 1; bb < NB; ++bb) mt = fmaxf(mt, s[bb][gi]);
-      mt = group_max<16>(mt);
-      const float mn = fmaxf(m[gi], mt);  // finite: key tt is always in range
-      const float corr = exp2_fast(m[gi] - mn);
-      m[gi] = mn;
-      float ls = 0.0f;
+      for (int km = 0; km < KM; ++km) c = DecMfma<KV>::mma(QREG ? qa[QREG ? gi : 0][QREG ? km : 0] : qfrag(gi, km),
+                                                           kb[km], c);
+      const float v = ((c.x + c.y) + c.z) * qup[gi];
+      s[gi] = (t0 + kcol < w1) ? v : -INFINITY;
+    }
+    // Block max per query; raise the references that grew by more than 8.
+    float mt[NG];
+    bool grow = false;
 #pragma unroll
-      for (int bb = 0; bb < NB; ++bb) {
-        const float pv = exp2_fast(s[bb][gi] - mn);
-        ls += pv;
-        pw[(16 * bb + kcol) * G + 4 * gi + (lane >> 4)] = pv;
+    for (int gi = 0; gi < NG; ++gi) {
+      mt[gi] = group_max<16>(s[gi]);  // finite: key t0 is always in range
+      grow = grow || mt[gi] > m[gi] + 8.0f;
+    }
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) {
+        const bool gg = mt[gi] > m[gi] + 8.0f;
+        const float corr = gg ? exp2_fast(m[gi] - mt[gi]) : 1.0f;  // m = -inf: 0
+        m[gi] = gg ? mt[gi] : m[gi];
+        lsum[gi] *= corr;
+        if (kcol == 0) crw[4 * gi + grp] = corr;
       }
-      lsum[gi] = lsum[gi] * corr + ls;
-      if (kcol == 0) pw[TK * G + 4 * gi + (lane >> 4)] = corr;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int pg = 0; pg < NPG; ++pg) {
+        // Rows 4 grp + r of row group pg hold query pg*QPR + (4 grp + r) / SL.
+        float cr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) cr[r] = crw[pg * QPR + (4 * grp + r) / SL];
+#pragma unroll
+        for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[pg][nd][r] *= cr[r];
+      }
+    }
+    // P of this lane's (query, key), its pieces into the P' tile at row
+    // (q % QPR) * SL + piece, column = key.
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+      const float p = exp2_fast(s[gi] - m[gi]);
+      lsum[gi] += p;
+      const int q = 4 * gi + grp;
+      uint16_t* prow = pt + (q / QPR) * 256 + ((q % QPR) * SL) * 16 + kcol;
+      float rest = p * DecMfma<KV>::kPScale;
+#pragma unroll
+      for (int pp = 0; pp < NPC; ++pp) {
+        float nxt;
+        prow[16 * pp] = DecMfma<KV>::piece(rest, nxt);
+        rest = nxt;
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    float cr[G];
+    // O += P' V: A = P' rows (lane: row l % 16, keys 4 grp .. +3), B = V^T.
 #pragma unroll
-    for (int g4 = 0; g4 < G / 4; ++g4) {
-      const f32x4 c = *reinterpret_cast<const f32x4*>(&pw[TK * G + 4 * g4]);
-      cr[4 * g4 + 0] = c.x;
-      cr[4 * g4 + 1] = c.y;
-      cr[4 * g4 + 2] = c.z;
-      cr[4 * g4 + 3] = c.w;
-    }
+    for (int pg = 0; pg < NPG; ++pg) {
+      const u32x2 pa = *reinterpret_cast<const u32x2*>(pt + pg * 256 + kcol * 16 + 4 * grp);
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[g][e] *= cr[g];
-#pragma unroll
-    for (int i = 0; i < VI; ++i) {
-      float pr[G];
-#pragma unroll
-      for (int g4 = 0; g4 < G / 4; ++g4) {
-        const f32x4 c = *reinterpret_cast<const f32x4*>(&pw[(i * RPW + vrow) * G + 4 * g4]);
-        pr[4 * g4 + 0] = c.x;
-        pr[4 * g4 + 1] = c.y;
-        pr[4 * g4 + 2] = c.z;
-        pr[4 * g4 + 3] = c.w;
+      for (int nd = 0; nd < ND; ++nd) {
+        const int ch = 2 * nd + (vc >> 1);
+        const dchar* vp = st + VOFF + vrow * RB + 16 * (ch ^ vswz<D>(vrow)) + 8 * (vc & 1);
+        const s16x4 vt = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(vp));
+        o[pg][nd] = DecMfma<KV>::mma16(pa, __builtin_bit_cast(u32x2, vt), o[pg][nd]);
       }
-      float vf[EPL];
-      Unpack<KV>::run(vr[i], vf);
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(pr[g], vf[e], acc[g][e]);
     }
-    // The next tile's LDS writes come after these reads in this wave's
-    // program order, and a wave's LDS operations complete in order.
+    // The next block's P' writes and DMA into this stage come after these
+    // reads in the wave's program order; LDS operations of a wave complete
+    // in order, and the DMA is issued after the wait below.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
 
-  // Every issue is unconditional (rows past w1 clamp to row w1 - 1, a line
-  // already in flight): with no load under a branch the compiler's wait
-  // counts stay exact, so each tile waits only for its own loads.
-  if (t0 < w1) {
-    for (;;) {
-      issue(t0 + TK, kb, vb);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(t0, ka, va);
-      t0 += TK;
-      if (t0 >= w1) break;
-      issue(t0 + TK, ka, va);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(t0, kb, vb);
-      t0 += TK;
-      if (t0 >= w1) break;
+  // Two stages per wave: block j in stage j % 2, block j + 2 issued into
+  // it once block j has been computed.  vmcnt counts this wave's DMA
+  // instructions (2 NI per block), so "block j has landed" is vmcnt <= 2 NI
+  // while block j + 1 is in flight, else 0.
+  for (int j = 0; j < n_blk; j += 2) {
+    if (j + 1 < n_blk) wait_vmcnt<2 * NI>(); else wait_vmcnt<0>();
+    compute(stg0, j);
+    if (j + 2 < n_blk) {
+      wait_lds();
+      issue(j + 2, stg0);
+    }
+    if (j + 1 >= n_blk) break;
+    if (j + 2 < n_blk) wait_vmcnt<2 * NI>(); else wait_vmcnt<0>();
+    compute(stg1, j + 1);
+    if (j + 3 < n_blk) {
+      wait_lds();
+      issue(j + 3, stg1);
     }
   }
 
-  // The wave's partial: l over the 16 lanes of each query's row, acc over
-  // the V lanes that share a column.
+  // The wave's partial: l over the 16 lanes of each query's group; O over
+  // each query's SL rows (the pieces), unscaled.  A wave without rows has
+  // m = -inf and contributes nothing.
 #pragma unroll
   for (int gi = 0; gi < NG; ++gi) lsum[gi] = group_sum<16>(lsum[gi]);
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[g][e] = stride_sum<LPR>(acc[g][e]);
   if (kcol == 0) {
 #pragma unroll
     for (int gi = 0; gi < NG; ++gi) {
-      s_m[wave][4 * gi + (lane >> 4)] = m[gi];
-      s_l[wave][4 * gi + (lane >> 4)] = lsum[gi];
+      s_m[wave][4 * gi + grp] = m[gi];
+      s_l[wave][4 * gi + grp] = lsum[gi];
     }
   }
-  if (vrow == 0) {
+  // s_o[wave][G][D] takes the place of the wave's own first stage, whose
+  // DMA has landed and whose reads are done.
+  float* const so = (float*)(s_stg0 + wave * SB);
+  constexpr float kUnscale = 1.0f / DecMfma<KV>::kPScale;
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+  for (int pg = 0; pg < NPG; ++pg)
 #pragma unroll
-      for (int e4 = 0; e4 < EPL / 4; ++e4)
-        *reinterpret_cast<f32x4*>(&s_o[wave][g][vcol * EPL + 4 * e4]) =
-            f32x4{acc[g][4 * e4], acc[g][4 * e4 + 1], acc[g][4 * e4 + 2], acc[g][4 * e4 + 3]};
-  }
+    for (int nd = 0; nd < ND; ++nd) {
+      const int col = 16 * nd + kcol;
+      if constexpr (SL == 4) {
+        so[(pg * QPR + grp) * D + col] = ((o[pg][nd][0] + o[pg][nd][1]) + o[pg][nd][2]) * kUnscale;
+      } else {
+        so[(pg * QPR + 2 * grp) * D + col] = (o[pg][nd][0] + o[pg][nd][1]) * kUnscale;
+        so[(pg * QPR + 2 * grp + 1) * D + col] = (o[pg][nd][2] + o[pg][nd][3]) * kUnscale;
+      }
+    }
   __syncthreads();
-  decode_finish<G, D, NW>(a, u, s_m, s_l, s_o);
+  decode_finish<G, D, NW, SB / 4>(a, u, s_m, s_l, reinterpret_cast<const float*>(s_stg0));
 }
 
 template <typename KV, int D, int G, int HG = 1>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
   if constexpr (decode_uses_mfma(KV::bytes, G))
-    decode_mfma_body<KV, D, G, decode_waves(KV::bytes, D, G), decode_mfma_nb(D)>(a);
+    decode_mfma_body<KV, D, G, decode_waves(KV::bytes, D, G)>(a);
   else
     decode_scalar_body<KV, D, G, decode_nit(G), decode_waves(KV::bytes, D, G), HG>(a);
 }

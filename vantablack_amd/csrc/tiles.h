@@ -26,16 +26,10 @@ constexpr int decode_nit(int g) {
 
 // Decode, MFMA form: f16/bf16 caches with GQA groups of 4 or more compute
 // the G query-key dot products of each 16-key block on
-// v_mfma_f32_16x16x32_{bf16,f16} (queries as three exact pieces); the
-// softmax and P.V stay f32 on the VALU.
+// v_mfma_f32_16x16x32_{bf16,f16} (queries as three exact pieces) and P.V on
+// v_mfma_f32_16x16x16_{bf16,f16}, with K and V staged in LDS by DMA (two
+// 16-key stages per wave).
 constexpr bool decode_uses_mfma(int kv_bytes, int g) { return kv_bytes == 2 && g >= 4; }
-// 16-key blocks per wave tile (double-buffered).  One block: at the C3
-// shape each wave owns 16 rows, and a two-block tile computed (and loaded) a
-// masked second block: 14.9 against 13.5 us per launch.
-#ifndef VTB_DECODE_MFMA_NB
-#define VTB_DECODE_MFMA_NB 1
-#endif
-constexpr int decode_mfma_nb(int) { return VTB_DECODE_MFMA_NB; }
 
 // Waves per decode workgroup.  Scalar form: for g = 1 one wave per SIMD
 // streams best: 16-wave workgroups keep 4x the loads in flight per CU and
@@ -47,18 +41,20 @@ constexpr int decode_mfma_nb(int) { return VTB_DECODE_MFMA_NB; }
 #ifndef VTB_DECODE_WAVES8
 #define VTB_DECODE_WAVES8 8
 #endif
-// MFMA form: 8 waves (two per SIMD) for head_dim <= 128 with groups of 4;
-// 4 waves, with the register file of a whole SIMD each, for head_dim 256 or
-// groups of 8 or 16 (their query pieces, accumulators and double-buffered
-// tiles exceed 256 registers).
+// MFMA form: the two K/V stages of every wave (64 * head_dim bytes each)
+// fill about 128 KiB of LDS: 8 waves (two per SIMD) for head_dim <= 128, 4
+// for 256; groups of 16 halve that to leave room for their query pieces.
 #ifndef VTB_DECODE_MFMA_WAVES
 #define VTB_DECODE_MFMA_WAVES 8
 #endif
 #ifndef VTB_DECODE_MFMA_WAVES_D256
 #define VTB_DECODE_MFMA_WAVES_D256 4
 #endif
+constexpr int decode_mfma_waves(int head_dim, int g) {
+  return (head_dim >= 256 ? VTB_DECODE_MFMA_WAVES_D256 : VTB_DECODE_MFMA_WAVES) / (g >= 16 ? 2 : 1);
+}
 constexpr int decode_waves(int kv_bytes, int head_dim, int g) {
-  return decode_uses_mfma(kv_bytes, g) ? (head_dim >= 256 || g >= 8 ? VTB_DECODE_MFMA_WAVES_D256 : VTB_DECODE_MFMA_WAVES)
+  return decode_uses_mfma(kv_bytes, g) ? decode_mfma_waves(head_dim, g)
          : g == 1                      ? VTB_DECODE_WAVES1
          : g <= 4                      ? VTB_DECODE_WAVES4
                                        : (g == 8 ? VTB_DECODE_WAVES8 : 4);

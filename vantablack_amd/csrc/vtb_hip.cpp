@@ -362,6 +362,10 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
     long long ws = (window <= 0 || qp < window) ? 0 : qp - window + 1;
     Lmax = std::max(Lmax, qp + 1 - ws);
   }
+  // The MFMA form's tile DMA addresses 16 rows of one KV head with 32-bit
+  // offsets.
+  if (vtb::decode_uses_mfma(kKvBytes[dtype], G) && (long long)(n_kv * head_dim) * 2 * 16 >= (1LL << 31))
+    return set_err(ctx, VTB_HIP_EUNSUPPORTED, "KV row too wide");
   const int HG = decode_heads_per_wg(n_heads, n_kv, head_dim, dtype, G);
   DecodePlan pl;
   int rc0 = plan_decode(ctx, n_q, n_kv / HG, head_dim, Lmax, dtype, G, HG, &pl);
