@@ -223,3 +223,40 @@ def test_fused_append_matches_separate_calls(ctx, orc, dtype):
     oc.pos = L - 1
     check(orc, outs[1], orc.cpu_attention(q, oc, orc.config(n_heads, n_kv, d, L), 0), n_heads, dtype,
           what="fused append")
+
+
+@pytest.mark.parametrize("n_heads,n_kv,d,dtype,pos,target", [
+    (8, 1, 256, "bf16", 32767, "256"),   # C5: 256 splits
+    (12, 4, 64, "f16", 3000, "512"),     # partial GQA group (slots past the group), 128 splits
+    (32, 32, 128, "f16", 8192, "1024"),  # head pairs, 64 splits
+    (6, 4, 128, "f32", 2000, "600"),     # uneven GQA map, scalar form
+])
+def test_merge_launch_matches_in_kernel_merge(ctx, orc, monkeypatch, n_heads, n_kv, d, dtype, pos, target):
+    """Merges of more splits than one level takes run as a launch of their
+    own (vtb_decode_merge); against the oracle and against the in-kernel
+    two-level merge of the same partials (a different but fixed summation
+    order), each bit-identical when repeated."""
+    import vantablack_amd as vb
+    ks, kx, vs, vx = make_kv(orc, pos + 1, n_kv, d, dtype, seed=pos % 89)
+    q = orc.normal(pos % 83 + 2, n_heads * d)
+    kb, vbuf, qb = ctx.to_device(ks), ctx.to_device(vs), ctx.to_device(q)
+    monkeypatch.setenv("VTB_DECODE_TARGET_WGS", target)
+    oc = orc.OracleKvCache(1, n_kv, d, pos + 1)
+    oc.layer_rows("k", 0)[:] = kx
+    oc.layer_rows("v", 0)[:] = vx
+    oc.pos = pos
+    ref = orc.cpu_attention(q, oc, orc.config(n_heads, n_kv, d, pos + 1), 0)
+    got = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("VTB_DECODE_MERGE_LAUNCH", mode)
+        outs = []
+        for _ in range(2):
+            ob = ctx.alloc(n_heads * d * 4)
+            with ctx.segment() as seg:
+                seg.attn_decode(ob, qb, kb, 0, vbuf, 0, n_heads, n_kv, d, pos + 1, 1.0 / np.sqrt(d),
+                                vb.hip.DTYPES[dtype])
+            outs.append(ctx.download(ob, np.float32, n_heads * d))
+        assert np.array_equal(outs[0], outs[1])
+        check(orc, outs[0], ref, n_heads, dtype, what=f"merge launch={mode} h{n_heads}/{n_kv} d{d} L{pos + 1}")
+        got[mode] = outs[0]
+    assert rel_err(got["1"], got["0"], n_heads) <= 2e-6

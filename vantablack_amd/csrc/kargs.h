@@ -30,7 +30,7 @@ struct DecodeArgs {
   long long pos0;       // absolute position of query 0
   long long window;     // sliding window in rows; <= 0 disables it
   float scale_log2;     // (1/sqrt(D)) * log2(e)
-  int pad;
+  int merge_mode;       // kDecodeMergeInKernel or kDecodeMergeLaunch
   const float* k_new;   // optional (decode only): f32 K/V row appended at
   const float* v_new;   //   row pos0 before attention; null when not fused
   const float* rope_inv_freq;  // optional: [D/2] 1/base^(2j/D); RoPE of q and
@@ -43,6 +43,33 @@ static_assert(offsetof(DecodeArgs, n_heads) == 72 && offsetof(DecodeArgs, pos0) 
                   offsetof(DecodeArgs, scale_log2) == 104 && offsetof(DecodeArgs, k_new) == 112 &&
                   offsetof(DecodeArgs, rope_pos) == 136 && offsetof(DecodeArgs, rope_half) == 144,
               "DecodeArgs layout");
+// DecodeArgs::merge_mode.  kDecodeMergeInKernel: the last-arriving
+// workgroup of each unit merges the split partials (in groups past
+// decode_merge_flat).  kDecodeMergeLaunch: the workgroups only publish their
+// partials and a vtb_decode_merge launch after the kernel merges them.
+constexpr int kDecodeMergeInKernel = 0;
+constexpr int kDecodeMergeLaunch = 1;
+
+// Split merge as a launch of its own (vtb_decode_merge): one wave per
+// float4 column of one unit's result, its lanes over the split partials
+// (4 per lane: n_splits <= 256).  Units and their query heads as in the
+// decode launch: unit u = (query b, KV head group kvg) with u = b * units +
+// kvg; hg KV heads of uniform GQA groups of g per unit when hg > 1, else
+// the group of KV head kvg under the (h * n_kv) / n_heads map.
+struct DecodeMergeArgs {
+  const float* ws_o;    // [n_units][n_splits][slots][D]
+  const float* ws_ml;   // [n_units][n_splits][slots][2]
+  float* out;           // [n_q][n_heads][D]
+  int n_splits;
+  int slots;            // query slots per unit (hg * g, or the kernel's G)
+  int head_dim;
+  int units;            // units per query
+  int n_units;          // units * n_q
+  int n_heads;
+  int n_kv;
+  int hg;
+};
+static_assert(sizeof(DecodeMergeArgs) == 56, "DecodeMergeArgs layout");
 
 // Causal prefill attention (vtb_prefill_d*).  Every MFMA
 // operand is f16: the f32 queries are converted in registers with a

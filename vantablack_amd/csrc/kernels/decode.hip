@@ -346,7 +346,7 @@ __device__ __forceinline__ void decode_finish(const DecodeArgs& a, const DecodeU
       }
     }
   }
-  if (single) return;
+  if (single || a.merge_mode == kDecodeMergeLaunch) return;
 
   const bool two_level = u.n_act > FLAT;
   const int n_grp = two_level ? (u.n_act + GS - 1) / GS : 1;
@@ -1041,7 +1041,80 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     decode_scalar_body<KV, D, G, decode_nit(G), decode_waves(KV::bytes, D, G), HG>(a);
 }
 
+// The split merge as a launch of its own, after a decode launch whose
+// workgroups only published their partials (kDecodeMergeLaunch: used when
+// the in-kernel merge would take two levels, C5: 256 partials of 8 KiB,
+// 21.4 -> 17.3 us per layer in a stamped probe; at one level a second
+// launch costs what it saves).  Wave w of workgroup i merges float4 column
+// 4 i + w of the concatenated unit results: lane l loads (m, l) and the
+// column of partials l, l + 64, l + 128, l + 192 (past n_splits: zeros
+// through the buffer range check), then M = max m, weights 2^(m - M),
+// L = sum l 2^(m - M) and the weighted column sum reduce over the wave in
+// a fixed order, and lane 0 writes O / L.
+__device__ __forceinline__ void decode_merge_launch(const DecodeMergeArgs& a) {
+  const int lane = threadIdx.x & 63;
+  const int D = a.head_dim, C4 = D / 4, MC = a.slots * C4;
+  const long long colg = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (colg >= (long long)a.n_units * MC) return;  // wave-uniform
+  const int ub = (int)(colg / MC), col = (int)(colg % MC);
+  const int g = col / C4, d4 = col % C4;
+  const int b = ub / a.units, kvg = ub % a.units;
+  int h_lo, gs;
+  if (a.hg > 1) {
+    h_lo = kvg * a.slots;
+    gs = a.slots;
+  } else {
+    h_lo = (kvg * a.n_heads + a.n_kv - 1) / a.n_kv;
+    gs = ((kvg + 1) * a.n_heads + a.n_kv - 1) / a.n_kv - h_lo;
+  }
+  if (g >= gs) return;  // wave-uniform: slots past a partial GQA group
+  const int n = a.n_splits;
+  const unsigned bytes_o = (unsigned)n * MC * 16, bytes_m = (unsigned)n * a.slots * 8;
+  const auto ro = buffer_rsrc(a.ws_o + (long long)ub * n * a.slots * D, bytes_o);
+  const auto rm = buffer_rsrc(a.ws_ml + (long long)ub * n * a.slots * 2, bytes_m);
+  f32x4 ov[4];
+  float mv[4], lv[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int s = lane + 64 * k;
+    ov[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          ro, s < n ? (s * MC + col) * 16 : (int)bytes_o, 0, 0));
+    // Whole-vector bit-cast (a bit_cast of one ext-vector element reads
+    // element 0 with this compiler).
+    const f32x2 ml = __builtin_bit_cast(
+        f32x2, __builtin_amdgcn_raw_buffer_load_b64(rm, s < n ? (s * a.slots + g) * 8 : (int)bytes_m, 0, 0));
+    mv[k] = s < n ? ml.x : -INFINITY;
+    lv[k] = ml.y;
+  }
+  float M = fmaxf(fmaxf(mv[0], mv[1]), fmaxf(mv[2], mv[3]));
+  M = group_max<64>(M);
+  const float Ms = M == -INFINITY ? 0.0f : M;
+  float L = 0.0f;
+  float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float f = mv[k] == -INFINITY ? 0.0f : exp2_fast(mv[k] - Ms);
+    L = fmaf(lv[k], f, L);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = fmaf(ov[k][e], f, o[e]);
+  }
+  L = group_sum<64>(L);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = group_sum<64>(o[e]);
+  if (lane == 0) {
+    float* op = a.out + ((long long)b * a.n_heads + h_lo + g) * D + d4 * 4;
+    op[0] = o[0] / L;
+    op[1] = o[1] / L;
+    op[2] = o[2] / L;
+    op[3] = o[3] / L;
+  }
+}
+
 }  // namespace vtb
+
+extern "C" __global__ __launch_bounds__(256) void vtb_decode_merge(vtb::DecodeMergeArgs a) {
+  vtb::decode_merge_launch(a);
+}
 
 // Split-K workspace of the no-allocation decode entry
 // (vtb_hip_segment_attn_decode_append_noalloc): a fixed device array of this

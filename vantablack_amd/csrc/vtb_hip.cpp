@@ -25,6 +25,7 @@ using vtb::AddNormArgs;
 using vtb::AppendArgs;
 using vtb::CopyArgs;
 using vtb::DecodeArgs;
+using vtb::DecodeMergeArgs;
 using vtb::EltArgs;
 using vtb::FillArgs;
 using vtb::GemvArgs;
@@ -82,6 +83,7 @@ struct VtbHipCtx {
               mod_qgemm = nullptr;
   hipFunction_t f_decode[kNumKv][kNumD][kNumG] = {};
   hipFunction_t f_decodeh[kNumKv][kNumD][2] = {};  // vtb_decodeh_<kv>_d<D>_g<1|2>: head-group form
+  hipFunction_t f_decode_merge = nullptr;            // vtb_decode_merge: the split merge as its own launch
   hipFunction_t f_prefill[kNumD] = {};
   hipFunction_t f_kvt[kNumKv][kNumD] = {};  // conversion pass per cache dtype (f16, bf16)
   hipFunction_t f_kvstat[kNumKv][kNumD] = {};  // statistics pass per cache dtype
@@ -413,9 +415,32 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
   a.rope_inv_freq = rope.inv_freq;
   a.rope_pos = rope.pos;
   a.rope_half = rope.half;
+  // A single query's merge that would take two levels in the kernel (more
+  // splits than decode_merge_flat) runs as a launch of its own after it;
+  // VTB_DECODE_MERGE_LAUNCH=0 keeps it in the kernel.  (With several queries
+  // the early ones have fewer active splits: in the kernel.)
+  const bool merge_launch = n_q == 1 && n_splits > vtb::decode_merge_flat(G * HG * (int)head_dim) &&
+                            env_flag("VTB_DECODE_MERGE_LAUNCH", true);
+  a.merge_mode = merge_launch ? vtb::kDecodeMergeLaunch : vtb::kDecodeMergeInKernel;
   hipFunction_t f = HG > 1 ? ctx->f_decodeh[dtype][di][G - 1] : ctx->f_decode[dtype][di][gi];
-  return launch(ctx, f, (unsigned)n_splits, (unsigned)(n_kv / HG), (unsigned)n_q,
-                64 * vtb::decode_waves(kKvBytes[dtype], (int)head_dim, G), &a);
+  int rc = launch(ctx, f, (unsigned)n_splits, (unsigned)(n_kv / HG), (unsigned)n_q,
+                  64 * vtb::decode_waves(kKvBytes[dtype], (int)head_dim, G), &a);
+  if (rc || !merge_launch) return rc;
+  DecodeMergeArgs m;
+  memset(&m, 0, sizeof m);
+  m.ws_o = a.ws_o;
+  m.ws_ml = a.ws_ml;
+  m.out = out;
+  m.n_splits = (int)n_splits;
+  m.slots = G * HG;
+  m.head_dim = (int)head_dim;
+  m.units = (int)(n_kv / HG);
+  m.n_units = (int)(n_q * (n_kv / HG));
+  m.n_heads = (int)n_heads;
+  m.n_kv = (int)n_kv;
+  m.hg = HG;
+  const long long cols = (long long)m.n_units * m.slots * (long long)(head_dim / 4);
+  return launch(ctx, ctx->f_decode_merge, (unsigned)((cols + 3) / 4), 1, 1, 256, &m);
 }
 
 // Prefill scratch layout for keys [0, vt_ld) of n_kv heads: f16 V^T
@@ -870,6 +895,7 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
       ok = hipModuleGetFunction(&ctx->f_append[kv], ctx->mod_kvcopy, name) == hipSuccess;
     }
   }
+  ok = ok && hipModuleGetFunction(&ctx->f_decode_merge, ctx->mod_decode, "vtb_decode_merge") == hipSuccess;
   ok = ok && hipModuleGetFunction(&ctx->f_copy, ctx->mod_kvcopy, "vtb_copy_f32") == hipSuccess;
   ok = ok && hipModuleGetFunction(&ctx->f_fill, ctx->mod_kvcopy, "vtb_fill_u32") == hipSuccess;
   for (int qk = 0; ok && qk < kNumQuant; ++qk)
