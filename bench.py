@@ -36,6 +36,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -569,7 +570,7 @@ def bench_full_prefill(ctx, torch, B=8192, reps=2):
     Q4_K projections (random blocks, small f16 scales), a distinct weight set
     per layer (3.9 GB).  Returns ms per prompt from HIP events on the context
     stream."""
-    import numpy as np
+    import vantablack_amd as vb
     from vantablack_amd import layer as ly
     dim, nh, nkv, hd, ffn, n_layers = 4096, 32, 8, 128, 14336, 32
     c = ly.LayerConfig(dim=dim, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn_dim=ffn, max_seq=B,
@@ -644,6 +645,24 @@ def bench_full_prefill(ctx, torch, B=8192, reps=2):
     t = e0.elapsed_time(e1) * 1e-3 / reps
     proj_flops = 2.0 * B * n_layers * sum(m * k for _, m, k in shapes) + 2.0 * vocab * dim
     attn_flops = n_layers * prefill_flops(B, nh, hd)
+    # The last layer's attention on the model's own q / K / V (s.q and the
+    # cache rows stay as the prompt left them): its time per call, and the
+    # share of (head, query block) work items that take two f16 pieces.
+    row_bytes = nkv * hd * 2
+    inv = 1.0 / math.sqrt(hd)
+    lo = (n_layers - 1) * B * row_bytes
+    ea = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(3)]
+    with ctx.segment() as seg:
+        for a0, a1 in ea:
+            a0.record(stream)
+            seg.attn_prefill(s.attn_out, s.q, kb, vb_, lo, B, 0, vb.NO_WINDOW, nh, nkv, hd, inv, vb.BF16)
+            a1.record(stream)
+    ctx.wait_idle()
+    torch.cuda.synchronize()
+    t_attn = sum(a0.elapsed_time(a1) for a0, a1 in ea) / len(ea) * 1e-3
+    qm = torch.from_numpy(ctx.download(s.q, np.float32, B * nh * hd)).to(dev).view(B, nh, hd)
+    paths = prefill_paths(torch, qm, kc[n_layers - 1].float(), vc[n_layers - 1].float(), inv)
+    del qm
     s.release()
     for b in (wb, kb, vb_, xin, last, logits):
         b.release()
@@ -651,9 +670,46 @@ def bench_full_prefill(ctx, torch, B=8192, reps=2):
     torch.cuda.empty_cache()
     log(f"full prefill: {t * 1e3:.1f} ms per {B}-token prompt ({B / t:.0f} tok/s), "
         f"{(proj_flops + attn_flops) / t / 1e12:.0f} TFLOP/s (reference flops)")
+    log(f"full prefill: last layer's attention {t_attn * 1e6:.1f} us per call; work items with two-piece "
+        f"q {paths['xq_frac']:.3f}, P {paths['xp_frac']:.3f} (score bound median {paths['bound_median']:.1f}, "
+        f"max {paths['bound_max']:.1f}; value crest max {paths['crest_max']:.2f})")
     return {"ms_per_prompt": round(t * 1e3, 2), "tok_per_s": round(B / t, 1),
             "ms_per_layer": round(t * 1e3 / n_layers, 3),
-            "tflops_reference": round((proj_flops + attn_flops) / t / 1e12, 1)}
+            "tflops_reference": round((proj_flops + attn_flops) / t / 1e12, 1),
+            "attn_last_layer_us": round(t_attn * 1e6, 2),
+            "attn_last_layer_tflops": round(prefill_flops(B, nh, hd) / t_attn / 1e12, 1),
+            "attn_precision_paths": paths}
+
+
+def prefill_paths(torch, q, k, v, inv_sqrt_hd, bm=128, tile=64):
+    """The prefill kernel's precision choice (prefill_entry) for every
+    (head, causal query block) of a pos0 = 0 prompt, from q [B][n_heads][D]
+    and the cache rows k, v [B][n_kv][D] (f32): two-piece q where
+    max |q| * max |k_t| * scale_log2 over the block's key tiles exceeds 32,
+    two-piece P where the values' crest factor over those tiles exceeds 8."""
+    B, nh, D = q.shape
+    nkv = k.shape[1]
+    nblk, nt = -(-B // bm), -(-B // tile)
+    pad = nt * tile - B
+    qn = q.norm(dim=2)                                                     # [B][nh]
+    qn = torch.nn.functional.pad(qn, (0, 0, 0, nblk * bm - B)).view(nblk, bm, nh).amax(1)
+    kn2 = torch.nn.functional.pad((k * k).sum(2), (0, 0, 0, pad)).view(nt, tile, nkv).amax(1)
+    va = torch.nn.functional.pad(v.abs().amax(2), (0, 0, 0, pad)).view(nt, tile, nkv).amax(1)
+    vs = torch.nn.functional.pad((v.double() ** 2).sum(2), (0, 0, 0, pad)).view(nt, tile, nkv).sum(1)
+    kend = torch.clamp(torch.arange(1, nblk + 1, device=q.device) * bm, max=B)
+    last = (kend + tile - 1) // tile - 1                                   # last tile of each block
+    kmax = torch.cummax(kn2, 0).values[last]                               # [nblk][nkv]
+    vmax = torch.cummax(va, 0).values[last]
+    vss = torch.cumsum(vs, 0)[last]
+    kvh = torch.arange(nh, device=q.device) * nkv // nh
+    bound = qn * kmax[:, kvh].sqrt() * (inv_sqrt_hd * 1.4426950408889634)
+    crest2 = (vmax.double() ** 2) * (kend[:, None].double() * D) / vss
+    xq = bound > 32.0
+    xp = (crest2 > 64.0)[:, kvh]
+    return {"items": nblk * nh, "xq_frac": round(xq.float().mean().item(), 4),
+            "xp_frac": round(xp.float().mean().item(), 4),
+            "bound_median": round(bound.median().item(), 2), "bound_max": round(bound.max().item(), 2),
+            "crest_max": round(crest2.max().sqrt().item(), 2)}
 
 
 def _timed(fn, budget_s):
@@ -834,8 +890,8 @@ def pmc_workload():
     C2 (vtb_decodeh_f16_d128_g1), C3 (vtb_decode_bf16_d128_g4) and C5
     (vtb_decode_bf16_d256_g8), each over PMC_DECODE's layer count of distinct
     cache layers; and the C4 (8192 tokens) and C5 (4096 tokens) causal
-    prefill calls: the statistics and conversion passes (vtb_kvstat_*,
-    vtb_kvt_*) and the attention kernels (vtb_prefill_d128,
+    prefill calls: the pre-pass (vtb_kvt_*: tile statistics and the f16
+    operands) and the attention kernels (vtb_prefill_d128,
     vtb_prefill_d256)."""
     import numpy as np
     import torch
@@ -1190,8 +1246,8 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(p8["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(p8["tflops"] / BF16_PEAK_TFLOPS, 4), "traffic": pre_tr,
                          "kernel": pre_kernel, "avg_launch_us": round(p8["avg_launch_s"] * 1e6, 2),
-                         "timed_span": "one attn_prefill call: the statistics and conversion passes "
-                                       "(vtb_kvstat_bf16_d128, vtb_kvt_bf16_d128) and the attention kernel",
+                         "timed_span": "one attn_prefill call: the pre-pass (vtb_kvt_bf16_d128: tile "
+                                       "statistics, f16 K and V^T) and the attention kernel",
                          "flops_per_launch": p8["flops"],
                          "mfma_busy": mfma_busy_field(counters.get(pre_kernel))},
             "all": {k: {"tflops": round(v["tflops"], 2), "us": round(v["avg_launch_s"] * 1e6, 2)}

@@ -291,11 +291,53 @@ def test_prefill_v_outlier_rows_beyond_f16(ctx, orc):
     prefill_case(ctx, orc, 8, 2, 128, "bf16", n_rows, seed=78, v_scale=scale)
 
 
-# A workgroup takes q and P as two f16 pieces each when its head's values
-# have a crest factor (max / rms) above 8 or the Cauchy-Schwarz bound on its
-# scores (max |q| * max |k_t| * scale_log2) exceeds 32: with one piece, x20
-# channel outliers (the C3 recipe) measured 6.9e-3 against the oracle.  Every
-# kernel shape holds both paths.
+# Value exponents per 64-key tile: bf16 value tiles whose ranges differ by
+# 16x or more get their own power-of-two unit, and the attention rescales O
+# whenever the unit changes (up the ramp, down it, through an all-zero tile
+# that fits any unit), including the d256 balanced launches, whose two
+# pieces of a split block then merge from different units.
+def _tile_ramp(n_rows, step, zero_tile=None):
+    sc = (2.0 ** (step * (np.arange(n_rows) // 64))).astype(np.float32).reshape(n_rows, 1, 1)
+    if zero_tile is not None:
+        sc[64 * zero_tile:64 * (zero_tile + 1)] = 0.0
+    return sc
+
+
+@pytest.mark.parametrize("what,step,zero_tile", [("ramp_up", 5.0, None), ("ramp_down", -5.0, None),
+                                                   ("zero_tile", 0.0, 2), ("ramp_up_zero_tile", 3.0, 4)])
+def test_prefill_value_tile_exponents(ctx, orc, what, step, zero_tile):
+    n_rows = 520
+    err = prefill_case(ctx, orc, 8, 2, 128, "bf16", n_rows, seed=83, v_scale=_tile_ramp(n_rows, step, zero_tile))
+    print(f"value tiles {what}: rel err {err:.2e}")
+
+
+@pytest.mark.parametrize("balance", ["1", "0"])
+@pytest.mark.parametrize("step", [4.0, -4.0])
+def test_prefill_d256_value_tile_exponents(ctx, orc, monkeypatch, balance, step):
+    monkeypatch.setenv("VTB_PREFILL_BALANCE", balance)
+    err = prefill_case(ctx, orc, 2, 1, 256, "bf16", 512, seed=84, v_scale=_tile_ramp(512, step))
+    print(f"d256 value tiles step {step} balance={balance}: rel err {err:.2e}")
+
+
+def test_prefill_pre_pass_starts_at_the_window(ctx, orc):
+    # Keys before the first query's window start are never read: the
+    # pre-pass starts at that key's 64-key tile and the attention's key loop
+    # and statistics at each block's own window start.  Rows before that
+    # tile hold NaN here (the oracle never reads them either); rows of that
+    # tile before the window start are finite and masked.
+    pos0, B, W = 1000, 100, 200
+    n_rows = pos0 + B
+    ks = np.ones((n_rows, 2, 1), np.float32)
+    ks[:(pos0 - W + 1) // 64 * 64] = np.nan
+    prefill_case(ctx, orc, 8, 2, 128, "bf16", B, pos0=pos0, window=W, seed=85, k_scale=ks, v_scale=ks)
+
+
+# A work item takes q as two f16 pieces when the Cauchy-Schwarz bound on its
+# scores (max |q| * max |k_t| * scale_log2 over its key tiles) exceeds 32,
+# and P as two pieces when its values' crest factor (max / rms over those
+# tiles) exceeds 8: with one piece each, x20 channel outliers (the C3
+# recipe) measured 6.9e-3 against the oracle.  Every kernel shape holds all
+# three compiled forms (q alone; q and P; neither).
 @pytest.mark.parametrize("n_heads,n_kv,d,B", [
     (8, 2, 128, 333),   # d128 (two-piece path with K fragments read in halves)
     (8, 2, 64, 300),    # d64
@@ -324,6 +366,22 @@ def test_prefill_range_beyond_f16_several_blocks(ctx, orc):
 
 def test_prefill_large_scores_take_two_pieces(ctx, orc):
     # q and k of rms ~40: scores of ~1e3 (a one-hot softmax), where q's 11-bit
-    # rounding alone would move a score by ~0.5; the score bound selects the
-    # two-piece form.
+    # rounding alone would move a score by ~0.5; the score bound selects
+    # two-piece q (values N(0,1): P in one piece).
     prefill_case(ctx, orc, 8, 2, 64, "bf16", 280, seed=82, k_scale=40.0, q_scale=40.0)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_prefill_large_scores_q_pieces_only_each_shape(ctx, orc, d):
+    # The q-only form in every kernel shape: large scores, N(0,1) values.
+    n_kv = 1 if d == 256 else 2
+    prefill_case(ctx, orc, 4 * n_kv, n_kv, d, "f16", 300, seed=86, k_scale=12.0, q_scale=12.0)
+
+
+def test_prefill_value_outliers_alone_take_p_pieces(ctx, orc):
+    # Small scores, a few value rows x300 (crest far above 8): the P pieces
+    # (compiled together with the q pieces).
+    n_rows = 400
+    vs = np.ones((n_rows, 2, 1), np.float32)
+    vs[[9, 150, 390]] = 300.0
+    prefill_case(ctx, orc, 8, 2, 128, "f16", n_rows, seed=87, v_scale=vs, q_scale=0.25)

@@ -71,23 +71,22 @@ struct DecodeMergeArgs {
 };
 static_assert(sizeof(DecodeMergeArgs) == 56, "DecodeMergeArgs layout");
 
-// Causal prefill attention (vtb_prefill_d*).  Every MFMA
-// operand is f16: the f32 queries are converted in registers with a
-// power-of-two scale per wave (32 queries of one head); keys come from the
-// conversion pass (or straight from an f16 cache) with a power-of-two
-// exponent per 64-key tile, V^T with one per KV head.  A workgroup takes q
-// and P as two f16 pieces each when its head is flagged by the conversion
-// pass (values with a crest factor above 8) or when the Cauchy-Schwarz
-// bound on its scores, max |q| * max |k| * scale_log2, exceeds 32.
+// Causal prefill attention (vtb_prefill_d*).  Every MFMA operand is f16:
+// the f32 queries are converted in registers with a power-of-two scale per
+// wave (32 queries of one head); keys come from the conversion pass (or
+// straight from an f16 cache) with a power-of-two exponent per 64-key tile,
+// V^T likewise.  A workgroup reads the conversion pass's statistics of the
+// key tiles it attends and takes q as two f16 pieces when the
+// Cauchy-Schwarz bound on its scores, max |q| * max |k_t| * scale_log2,
+// exceeds 32, and P as two pieces when its values' crest factor (max / rms)
+// exceeds 8.
 struct PrefillArgs {
   const float* q;            // [n_q][n_heads][D] f32 (prefill.zig's s.q)
   const void* k;             // f16 keys: key t of KV head h at k + h*k_head_stride + t*k_row_stride elements
   const void* vt;            // f16 V^T from the pre-pass: [n_kv][D][vt_ld]
   float* out;                // [n_q][n_heads][D] f32
-  const int* kexp;           // [n_kv][vt_ld / 64]: the keys of a tile were scaled by 2^-e; null: 0
-  const int* vexp;           // [n_kv]: the values of a head were scaled by 2^-e; null: 0
-  const int* hflag;          // [n_kv]: 1 = two-piece q and P for this head
-  const float* knorm;        // [n_kv]: largest key-row norm |k_t| of the head
+  const int* texp;           // [n_kv][vt_ld / 64][2]: a tile's keys / values were scaled by 2^-ek / 2^-ev; null: 0
+  const float* tstat;        // [n_kv][vt_ld / 64][8]: the conversion pass's tile statistics
   long long k_row_stride;    // elements between consecutive keys of one head
   long long k_head_stride;   // elements between KV heads
   long long pos0;            // absolute position of query 0
@@ -99,60 +98,44 @@ struct PrefillArgs {
   float scale_log2;          // (1/sqrt(D)) * log2(e)
   int flags;                 // kPrefillBalance
   float* part_o;             // balance: split-block partials [n_heads][nblk / 2][2][threads][D / 2] f32
-  float* part_ml;            // [n_heads][nblk / 2][2][threads][2]: (m, l)
+  float* part_ml;            // [n_heads][nblk / 2][2][threads][4]: (m, l, E, 0), O in units of 2^E
   unsigned* part_ctr;        // [n_heads][nblk / 2] x 32 arrival counters, zero between launches
 };
 // PrefillArgs::flags.  kPrefillBalance: paired key ranges (prefill_entry;
 // d256, nblk even).
 constexpr int kPrefillBalance = 1;
-static_assert(sizeof(PrefillArgs) == 144 && offsetof(PrefillArgs, flags) == 116 &&
-                  offsetof(PrefillArgs, part_o) == 120 && offsetof(PrefillArgs, part_ctr) == 136,
+static_assert(sizeof(PrefillArgs) == 128 && offsetof(PrefillArgs, flags) == 100 &&
+                  offsetof(PrefillArgs, part_o) == 104 && offsetof(PrefillArgs, part_ctr) == 120,
               "PrefillArgs layout");
-static_assert(offsetof(PrefillArgs, kexp) == 32 && offsetof(PrefillArgs, hflag) == 48 &&
-                  offsetof(PrefillArgs, knorm) == 56 && offsetof(PrefillArgs, k_row_stride) == 64 &&
-                  offsetof(PrefillArgs, pos0) == 80 && offsetof(PrefillArgs, n_q) == 96 &&
-                  offsetof(PrefillArgs, vt_ld) == 108 && offsetof(PrefillArgs, scale_log2) == 112,
+static_assert(offsetof(PrefillArgs, texp) == 32 && offsetof(PrefillArgs, tstat) == 40 &&
+                  offsetof(PrefillArgs, k_row_stride) == 48 && offsetof(PrefillArgs, pos0) == 64 &&
+                  offsetof(PrefillArgs, n_q) == 80 && offsetof(PrefillArgs, vt_ld) == 92 &&
+                  offsetof(PrefillArgs, scale_log2) == 96,
               "PrefillArgs layout");
-
-// Prefill statistics pass (vtb_kvstat_*): grid (n_part, n_kv); partition p
-// of KV head h covers rows [p*rows_per_part, +rows_per_part) and writes
-// part[h][p] = {max |K|, max |V|, sum K^2, sum V^2, max row |k_t|^2, 0, 0, 0}
-// as f32.
-struct KvStatArgs {
-  const void* k;       // layer base: row t at k + t*n_kv*D elements
-  const void* v;
-  float* part;         // [n_kv][n_part][8]
-  int n_rows;
-  int n_kv;
-  int rows_per_part;
-  int pad;
-};
-static_assert(sizeof(KvStatArgs) == 40 && offsetof(KvStatArgs, n_rows) == 24, "KvStatArgs layout");
 
 // Prefill conversion pass (vtb_kvt_*): one workgroup per (64-key tile, KV
-// head).  V^T as f16 (keys permuted inside each 16-key group) and, for bf16
-// caches, the keys as f16.  A bf16 key tile is scaled by the power of two
-// 2^-e that brings its largest magnitude into [2^14, 2^15) (e to kexp); a
-// bf16 head's values likewise by one exponent per head (e to vexp).  From
-// the statistics pass's partials it also flags the heads whose values have
-// a crest factor (max / rms) above 8 (hflag) and records the largest
-// key-row norm (knorm).
+// head), for the tiles [tile_lo, n_tiles) some query attends.  V^T as f16
+// (keys permuted inside each 16-key group) and, for bf16 caches, the keys as
+// f16.  A bf16 key tile is scaled by the power of two 2^-ek that brings its
+// largest magnitude into [2^14, 2^15), a bf16 value tile by 2^-ev with ev
+// that exponent rounded up to a multiple of 4 (largest magnitude in
+// [2^11, 2^15): tiles of one head then share ev unless their ranges differ by
+// 16x, and the attention rescales O only when ev changes); (ek, ev) go to
+// texp.  Each tile's statistics go to tstat: largest |k|, sum of k^2,
+// largest key-row |k_t|^2, valid keys, largest |v|, sum of v^2.
 struct KvtArgs {
   const void* k;         // layer base: row t at k + t*n_kv*D elements
   const void* v;
   void* k16;             // bf16 caches: f16 keys [n_kv][vt_ld][D]; null for f16 caches
   void* vt;              // f16 [n_kv][D][vt_ld]
-  const float* part;     // the statistics pass's [n_kv][n_part][8]
-  int* kexp;             // bf16 caches: [n_kv][vt_ld / 64]; null for f16 caches
-  int* vexp;             // bf16 caches: [n_kv]; null for f16 caches
-  int* hflag;            // [n_kv]
-  float* knorm;          // [n_kv]
+  float* tstat;          // [n_kv][n_tiles][8]
+  int* texp;             // bf16 caches: [n_kv][n_tiles][2] = (ek, ev); null for f16 caches
   int n_rows;            // rows of K/V to convert; keys >= n_rows are zero
   int n_kv;
-  int vt_ld;
-  int n_part;            // 1 .. 64
+  int vt_ld;             // n_tiles * 64
+  int tile_lo;           // first tile converted (blockIdx.x + tile_lo is the tile)
 };
-static_assert(sizeof(KvtArgs) == 88 && offsetof(KvtArgs, n_rows) == 72, "KvtArgs layout");
+static_assert(sizeof(KvtArgs) == 64 && offsetof(KvtArgs, n_rows) == 48, "KvtArgs layout");
 
 // KV-slot append (vtb_kv_append_*).
 struct AppendArgs {

@@ -7,23 +7,22 @@
 // over t in [window_start(pos0+b), pos0+b], kv_h = (h*n_kv)/n_heads.
 //
 // Kernels per call:
-//   vtb_kvstat_<dt>_d<D>   statistics pass: the largest |K| and |V| and the
-//                          sums of squares of each KV head over keys
-//                          [0, pos0 + n_q), as up to 64 partials per head.
-//   vtb_kvt_<dt>_d<D>      conversion pass, one workgroup per (64-key tile,
-//                          KV head): V^T as f16, [kv_h][d][key], keys
-//                          permuted inside each 16-key group (vt_col),
-//                          zero-padded to whole tiles; for bf16 caches also
-//                          the keys as f16 [kv_h][key][d].  bf16 values are
-//                          scaled by the power of two 2^-e that brings the
-//                          head's largest |V| into [2^14, 2^15), and each
-//                          bf16 key tile likewise by its own: exact for every
-//                          value within 2^29 of that maximum (f16's normal
-//                          range holds every 8-bit bf16 mantissa), whatever
-//                          the absolute range; the exponents go to vexp /
-//                          kexp.  f16 caches are f16 already.  A head whose
-//                          keys or values have a crest factor (max / rms)
-//                          above 8 is flagged (hflag) for the two-piece path.
+//   vtb_kvt_<dt>_d<D>      pre-pass, one workgroup per (64-key tile, KV
+//                          head) over the tiles some query attends: V^T as
+//                          f16, [kv_h][d][key], keys permuted inside each
+//                          16-key group (vt_col), zero-padded to whole tiles;
+//                          for bf16 caches also the keys as f16
+//                          [kv_h][key][d].  A bf16 key tile is scaled by the
+//                          power of two 2^-ek that brings its largest |k|
+//                          into [2^14, 2^15), a value tile by 2^-ev with ev
+//                          that exponent rounded up to a multiple of 4: exact
+//                          for every value within 2^25 of the tile's maximum
+//                          (f16's normal range holds every 8-bit bf16
+//                          mantissa), whatever the absolute range; (ek, ev)
+//                          go to texp.  f16 caches are f16 already.  Each
+//                          tile's statistics (largest |k|, sum of k^2,
+//                          largest key-row |k_t|^2, keys, largest |v|, sum
+//                          of v^2) go to tstat for the precision choice.
 //   vtb_prefill_d<D>       flash attention, transposed so that every lane
 //                          owns one query:
 //     q                    read as f32 (prefill.zig's s.q), scaled per wave
@@ -44,17 +43,22 @@
 //     O^T += V^T P^T       v_mfma_f32_32x32x16_f16; B = P^T straight from the
 //                          S^T accumulators (rounded to f16), A = V^T from LDS.
 //                          The pre-pass permutation makes the 8 keys a lane
-//                          holds in P^T 8 contiguous f16 of a V^T row.  The
-//                          value scale comes back out with the final 1/l.
+//                          holds in P^T 8 contiguous f16 of a V^T row.  O is
+//                          held in units of 2^E, E the value exponent of the
+//                          tiles accumulated (a tile with another one
+//                          rescales O first); 2^E comes back out with the
+//                          final 1/l.
 // P is rounded to f16 (11 significant bits; bf16's 8 bits would give ~2e-3
 // relative error, at the parity bar).
 //
-// Precision.  With 11-bit q and P the output error grows with the crest
-// factor of K (q's rounding error is weighted by |k|) and of V (P's rounding
-// error is weighted by |v - out|).  N(0,1) data (crest ~5) stays near 7e-4
-// of max|out|; channel outliers x20 (crest ~27) reach ~7e-3.  Flagged heads
-// therefore enter q and P as two f16 pieces each (hi + lo, 22 significant
-// bits): twice the MFMA work for those heads only, the error below 1e-4.
+// Precision.  With 11-bit q and P the output error grows with the score
+// magnitude (q's rounding error is weighted by |k|) and with the crest
+// factor of V (P's rounding error is weighted by |v - out|).  N(0,1) data
+// stays near 7e-4 of max|out|; channel outliers x20 (crest ~27) reach
+// ~7e-3 with one piece.  A work item whose key tiles allow large scores
+// therefore enters q as two f16 pieces (hi + lo, 22 significant bits), one
+// whose value tiles have a large crest factor P likewise (prefill_entry):
+// twice the QK or the PV products for those items only.
 //
 // Workgroup = 4 waves x 32 queries = 128 queries of one head; key tiles of BN
 // rows stream through LDS (K row-major, V^T row-major, both padded so the
@@ -97,19 +101,6 @@ __device__ inline void lane_halves(float v, float& lo_half, float& hi_half) {
 // ---------------------------------------------------------------- pre-pass
 // Power-of-two scaling: scale_exp / pow2f (common.h).
 
-// Largest |x| of the eight bf16 values of w, as bf16 magnitude bits.
-__device__ inline uint32_t bf16x8_absmax(u32x4 w) {
-  uint32_t m = 0;
-  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t lo = ww[i] & 0x7fffu, hi = (ww[i] >> 16) & 0x7fffu;
-    m = m > lo ? m : lo;
-    m = m > hi ? m : hi;
-  }
-  return m;
-}
-
 // Max over the 64 lanes of a wave (every lane gets it).
 __device__ inline float wave_max(float v) {
   v = fmaxf(v, dpp<DPP_XOR1>(v));
@@ -118,10 +109,6 @@ __device__ inline float wave_max(float v) {
   v = fmaxf(v, dpp<DPP_MIRROR>(v));
   v = xor_max<16>(v);
   return xor_max<32>(v);
-}
-__device__ inline uint32_t wave_max_u16(uint32_t m) {
-  // Magnitude bits in the high half of an f32 keep their order.
-  return __builtin_bit_cast(uint32_t, wave_max(__builtin_bit_cast(float, m << 16))) >> 16;
 }
 
 // |x| maximum over the eight 16-bit values of w; returns their sum of
@@ -139,153 +126,114 @@ __device__ inline float stat8(u32x4 w, float& mx) {
   return ss;
 }
 
-template <typename DT, int D>
-__device__ __forceinline__ void kvstat_body(const KvStatArgs& a) {
-  constexpr int CPR = D / 8;  // 16-byte chunks per row
-  constexpr int NB = 4;       // K and V load pairs in flight per thread
-  __shared__ float s_p[4][5];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int p = blockIdx.x, kvh = blockIdx.y;
-  const long long r0 = (long long)p * a.rows_per_part;
-  long long r1 = r0 + a.rows_per_part;
-  r1 = r1 < a.n_rows ? r1 : a.n_rows;
-  const long long n_chunks = r1 > r0 ? (r1 - r0) * CPR : 0;
-  const long long row_stride = (long long)a.n_kv * D;
-  const uint16_t* kg = (const uint16_t*)a.k + (long long)kvh * D;
-  const uint16_t* vg = (const uint16_t*)a.v + (long long)kvh * D;
-  float kmx = 0.0f, vmx = 0.0f, kss = 0.0f, vss = 0.0f, kn2 = 0.0f;
-  // Batches of NB independent load pairs per thread (ordinary, cached loads:
-  // the conversion pass reads the same rows next).  Chunks past the range
-  // load chunk 0 and are not counted.
-  for (long long c0 = tid; c0 < n_chunks; c0 += 256LL * NB) {
-    u32x4 kw[NB], vw[NB];
-#pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      const long long c = c0 + 256LL * i < n_chunks ? c0 + 256LL * i : 0;
-      const long long off = (r0 + c / CPR) * row_stride + (int)(c % CPR) * 8;
-      kw[i] = load16_cached(kg + off);
-      vw[i] = load16_cached(vg + off);
-    }
-#pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      // A row's CPR chunks sit in CPR consecutive lanes (256 and 64 are
-      // multiples of CPR), all in range or all out: its |k_t|^2 is their sum.
-      const bool in = c0 + 256LL * i < n_chunks;
-      float kc = stat8<DT>(kw[i], kmx), vc = stat8<DT>(vw[i], vmx);
-      kc = in ? kc : 0.0f;
-      vc = in ? vc : 0.0f;
-      kss += kc;
-      vss += vc;
-      kn2 = fmaxf(kn2, group_sum<CPR>(kc));
-    }
-  }
-  kmx = wave_max(kmx);
-  vmx = wave_max(vmx);
-  kss = group_sum<64>(kss);
-  vss = group_sum<64>(vss);
-  kn2 = wave_max(kn2);
-  if (lane == 0) {
-    s_p[wave][0] = kmx;
-    s_p[wave][1] = vmx;
-    s_p[wave][2] = kss;
-    s_p[wave][3] = vss;
-    s_p[wave][4] = kn2;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    f32x4 r = {0.0f, 0.0f, 0.0f, 0.0f}, r2 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      r[0] = fmaxf(r[0], s_p[i][0]);
-      r[1] = fmaxf(r[1], s_p[i][1]);
-      r[2] += s_p[i][2];
-      r[3] += s_p[i][3];
-      r2[0] = fmaxf(r2[0], s_p[i][4]);
-    }
-    float* dst = a.part + ((long long)kvh * gridDim.x + p) * 8;
-    *reinterpret_cast<f32x4*>(dst) = r;
-    *reinterpret_cast<f32x4*>(dst + 4) = r2;
-  }
+// Value exponent of a bf16 tile: scale_exp of its largest |v| rounded up to
+// a multiple of 4 (largest scaled magnitude in [2^11, 2^15)), so tiles of
+// similar range share it; kEvAny for an all-zero tile (any scale holds it).
+constexpr int kEvAny = -1000;
+__device__ inline int value_exp(float vmx) {
+  if (vmx == 0.0f) return kEvAny;
+  return ((scale_exp(vmx) + 3) >> 2) << 2;  // arithmetic shift: floor, so ceil to 4
 }
 
+// One pass per (64-key tile, KV head): statistics, exponents and the f16
+// operands of the tile.  Keys at or past n_rows are zero.
 template <typename DT, int D>
 __device__ __forceinline__ void kvt_body(const KvtArgs& a) {
   constexpr int TK = 64;                 // keys per workgroup
   constexpr int TP = D + 8;              // LDS pitch (16-bit elements)
+  constexpr int CPR = D / 8;             // 16-byte chunks per row
   constexpr int CH = TK * D / 8 / 256;   // 16-byte chunks per thread
   constexpr bool kBf = __is_same(DT, kv_bf16);
   static_assert(CH * 256 * 8 == TK * D, "tile does not match the workgroup");
   __shared__ __attribute__((aligned(16))) uint16_t tile[TK * TP];
-  __shared__ uint32_t s_km[4];
+  __shared__ float s_st[4][5];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int kvh = blockIdx.y;
-  const int tix = blockIdx.x;
+  const int tix = blockIdx.x + a.tile_lo;
+  const int n_tiles = a.vt_ld / TK;
   const long long key0 = (long long)tix * TK;
   const long long row_stride = (long long)a.n_kv * D;
   const uint16_t* vg = (const uint16_t*)a.v + (long long)kvh * D;
   const uint16_t* kg = (const uint16_t*)a.k + (long long)kvh * D;
-  // The head's statistics from the partials (every wave reduces them
-  // itself: at most 64, one per lane): the value scale (bf16), the
-  // precision flag (crest factor max / rms of V above 8) and the largest
-  // key-row norm.
-  float vscale = 1.0f;
-  {
-    f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f}, st2 = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (lane < a.n_part) {
-      st = *reinterpret_cast<const f32x4*>(a.part + ((long long)kvh * a.n_part + lane) * 8);
-      st2 = *reinterpret_cast<const f32x4*>(a.part + ((long long)kvh * a.n_part + lane) * 8 + 4);
-    }
-    const float vmx = wave_max(st[1]), vss = group_sum<64>(st[3]), kn2 = wave_max(st2[0]);
-    if constexpr (kBf) {
-      const int ev = scale_exp(vmx);
-      vscale = pow2f(-ev);
-      if (tix == 0 && tid == 0) a.vexp[kvh] = ev;
-    }
-    if (tix == 0 && tid == 0) {
-      // crest^2 = max^2 * count / sum v^2, in f64 (no overflow for any f32).
-      const double cnt = (double)a.n_rows * D;
-      a.hflag[kvh] = (double)vmx * vmx * cnt > 64.0 * (double)vss ? 1 : 0;
-      a.knorm[kvh] = sqrtf(kn2);
-    }
-  }
-  // 64 keys x D dims of V into LDS row-major as they are; for bf16 the same
-  // chunks of K, kept in registers until the tile's key exponent is known.
-  u32x4 kw[CH];
-  uint32_t kmx = 0;
+  // 64 keys x D dims of K and V, CH 16-byte chunks of each per thread
+  // (chunk c: key c / CPR, dims 8 (c % CPR) ..); a row's CPR chunks sit in
+  // CPR consecutive lanes.  V goes to LDS as it is for the transpose; K
+  // stays in registers until the tile's key exponent is known.
+  u32x4 kw[CH], vw[CH];
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int c = tid + 256 * i;
-    const int key = c / (D / 8), dc = (c % (D / 8)) * 8;
+    const int key = c / CPR, dc = (c % CPR) * 8;
     const bool in = key0 + key < a.n_rows;
-    u32x4 w = {0u, 0u, 0u, 0u};
-    if (in) w = load16(vg + (key0 + key) * row_stride + dc);
-    *reinterpret_cast<u32x4*>(&tile[key * TP + dc]) = w;
-    if constexpr (kBf) {
-      u32x4 kk = {0u, 0u, 0u, 0u};
-      if (in) kk = load16(kg + (key0 + key) * row_stride + dc);
-      kw[i] = kk;
-      const uint32_t m = bf16x8_absmax(kk);
-      kmx = kmx > m ? kmx : m;
-    }
+    const long long off = (key0 + key) * row_stride + dc;
+    kw[i] = in ? load16(kg + off) : u32x4{0u, 0u, 0u, 0u};
+    vw[i] = in ? load16(vg + off) : u32x4{0u, 0u, 0u, 0u};
   }
-  if constexpr (kBf) {
-    const uint32_t m = wave_max_u16(kmx);
-    if (lane == 0) s_km[wave] = m;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int c = tid + 256 * i;
+    *reinterpret_cast<u32x4*>(&tile[(c / CPR) * TP + (c % CPR) * 8]) = vw[i];
+  }
+  // Statistics: largest |k|, sum of k^2, largest |k_t|^2 of a key row,
+  // largest |v|, sum of v^2 (zero rows add nothing).
+  float kmx = 0.0f, kss = 0.0f, kn2 = 0.0f, vmx = 0.0f, vss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const float kc = stat8<DT>(kw[i], kmx);
+    kss += kc;
+    kn2 = fmaxf(kn2, group_sum<CPR>(kc));
+    vss += stat8<DT>(vw[i], vmx);
+  }
+  kmx = wave_max(kmx);
+  kn2 = wave_max(kn2);
+  vmx = wave_max(vmx);
+  kss = group_sum<64>(kss);
+  vss = group_sum<64>(vss);
+  if (lane == 0) {
+    s_st[wave][0] = kmx;
+    s_st[wave][1] = kss;
+    s_st[wave][2] = kn2;
+    s_st[wave][3] = vmx;
+    s_st[wave][4] = vss;
   }
   __syncthreads();
-  if constexpr (kBf) {
-    uint32_t km = 0;
+  // The tile's maxima, the same in every thread (the exponents must agree
+  // with what thread 0 records).
+  kmx = s_st[0][0];
+  vmx = s_st[0][3];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) km = km > s_km[i] ? km : s_km[i];
-    const int ek = scale_exp(__builtin_bit_cast(float, km << 16));
+  for (int w = 1; w < 4; ++w) {
+    kmx = fmaxf(kmx, s_st[w][0]);
+    vmx = fmaxf(vmx, s_st[w][3]);
+  }
+  if (tid == 0) {
+    f32x4 r0 = {s_st[0][0], s_st[0][1], s_st[0][2], 0.0f}, r1 = {s_st[0][3], s_st[0][4], 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      r0[0] = fmaxf(r0[0], s_st[w][0]);
+      r0[1] += s_st[w][1];
+      r0[2] = fmaxf(r0[2], s_st[w][2]);
+      r1[0] = fmaxf(r1[0], s_st[w][3]);
+      r1[1] += s_st[w][4];
+    }
+    const long long valid = a.n_rows - key0;
+    r0[3] = (float)(valid < TK ? valid : TK);
+    float* dst = a.tstat + ((long long)kvh * n_tiles + tix) * 8;
+    *reinterpret_cast<f32x4*>(dst) = r0;
+    *reinterpret_cast<f32x4*>(dst + 4) = r1;
+  }
+  float vscale = 1.0f;
+  if constexpr (kBf) {
+    const int ek = scale_exp(kmx), ev = value_exp(vmx);
+    vscale = pow2f(ev == kEvAny ? 0 : -ev);
     const float kscale = pow2f(-ek);
-    if (tid == 0) a.kexp[(long long)kvh * (a.vt_ld / TK) + tix] = ek;
+    if (tid == 0) *reinterpret_cast<int2*>(a.texp + ((long long)kvh * n_tiles + tix) * 2) = int2{ek, ev};
     // f16 keys [kv_h][key][d], scaled by 2^-ek.
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + 256 * i;
-      const int key = c / (D / 8), dc = (c % (D / 8)) * 8;
+      const int key = c / CPR, dc = (c % CPR) * 8;
       const uint32_t ww[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
       f16x8 h;
 #pragma unroll
@@ -314,8 +262,8 @@ __device__ __forceinline__ void kvt_body(const KvtArgs& a) {
 }
 
 // ---------------------------------------------------------------- attention
-// X2: q and P enter the MFMAs as two f16 pieces (hi + lo, 22 significant
-// bits), twice the products of the single-piece form.
+// XQ / XP: q / P enter their MFMAs as two f16 pieces (hi + lo, 22
+// significant bits), twice the products of the single-piece form.
 // The K and V^T tile stages of one workgroup: two of each, so tile j is read
 // from stage j%2 while tile j+1 is written into the other and one barrier
 // per tile suffices.  K rows are padded by one 16-byte chunk, V^T rows
@@ -416,17 +364,22 @@ struct TileDma {
 template <int D>
 constexpr bool kBalanced = D >= 256;
 
+// 2^e for an exponent difference e, clamped to pow2f's range: O rescaled by
+// more than 2^126 either way has left f32 anyway.
+__device__ inline float pow2_diff(int e) { return pow2f(e < -126 ? -126 : (e > 126 ? 126 : e)); }
+
 // A piece of a split query block (balanced launches): publish this
-// workgroup's unnormalised partial (o, m, l per thread) with coherent
-// stores and count it in; the second piece to arrive loads the first's and
-// merges them, always as piece 0's terms plus piece 1's, so the result does
-// not depend on the arrival order.  Returns true in the workgroup that then
-// writes the block's output.  Layout: part_o[slot][piece][j][thread] float4
-// (j < D/8: the thread's o, consecutive threads adjacent), part_ml[slot]
-// [piece][thread] (m, l); slot = head * nblk/2 + pair.
+// workgroup's unnormalised partial (o, m, l per thread, o in units of 2^E)
+// with coherent stores and count it in; the second piece to arrive loads
+// the first's and merges them, always as piece 0's terms plus piece 1's, so
+// the result does not depend on the arrival order.  Returns true in the
+// workgroup that then writes the block's output.  Layout: part_o[slot]
+// [piece][j][thread] float4 (j < D/8: the thread's o, consecutive threads
+// adjacent), part_ml[slot][piece][thread] float4 (m, l, E, 0); slot =
+// head * nblk/2 + pair.
 template <int D, int NW>
 __device__ __forceinline__ bool prefill_merge_pieces(const PrefillArgs& a, int h, int qb, int piece,
-                                                    f32x16 (&o)[D / 32], float& m_ref, float& l_run) {
+                                                    f32x16 (&o)[D / 32], float& m_ref, float& l_run, int& E) {
   constexpr int NT = 64 * NW, ND = D / 32, J = D / 8;
   __shared__ int s_last;
   const int tid = threadIdx.x;
@@ -441,8 +394,8 @@ __device__ __forceinline__ bool prefill_merge_pieces(const PrefillArgs& a, int h
       for (int q4 = 0; q4 < 4; ++q4)
         buffer_store_f4_coherent(rw, ((4 * dt + q4) * NT + tid) * 16,
                                  f32x4{o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]});
-    store_coherent(&a.part_ml[(mine * NT + tid) * 2 + 0], m_ref);
-    store_coherent(&a.part_ml[(mine * NT + tid) * 2 + 1], l_run);
+    const auto rm = buffer_rsrc(a.part_ml + mine * NT * 4, NT * 16);
+    buffer_store_f4_coherent(rm, tid * 16, f32x4{m_ref, l_run, (float)E, 0.0f});
   }
   wait_stores();
   __syncthreads();
@@ -456,12 +409,17 @@ __device__ __forceinline__ bool prefill_merge_pieces(const PrefillArgs& a, int h
   __syncthreads();
   if (!s_last) return false;
   const auto rr = buffer_rsrc(a.part_o + other * J * NT * 4, J * NT * 16);
-  const float mo = load_coherent(&a.part_ml[(other * NT + tid) * 2 + 0]);
-  const float lo = load_coherent(&a.part_ml[(other * NT + tid) * 2 + 1]);
+  const f32x4 mlo = buffer_load_f4_coherent(buffer_rsrc(a.part_ml + other * NT * 4, NT * 16), tid * 16);
+  const float mo = mlo[0], lo = mlo[1];
+  const int Eo = (int)mlo[2];
   const float M = fmaxf(m_ref, mo);
   const float fm = m_ref == -INFINITY ? 0.0f : exp2_fast(m_ref - M);
   const float fo = mo == -INFINITY ? 0.0f : exp2_fast(mo - M);
+  // o terms also move from their own value exponent to the larger one.
+  const int Em = E > Eo ? E : Eo;
+  const float gm = fm * pow2_diff(E - Em), go = fo * pow2_diff(Eo - Em);
   const float f0 = piece == 0 ? fm : fo, f1 = piece == 0 ? fo : fm;
+  const float g0 = piece == 0 ? gm : go, g1 = piece == 0 ? go : gm;
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) {
     f32x4 ov[4];
@@ -473,27 +431,28 @@ __device__ __forceinline__ bool prefill_merge_pieces(const PrefillArgs& a, int h
       for (int e = 0; e < 4; ++e) {
         const float mv = o[dt][4 * q4 + e], xv = ov[q4][e];
         const float v0 = piece == 0 ? mv : xv, v1 = piece == 0 ? xv : mv;
-        o[dt][4 * q4 + e] = v0 * f0 + v1 * f1;
+        o[dt][4 * q4 + e] = v0 * g0 + v1 * g1;
       }
   }
   const float l0v = piece == 0 ? l_run : lo, l1v = piece == 0 ? lo : l_run;
   l_run = l0v * f0 + l1v * f1;
   m_ref = M;
+  E = Em;
   return true;
 }
 
-// out[mq][h][d] = O^T[d][mq] / l.  The lane holds d = 32dt + 8(r/4) + 4hi +
-// (r%4): four consecutive dims per r/4, written as one 16-byte store.  The
-// row sum is split over the lane pair (hi = 0, 1); ev is the head's value
-// exponent.
+// out[mq][h][d] = O^T[d][mq] * 2^E / l.  The lane holds d = 32dt + 8(r/4) +
+// 4hi + (r%4): four consecutive dims per r/4, written as one 16-byte store.
+// The row sum is split over the lane pair (hi = 0, 1); E is the value
+// exponent O is held in.
 template <int D>
 __device__ __forceinline__ void prefill_write_out(const PrefillArgs& a, int h, int mq, int hi,
-                                                  const f32x16 (&o)[D / 32], float l_run, int ev) {
+                                                  const f32x16 (&o)[D / 32], float l_run, int E) {
   float l0, l1;
   lane_halves(l_run, l0, l1);
   const float l_tot = l0 + l1;
   if (mq < a.n_q) {
-    const float inv = (1.0f / l_tot) * pow2f(ev);
+    const float inv = (1.0f / l_tot) * pow2_diff(E);
     float* op = a.out + ((long long)mq * a.n_heads + h) * D + 4 * hi;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt) {
@@ -511,7 +470,7 @@ __device__ __forceinline__ void prefill_write_out(const PrefillArgs& a, int h, i
 // One work item: queries of block qb against keys [k_lo, k_hi) (intersected
 // with each query's causal and window range); piece < 0: the whole block
 // (write the output), else a piece of a split block (prefill_merge_pieces).
-template <int D, int NW, bool X2>
+template <int D, int NW, bool XQ, bool XP>
 __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, const int qb, const int kvh,
                                              const f16x8 (&qf)[D / 16], const f16x8 (&ql)[D / 16],
                                              const int eq, PrefillLds<D>& lds, const long long k_lo,
@@ -534,12 +493,12 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
 #define VTB_PF_VB 2
 #endif
   constexpr int KB = NS < VTB_PF_KB ? NS : VTB_PF_KB;  // S^T tiles per K-fragment batch
-  // O^T tiles per V-fragment batch (one in the two-piece form, whose second
-  // q and P pieces take the registers).
-  constexpr int VB = X2 ? 1 : (ND < VTB_PF_VB ? ND : VTB_PF_VB);
+  // O^T tiles per V-fragment batch (one in the two-piece forms, whose second
+  // q or P pieces take the registers).
+  constexpr int VB = (XQ || XP) ? 1 : (ND < VTB_PF_VB ? ND : VTB_PF_VB);
   static_assert(NS % KB == 0 && ND % VB == 0, "batches must divide the tiles");
-  // The register-tight case: the two-piece form of the 4-wave d128 kernel.
-  constexpr bool LATE = X2 && NW == 4 && D == 128;
+  // The register-tight case: two-piece q in the 4-wave d128 kernel.
+  constexpr bool LATE = XQ && NW == 4 && D == 128;
 
   static_assert(PrefillLds<D>::KBYTES == BN * KPB && PrefillLds<D>::VBYTES == D * VPB, "LDS stage size");
   lchar* const k_lds0 = lds.k0;
@@ -580,19 +539,22 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   };
 
   // Q^T fragments (B operand) from the entry: qf (and the second pieces ql,
-  // read only by the two-piece form), scaled by 2^-eq.
-  // The head's value exponent (null: 0) and the key-tile exponents of the
-  // pre-pass: a tile's score multiplier is scale_log2 * 2^(eq + ek), the
-  // exponent sum clamped so the product stays a normal f32 (beyond it every
-  // score is ~0 or overflows, as in f32).
-  const int ev = a.vexp ? a.vexp[kvh] : 0;
-  const int* kexp_h = a.kexp ? a.kexp + (long long)kvh * (a.vt_ld >> 6) : nullptr;
+  // read only by the two-piece q form), scaled by 2^-eq.
+  // The pre-pass's (key, value) exponents of each 64-key tile (null: f16
+  // cache, both 0): a tile's score multiplier is scale_log2 * 2^(eq + ek),
+  // the exponent sum clamped so the product stays a normal f32 (beyond it
+  // every score is ~0 or overflows, as in f32); its V^T is in units of 2^ev.
+  const int* texp_h = a.texp ? a.texp + (long long)kvh * (a.vt_ld >> 6) * 2 : nullptr;
 
   f32x16 o[ND];
 #pragma unroll
   for (int i = 0; i < ND; ++i) o[i] = f32x16{};
   float m_ref = -INFINITY;  // running reference max (log2 domain, scaled)
   float l_run = 0.0f;
+  // O is held in units of 2^E, E the value exponent of the last tile this
+  // wave accumulated (wave-uniform); a tile with another exponent first
+  // rescales O by a power of two (exact).
+  int E = 0;
   // The window as a 32-bit bound (positions stay below 2^30; a larger or
   // absent window keeps every causal key).
   const int wcap = (a.window > 0 && a.window < (1 << 30)) ? (int)a.window : (1 << 30);
@@ -605,12 +567,13 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   const int iwq_hi = __builtin_amdgcn_readfirstlane((int)wq_hi);
   const int iqpos = (int)qpos;
 
-  auto compute = [&](const lchar* kl, const lchar* vl, long long kt0, int ek) {
+  auto compute = [&](const lchar* kl, const lchar* vl, long long kt0, int ek, int evt) {
     // Skip tiles entirely above this wave's diagonal or before its windows.
     const int t0 = __builtin_amdgcn_readfirstlane((int)kt0);
     bool live = wave_live && t0 <= iwq_hi;
     if (iwin > 0 && t0 + BN - 1 < iwq_lo - iwin + 1) live = false;
     if (!live) return;
+    evt = evt == kEvAny ? E : evt;  // an all-zero tile fits any unit
     int es = eq + ek;
     es = es < -120 ? -120 : (es > 120 ? 120 : es);
     const float sl = a.scale_log2 * pow2f(es);
@@ -642,7 +605,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
 #pragma unroll
           for (int nb = 0; nb < KB; ++nb)
             s[n0 + nb] = mfma_qk(__builtin_bit_cast(f16x8, kf[ks][nb]), qf[k0 + ks], s[n0 + nb]);
-        if constexpr (X2) {
+        if constexpr (XQ) {
 #pragma unroll
           for (int ks = 0; ks < KSH; ++ks)
 #pragma unroll
@@ -692,20 +655,23 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
     }
 
     // Lazy rescale: raise the reference only if some row's max exceeds it by
-    // more than 8 (log2), keeping P <= 2^8.
+    // more than 8 (log2), keeping P <= 2^8.  A change of value exponent
+    // rescales O in the same multiply.
     const bool grow = mt > m_ref + 8.0f;
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+    if (__builtin_amdgcn_ballot_w64(grow) != 0 || evt != E) {
       // Rows that do not grow keep their reference (corr 1; also avoids
       // -inf - -inf for rows still fully masked); m_ref = -inf -> corr 0.
       const float corr = grow ? exp2_fast(m_ref - mt) : 1.0f;
       m_ref = grow ? mt : m_ref;
       l_run *= corr;
+      const float oc = corr * pow2_diff(E - evt);
+      E = evt;
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt) o[dt] *= corr;
+      for (int dt = 0; dt < ND; ++dt) o[dt] *= oc;
     }
     const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;  // row masked so far
 
-    f16x8 pf[PS], pl[X2 ? PS : 1];
+    f16x8 pf[PS], pl[XP ? PS : 1];
 #pragma unroll
     for (int nt = 0; nt < NS; ++nt) {
 #pragma unroll
@@ -713,7 +679,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
       {
         const float pv = exp2_fast(fmaf(s[nt][r], sl, -m_use));
         pf[2 * nt + (r >> 3)][r & 7] = (_Float16)pv;
-        if constexpr (X2) pl[2 * nt + (r >> 3)][r & 7] = (_Float16)(pv - (float)pf[2 * nt + (r >> 3)][r & 7]);
+        if constexpr (XP) pl[2 * nt + (r >> 3)][r & 7] = (_Float16)(pv - (float)pf[2 * nt + (r >> 3)][r & 7]);
       }
     }
     // Row sum over the f16-rounded P, the values the PV MFMAs consume:
@@ -727,7 +693,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
       for (int e = 0; e < 8; e += 2) {
         const h2 pr = {pf[i][e], pf[i][e + 1]};
         ls = __builtin_amdgcn_fdot2(pr, ones, ls, false);
-        if constexpr (X2) {
+        if constexpr (XP) {
           const h2 pr2 = {pl[i][e], pl[i][e + 1]};
           ls = __builtin_amdgcn_fdot2(pr2, ones, ls, false);
         }
@@ -752,7 +718,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
 #pragma unroll
         for (int db = 0; db < VB; ++db)
           o[d0 + db] = mfma_pv(__builtin_bit_cast(f16x8, vf[ks][db]), pf[ks], o[d0 + db]);
-      if constexpr (X2) {
+      if constexpr (XP) {
 #pragma unroll
         for (int ks = 0; ks < PS; ++ks)
 #pragma unroll
@@ -767,63 +733,76 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   // Key loop, two tiles per trip so each stage is a fixed LDS object.  Per
   // tile: barrier (the stage to read is complete; every wave is done with the
   // other stage), DMA of the next tile into the other stage, compute, wait
-  // for this wave's DMA.  The next tile's key exponent is read with its DMA,
+  // for this wave's DMA.  The next tile's exponents are read with its DMA,
   // as a vector load that the same wait covers: a scalar load would be
   // waited for together with the tile's LDS fragment reads (one counter).
-  // (Moved to a scalar register right after that wait, so no later
-  // instruction waits on it.)
-  auto kexp_of = [&](long long kt0) -> int { return kexp_h ? kexp_h[kt0 >> 6] : 0; };
-  int ek0 = 0, ek1 = 0;
+  // (Moved to scalar registers right after that wait, so no later
+  // instruction waits on them.)
+  auto texp_of = [&](long long kt0) -> int2 {
+    return texp_h ? *reinterpret_cast<const int2*>(texp_h + (kt0 >> 6) * 2) : int2{0, 0};
+  };
+  int2 x0 = {0, 0}, x1 = {0, 0};
   const int ikend = __builtin_amdgcn_readfirstlane((int)kend);
   const int ikt_first = __builtin_amdgcn_readfirstlane((int)kt_first);
   if (ikt_first < ikend) {
     fetch(kt_first, k_lds0, v_lds0);
-    ek0 = kexp_of(kt_first);
+    x0 = texp_of(kt_first);
     wait_loads();
-    ek0 = __builtin_amdgcn_readfirstlane(ek0);
+    x0.x = __builtin_amdgcn_readfirstlane(x0.x);
+    x0.y = __builtin_amdgcn_readfirstlane(x0.y);
+    E = x0.y == kEvAny ? 0 : x0.y;
   }
   for (int kt0 = ikt_first; kt0 < ikend; kt0 += 2 * BN) {
     __syncthreads();
     const bool more1 = kt0 + BN < ikend;
     if (more1) {
       fetch(kt0 + BN, k_lds1, v_lds1);
-      ek1 = kexp_of(kt0 + BN);
+      x1 = texp_of(kt0 + BN);
     }
-    compute(k_lds0, v_lds0, kt0, ek0);
+    compute(k_lds0, v_lds0, kt0, x0.x, x0.y);
     if (!more1) break;
     wait_loads();
-    ek1 = __builtin_amdgcn_readfirstlane(ek1);
+    x1.x = __builtin_amdgcn_readfirstlane(x1.x);
+    x1.y = __builtin_amdgcn_readfirstlane(x1.y);
     __syncthreads();
     const bool more2 = kt0 + 2 * BN < ikend;
     if (more2) {
       fetch(kt0 + 2 * BN, k_lds0, v_lds0);
-      ek0 = kexp_of(kt0 + 2 * BN);
+      x0 = texp_of(kt0 + 2 * BN);
     }
-    compute(k_lds1, v_lds1, kt0 + BN, ek1);
+    compute(k_lds1, v_lds1, kt0 + BN, x1.x, x1.y);
     if (!more2) break;
     wait_loads();
-    ek0 = __builtin_amdgcn_readfirstlane(ek0);
+    x0.x = __builtin_amdgcn_readfirstlane(x0.x);
+    x0.y = __builtin_amdgcn_readfirstlane(x0.y);
   }
 
   if constexpr (kBalanced<D>) {
-    if (piece >= 0 && !prefill_merge_pieces<D, NW>(a, h, qb, piece, o, m_ref, l_run)) return;
+    if (piece >= 0 && !prefill_merge_pieces<D, NW>(a, h, qb, piece, o, m_ref, l_run, E)) return;
   }
 
-  prefill_write_out<D>(a, h, mq, hi, o, l_run, ev);
+  prefill_write_out<D>(a, h, mq, hi, o, l_run, E);
 }
 
 // Entry: the workgroup's (head, query block), its queries in registers
-// (f32) and its precision path: two f16 pieces for q and P when the head is
-// flagged (values with a crest factor above 8) or when the Cauchy-Schwarz
-// bound on the workgroup's scores in log2 units, max |q| * max |k_t| *
-// scale_log2, exceeds 32 (then q's 11-bit rounding alone could move a score
-// by 2^-7).
+// (f32) and its precision path, from the pre-pass statistics of the key
+// tiles the work item reads:
+//   XQ  q as two f16 pieces when the Cauchy-Schwarz bound on the item's
+//       scores in log2 units, B = max |q| * max |k_t| * scale_log2, exceeds
+//       32: f16 rounding moves each q element by at most 2^-11 of itself, so
+//       a score by at most 2^-11 * B, which is 2^-6 at the threshold.
+//   XP  P as two f16 pieces when the item's values have a crest factor
+//       max |v| / rms(v) above 8: P's rounding error is weighted by
+//       |v - out|, so outlier values carry it into the output.
+// Keys of bf16 caches are exact in f16 (per-tile power-of-two scale), f16
+// keys are the cache itself; P's rounding enters the output through V only.
 template <int D, int NW>
 __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
   constexpr int KS = D / 16;
   constexpr int BM = 32 * NW;
   constexpr int BN = prefill_block_n(D);
-  __shared__ float s_qn[NW];
+  constexpr int NT = 64 * NW;
+  __shared__ float s_red[NW][5];
   __shared__ __attribute__((aligned(16))) char s_k0[PrefillLds<D>::KBYTES];
   __shared__ __attribute__((aligned(16))) char s_k1[PrefillLds<D>::KBYTES];
   __shared__ __attribute__((aligned(16))) char s_v0[PrefillLds<D>::VBYTES];
@@ -924,28 +903,75 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
           }
     }
     // |q|^2 of the lane's row (the lane pair hi = 0, 1 holds it), max over
-    // the workgroup.
+    // the workgroup; the item's key tiles (the body's key range, in 64-key
+    // pre-pass tiles): largest |k_t|^2, keys, largest |v|, sum of v^2.
     float n2lo, n2hi;
     lane_halves(n2, n2lo, n2hi);
     const float wn2 = wave_max(n2lo + n2hi);
-    if (lane == 0) s_qn[wave] = wn2;
+    const int m0 = qb * BM;
+    const int m_last = (m0 + BM < a.n_q ? m0 + BM : a.n_q) - 1;
+    long long kend = a.pos0 + m_last + 1;
+    if (k_hi < kend) kend = k_hi;
+    long long kbeg = k_lo;
+    const long long q_lo = a.pos0 + m0;
+    if (a.window > 0 && q_lo >= a.window && q_lo - a.window + 1 > kbeg) kbeg = q_lo - a.window + 1;
+    float kn2 = 0.0f, vmx = 0.0f, vss = 0.0f, cnt = 0.0f;
+    {
+      const float* ts = a.tstat + (long long)kvh * (a.vt_ld >> 6) * 8;
+      for (long long t = (kbeg >> 6) + tid; t < ((kend + 63) >> 6); t += NT) {
+        const f32x4 r0 = *reinterpret_cast<const f32x4*>(ts + t * 8);
+        const f32x4 r1 = *reinterpret_cast<const f32x4*>(ts + t * 8 + 4);
+        kn2 = fmaxf(kn2, r0[2]);
+        cnt += r0[3];
+        vmx = fmaxf(vmx, r1[0]);
+        vss += r1[1];
+      }
+    }
+    kn2 = wave_max(kn2);
+    vmx = wave_max(vmx);
+    cnt = group_sum<64>(cnt);
+    vss = group_sum<64>(vss);
+    if (lane == 0) {
+      s_red[wave][0] = wn2;
+      s_red[wave][1] = kn2;
+      s_red[wave][2] = vmx;
+      s_red[wave][3] = vss;
+      s_red[wave][4] = cnt;
+    }
     __syncthreads();
-    float qn2 = s_qn[0];
+    float qn2 = s_red[0][0];
+    kn2 = s_red[0][1];
+    vmx = s_red[0][2];
+    vss = s_red[0][3];
+    cnt = s_red[0][4];
 #pragma unroll
-    for (int ww = 1; ww < NW; ++ww) qn2 = fmaxf(qn2, s_qn[ww]);
-    const bool x2 = (a.hflag && a.hflag[kvh] != 0) ||
-                    (a.knorm && sqrtf(qn2) * a.knorm[kvh] * a.scale_log2 > 32.0f);
-    if (x2)
-      prefill_body<D, NW, true>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece);
+    for (int ww = 1; ww < NW; ++ww) {
+      qn2 = fmaxf(qn2, s_red[ww][0]);
+      kn2 = fmaxf(kn2, s_red[ww][1]);
+      vmx = fmaxf(vmx, s_red[ww][2]);
+      vss += s_red[ww][3];
+      cnt += s_red[ww][4];
+    }
+    const bool xq = sqrtf(qn2) * sqrtf(kn2) * a.scale_log2 > 32.0f;
+    // crest^2 = max^2 * count / sum v^2 > 64, in f64 (no overflow for any f32).
+    const bool xp = (double)vmx * vmx * ((double)cnt * D) > 64.0 * (double)vss;
+    // Three compiled forms: both flags (also for xp alone, rare: values
+    // with outliers), q alone, neither.  A fourth body inlined into the
+    // kernel made the register allocator spill VGPRs in the d128 and d256
+    // kernels.
+    if (xp)
+      prefill_body<D, NW, true, true>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece);
+    else if (xq)
+      prefill_body<D, NW, true, false>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece);
     else
-      prefill_body<D, NW, false>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece);
+      prefill_body<D, NW, false, false>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece);
   }
 }
 
 }  // namespace vtb
 
 // The attention kernels are the same for both cache dtypes (f16 operands);
-// the statistics and conversion passes are per dtype.
+// the pre-pass is per dtype.
 #define VTB_PREFILL(D)                                                                     \
   extern "C" __global__ __launch_bounds__(256, vtb::prefill_waves_per_simd(D))             \
   void vtb_prefill_d##D(vtb::PrefillArgs a) {                                              \
@@ -954,9 +980,6 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
 #define VTB_KVT(DTN, DTT, D)                                                               \
   extern "C" __global__ __launch_bounds__(256) void vtb_kvt_##DTN##_d##D(vtb::KvtArgs a) { \
     vtb::kvt_body<vtb::DTT, D>(a);                                                         \
-  }                                                                                        \
-  extern "C" __global__ __launch_bounds__(256) void vtb_kvstat_##DTN##_d##D(vtb::KvStatArgs a) { \
-    vtb::kvstat_body<vtb::DTT, D>(a);                                                      \
   }
 
 VTB_PREFILL(64)

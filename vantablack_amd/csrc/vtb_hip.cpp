@@ -33,7 +33,6 @@ using vtb::PrefillArgs;
 using vtb::QGemmArgs;
 using vtb::RmsNormArgs;
 using vtb::RopeRowsArgs;
-using vtb::KvStatArgs;
 using vtb::KvtArgs;
 using vtb::XSplitArgs;
 
@@ -85,8 +84,7 @@ struct VtbHipCtx {
   hipFunction_t f_decodeh[kNumKv][kNumD][2] = {};  // vtb_decodeh_<kv>_d<D>_g<1|2>: head-group form
   hipFunction_t f_decode_merge = nullptr;            // vtb_decode_merge: the split merge as its own launch
   hipFunction_t f_prefill[kNumD] = {};
-  hipFunction_t f_kvt[kNumKv][kNumD] = {};  // conversion pass per cache dtype (f16, bf16)
-  hipFunction_t f_kvstat[kNumKv][kNumD] = {};  // statistics pass per cache dtype
+  hipFunction_t f_kvt[kNumKv][kNumD] = {};  // pre-pass per cache dtype (f16, bf16)
   hipFunction_t f_append[kNumKv] = {};
   hipFunction_t f_copy = nullptr;
   hipFunction_t f_fill = nullptr;
@@ -106,7 +104,7 @@ struct VtbHipCtx {
   // Used only by the no-allocation decode entry; null if unavailable.
   unsigned char* dscratch = nullptr;
   // Prefill scratch written by the vtb_kvt_* pre-pass: f16 V^T, f16 keys
-  // (bf16 caches) and the per-tile multipliers.
+  // (bf16 caches), the per-tile statistics and exponents.
   void* pf = nullptr;
   size_t pf_bytes = 0;
   // Batched-matmul activation scratch: three bf16 planes [3][Bp][k] and the
@@ -444,34 +442,33 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
 }
 
 // Prefill scratch layout for keys [0, vt_ld) of n_kv heads: f16 V^T
-// [n_kv][D][vt_ld], the statistics partials [n_kv][64][8], the precision
-// flags [n_kv] and the key-row norms [n_kv], then (bf16 caches) f16 keys [n_kv][vt_ld][D], the key-tile
-// exponents [n_kv][vt_ld / 64] and the value exponents [n_kv]; sections
-// 256-byte aligned.
-constexpr int kPrefillMaxParts = 64;
+// [n_kv][D][vt_ld], the tile statistics [n_kv][vt_ld / 64][8] f32, then
+// (bf16 caches) f16 keys [n_kv][vt_ld][D] and the tile exponents
+// [n_kv][vt_ld / 64][2] int, then (balanced launches) the split-block
+// partials; sections 256-byte aligned.
 struct PrefillScratch {
-  size_t vt = 0, part = 0, hflag = 0, knorm = 0, k16 = 0, kexp = 0, vexp = 0, bal_o = 0, bal_ml = 0, bytes = 0;
+  size_t vt = 0, tstat = 0, k16 = 0, texp = 0, bal_o = 0, bal_ml = 0, bytes = 0;
 };
 // Balanced launches (4-wave kernel): split-block partials for n_heads heads
-// of nblk query blocks, threads per workgroup nt.
+// of nblk query blocks, threads per workgroup nt: o (head_dim / 2 floats per
+// thread and piece) and (m, l, E, 0).
 size_t prefill_balance_floats(size_t n_heads, size_t nblk, size_t head_dim, size_t nt) {
   return n_heads * nblk * nt * (head_dim / 2);
 }
+size_t prefill_balance_ml_floats(size_t n_heads, size_t nblk, size_t nt) { return n_heads * nblk * nt * 4; }
 PrefillScratch prefill_scratch(size_t n_kv, size_t head_dim, long long vt_ld, int dtype, size_t bal_floats = 0,
                                size_t bal_ml_floats = 0) {
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   PrefillScratch p;
   const size_t plane = n_kv * head_dim * (size_t)vt_ld * 2;
+  const size_t n_tiles = (size_t)(vt_ld / 64);
   p.vt = 0;
-  p.part = up(plane);
-  p.hflag = p.part + up(n_kv * kPrefillMaxParts * 8 * sizeof(float));
-  p.knorm = p.hflag + up(n_kv * sizeof(int));
-  p.bytes = p.knorm + up(n_kv * sizeof(float));
+  p.tstat = up(plane);
+  p.bytes = p.tstat + up(n_kv * n_tiles * 8 * sizeof(float));
   if (dtype == VTB_HIP_BF16) {
     p.k16 = p.bytes;
-    p.kexp = p.k16 + up(plane);
-    p.vexp = p.kexp + up(n_kv * (size_t)(vt_ld / 64) * sizeof(int));
-    p.bytes = p.vexp + up(n_kv * sizeof(int));
+    p.texp = p.k16 + up(plane);
+    p.bytes = p.texp + up(n_kv * n_tiles * 2 * sizeof(int));
   }
   if (bal_floats) {
     p.bal_o = p.bytes;
@@ -495,9 +492,9 @@ int ensure_scratch(VtbHipCtx* ctx, void** buf, size_t* have, size_t need, const 
 }
 
 // MFMA prefill: q is f32 (prefill.zig's s.q); k/v the layer base of an f16
-// or bf16 cache.  A statistics pass and a conversion pass (V^T, the
-// precision flags and, for bf16, the scaled f16 keys) over keys
-// [0, pos0 + n_q), then the attention.
+// or bf16 cache.  One pre-pass (V^T, tile statistics and, for bf16, the
+// scaled f16 keys and tile exponents) over the 64-key tiles from the window
+// start of the first query to pos0 + n_q, then the attention.
 int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* k, const void* v,
                         size_t n_q, size_t n_heads, size_t n_kv, size_t head_dim, long long pos0,
                         long long window, float inv_sqrt_hd, int dtype) {
@@ -505,7 +502,7 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
   if (di < 0) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "head_dim must be 64, 128 or 256");
   if (dtype != VTB_HIP_F16 && dtype != VTB_HIP_BF16)
     return set_err(ctx, VTB_HIP_EINVAL, "MFMA prefill needs an f16 or bf16 cache");
-  if (!ctx->f_prefill[di] || !ctx->f_kvt[dtype][di] || !ctx->f_kvstat[dtype][di])
+  if (!ctx->f_prefill[di] || !ctx->f_kvt[dtype][di])
     return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prefill kernel not built for this shape");
   if (!aligned16(k) || !aligned16(v) || !aligned16(q))
     return set_err(ctx, VTB_HIP_EINVAL, "q/K/V not 16-byte aligned");
@@ -520,8 +517,11 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
   const bool balance = env_flag("VTB_PREFILL_BALANCE", true) && head_dim >= 256 && nblk >= 2 &&
                        nblk % 2 == 0 && (window <= 0 || window >= pos0 + (long long)n_q);
   const size_t nt = 256;
-  // Pre-pass over keys [0, pos0 + n_q), padded to whole 64-key tiles.
+  // Pre-pass over keys [0, pos0 + n_q), padded to whole 64-key tiles, from
+  // the tile of the first query's window start on (no query reads earlier
+  // keys).
   const long long n_rows = pos0 + (long long)n_q;
+  const long long key_lo = window > 0 && pos0 >= window ? pos0 - window + 1 : 0;
   const long long bn = vtb::prefill_block_n((int)head_dim);
   const long long vt_ld = (n_rows + 63) / 64 * 64;  // multiple of the pre-pass tile and of bn
   // The kernels compare positions in 32-bit arithmetic, and their tile DMA
@@ -531,7 +531,7 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
     return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prompt too long");
   const PrefillScratch ps =
       prefill_scratch(n_kv, head_dim, vt_ld, dtype, balance ? prefill_balance_floats(n_heads, nblk, head_dim, nt) : 0,
-                      balance ? n_heads * nblk * nt * 2 : 0);
+                      balance ? prefill_balance_ml_floats(n_heads, nblk, nt) : 0);
   int rc = ensure_scratch(ctx, &ctx->pf, &ctx->pf_bytes, ps.bytes, "hipMalloc(prefill scratch)");
   if (rc) return rc;
   if (balance) {
@@ -545,33 +545,16 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
   ka.k = k;
   ka.v = v;
   ka.vt = base + ps.vt;
+  ka.tstat = (float*)(base + ps.tstat);
+  if (bf) {
+    ka.k16 = base + ps.k16;
+    ka.texp = (int*)(base + ps.texp);
+  }
   ka.n_rows = (int)n_rows;
   ka.n_kv = (int)n_kv;
   ka.vt_ld = (int)vt_ld;
-  // Statistics pass: about one workgroup per CU over all heads, at most 64
-  // partitions per head.
-  long long n_part = (std::max(ctx->cu_count, 1) + (long long)n_kv - 1) / (long long)n_kv;
-  n_part = std::min<long long>(std::min<long long>(n_part, kPrefillMaxParts), n_rows);
-  KvStatArgs sa;
-  memset(&sa, 0, sizeof sa);
-  sa.k = k;
-  sa.v = v;
-  sa.part = (float*)(base + ps.part);
-  sa.n_rows = (int)n_rows;
-  sa.n_kv = (int)n_kv;
-  sa.rows_per_part = (int)((n_rows + n_part - 1) / n_part);
-  rc = launch(ctx, ctx->f_kvstat[dtype][di], (unsigned)n_part, (unsigned)n_kv, 1, 256, &sa);
-  if (rc) return rc;
-  ka.part = sa.part;
-  ka.hflag = (int*)(base + ps.hflag);
-  ka.knorm = (float*)(base + ps.knorm);
-  ka.n_part = (int)n_part;
-  if (bf) {
-    ka.k16 = base + ps.k16;
-    ka.kexp = (int*)(base + ps.kexp);
-    ka.vexp = (int*)(base + ps.vexp);
-  }
-  rc = launch(ctx, ctx->f_kvt[dtype][di], (unsigned)(vt_ld / 64), (unsigned)n_kv, 1, 256, &ka);
+  ka.tile_lo = (int)(key_lo / 64);
+  rc = launch(ctx, ctx->f_kvt[dtype][di], (unsigned)(vt_ld / 64 - ka.tile_lo), (unsigned)n_kv, 1, 256, &ka);
   if (rc) return rc;
 
   PrefillArgs a;
@@ -587,10 +570,8 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
     a.k_head_stride = (long long)head_dim;
   }
   a.vt = ka.vt;
-  a.kexp = ka.kexp;
-  a.vexp = ka.vexp;
-  a.hflag = ka.hflag;
-  a.knorm = ka.knorm;
+  a.texp = ka.texp;
+  a.tstat = ka.tstat;
   a.vt_ld = (int)vt_ld;
   a.out = out;
   a.n_q = (int)n_q;
@@ -880,9 +861,6 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
         snprintf(name, sizeof name, "vtb_kvt_%s_d%d", kKvNames[kv], D);
         if (hipModuleGetFunction(&ctx->f_kvt[kv][di], ctx->mod_prefill, name) != hipSuccess)
           ctx->f_kvt[kv][di] = nullptr;  // shape not built: reported at launch
-        snprintf(name, sizeof name, "vtb_kvstat_%s_d%d", kKvNames[kv], D);
-        if (hipModuleGetFunction(&ctx->f_kvstat[kv][di], ctx->mod_prefill, name) != hipSuccess)
-          ctx->f_kvstat[kv][di] = nullptr;
       }
       if (kv == 0) {
         snprintf(name, sizeof name, "vtb_prefill_d%d", D);
@@ -1722,7 +1700,7 @@ extern "C" int vtb_hip_reserve(VtbHipCtx* ctx, const VtbHipAttnConfig* cfg, int 
     const size_t nblk4 = (max_batch + bm4 - 1) / bm4 + 1;
     rc = ensure_scratch(ctx, &ctx->pf, &ctx->pf_bytes,
                         prefill_scratch(n_kv, D, vt_ld, kv_dtype, bal ? prefill_balance_floats(n_heads, nblk4, D, 256) : 0,
-                                        bal ? n_heads * nblk4 * 256 * 2 : 0)
+                                        bal ? prefill_balance_ml_floats(n_heads, nblk4, 256) : 0)
                             .bytes,
                         "hipMalloc(prefill scratch)");
     if (rc) return rc;
