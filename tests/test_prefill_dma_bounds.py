@@ -123,6 +123,41 @@ def test_launcher_limits_keep_offsets_32_bit(d, n_kv):
         assert bn * krow < 2 ** 32
 
 
+def test_stage_arrays_and_lds_pointers():
+    # The four stage arrays are separate __shared__ objects of exactly the
+    # modelled sizes (so a write inside a stage is inside the workgroup's
+    # allocation; test_code_objects checks that allocation holds them), and
+    # every DMA destination is an LDS-address-space pointer derived from
+    # them: M0 comes from a local (32-bit LDS) address, never from a generic
+    # pointer converted at run time.
+    import os
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    src = open(os.path.join(root, "vantablack_amd", "csrc", "kernels", "prefill.hip")).read()
+    for decl in ("__shared__ __attribute__((aligned(16))) char s_k0[PrefillLds<D>::KBYTES];",
+                 "__shared__ __attribute__((aligned(16))) char s_k1[PrefillLds<D>::KBYTES];",
+                 "__shared__ __attribute__((aligned(16))) char s_v0[PrefillLds<D>::VBYTES];",
+                 "__shared__ __attribute__((aligned(16))) char s_v1[PrefillLds<D>::VBYTES];",
+                 "PrefillLds<D> lds{(lchar*)s_k0, (lchar*)s_k1, (lchar*)s_v0, (lchar*)s_v1};",
+                 "static constexpr int KBYTES = BN * (D / 8 + 1) * 16;",
+                 "static constexpr int VBYTES = D * (BN / 8 + 1) * 16;",
+                 "typedef __attribute__((address_space(3))) char lchar;"):
+        assert decl in src, decl
+    for d in (64, 128, 256):
+        m = tile_dma_model(d)
+        assert m["ksl"] * 16 == m["bn"] * (d // 8 + 1) * 16  # KBYTES
+        assert m["vsl"] * 16 == d * (m["bn"] // 8 + 1) * 16  # VBYTES
+    # Every buffer-to-LDS DMA in the kernels takes an address_space(3)
+    # destination built from an lchar / dchar stage pointer.
+    import re
+    for name in ("prefill.hip", "decode.hip"):
+        text = open(os.path.join(root, "vantablack_amd", "csrc", "kernels", name)).read()
+        calls = [m.start() for m in re.finditer(r"__builtin_amdgcn_raw_ptr_buffer_load_lds\(", text)]
+        assert calls, name
+        for c in calls:
+            args = text[c:text.index(";", c)]
+            assert "address_space(3)" in args, (name, args)
+
+
 def test_model_constants_match_the_sources():
     import os
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))

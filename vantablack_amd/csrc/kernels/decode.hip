@@ -1035,7 +1035,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a) {
 
 template <typename KV, int D, int G, int HG = 1>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
-  if constexpr (decode_uses_mfma(KV::bytes, G))
+  if constexpr (decode_uses_mfma(KV::bytes, D, G))
     decode_mfma_body<KV, D, G, decode_waves(KV::bytes, D, G)>(a);
   else
     decode_scalar_body<KV, D, G, decode_nit(G), decode_waves(KV::bytes, D, G), HG>(a);

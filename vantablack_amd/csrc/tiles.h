@@ -28,8 +28,12 @@ constexpr int decode_nit(int g) {
 // the G query-key dot products of each 16-key block on
 // v_mfma_f32_16x16x32_{bf16,f16} (queries as three exact pieces) and P.V on
 // v_mfma_f32_16x16x16_{bf16,f16}, with K and V staged in LDS by DMA (two
-// 16-key stages per wave).
-constexpr bool decode_uses_mfma(int kv_bytes, int g) { return kv_bytes == 2 && g >= 4; }
+// 16-key stages per wave).  Not for groups of 9-16 at head_dim 256: that
+// body needs more than the 512 registers a wave can hold (the compiler
+// spilled 600 of them to scratch), so those shapes take the scalar form.
+constexpr bool decode_uses_mfma(int kv_bytes, int head_dim, int g) {
+  return kv_bytes == 2 && g >= 4 && !(g >= 16 && head_dim >= 256);
+}
 
 // Waves per decode workgroup.  Scalar form: for g = 1 one wave per SIMD
 // streams best: 16-wave workgroups keep 4x the loads in flight per CU and
@@ -54,7 +58,7 @@ constexpr int decode_mfma_waves(int head_dim, int g) {
   return (head_dim >= 256 ? VTB_DECODE_MFMA_WAVES_D256 : VTB_DECODE_MFMA_WAVES) / (g >= 16 ? 2 : 1);
 }
 constexpr int decode_waves(int kv_bytes, int head_dim, int g) {
-  return decode_uses_mfma(kv_bytes, g) ? decode_mfma_waves(head_dim, g)
+  return decode_uses_mfma(kv_bytes, head_dim, g) ? decode_mfma_waves(head_dim, g)
          : g == 1                      ? VTB_DECODE_WAVES1
          : g <= 4                      ? VTB_DECODE_WAVES4
                                        : (g == 8 ? VTB_DECODE_WAVES8 : 4);
@@ -93,7 +97,7 @@ constexpr unsigned long long decode_scratch_counter_bytes = 256ull << 10;
 // Rows per split are a multiple of this: the rows one wave load instruction
 // covers (scalar form) or one 16-key MFMA block.
 constexpr int decode_split_quantum(int head_dim, int kv_bytes, int g, int hg = 1) {
-  return decode_uses_mfma(kv_bytes, g) ? 16 : 64 / (head_dim * kv_bytes / 16 * hg);
+  return decode_uses_mfma(kv_bytes, head_dim, g) ? 16 : 64 / (head_dim * kv_bytes / 16 * hg);
 }
 
 // Prefill (MFMA): 4 waves x 32 queries per workgroup; keys per LDS tile by

@@ -312,7 +312,7 @@ void decode_bound(VtbHipCtx* ctx, size_t n_q, size_t units, size_t head_dim, lon
 // with groups of 1 or 2 on the scalar path whose KV-head count it divides;
 // VTB_DECODE_HG=1 forces one head per workgroup.
 int decode_heads_per_wg(size_t n_heads, size_t n_kv, size_t head_dim, int dtype, int G) {
-  if (vtb::decode_uses_mfma(kKvBytes[dtype], G) || G > 2 || n_heads != n_kv * (size_t)G) return 1;
+  if (vtb::decode_uses_mfma(kKvBytes[dtype], (int)head_dim, G) || G > 2 || n_heads != n_kv * (size_t)G) return 1;
   const int hg = vtb::decode_head_group(kKvBytes[dtype], (int)head_dim);
   if (hg <= 1 || n_kv % (size_t)hg != 0) return 1;
   const char* e = getenv("VTB_DECODE_HG");
@@ -364,7 +364,7 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
   }
   // The MFMA form's tile DMA addresses 16 rows of one KV head with 32-bit
   // offsets.
-  if (vtb::decode_uses_mfma(kKvBytes[dtype], G) && (long long)(n_kv * head_dim) * 2 * 16 >= (1LL << 31))
+  if (vtb::decode_uses_mfma(kKvBytes[dtype], (int)head_dim, G) && (long long)(n_kv * head_dim) * 2 * 16 >= (1LL << 31))
     return set_err(ctx, VTB_HIP_EUNSUPPORTED, "KV row too wide");
   const int HG = decode_heads_per_wg(n_heads, n_kv, head_dim, dtype, G);
   DecodePlan pl;
