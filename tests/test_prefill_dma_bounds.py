@@ -123,6 +123,49 @@ def test_launcher_limits_keep_offsets_32_bit(d, n_kv):
         assert bn * krow < 2 ** 32
 
 
+def _k_tile_accesses(m, krow, kend, kt0, pad_chunk, clamp):
+    """Memory bytes [lo, hi) relative to the key allocation's start that the K
+    DMA of the tile at kt0 touches, for an addressing variant: the pad slot
+    reads chunk 0 of its row (pad_chunk 0, the current kernel) or another
+    chunk (KCH: one chunk past the row's D elements); the descriptor covers
+    the rows before kend (clamp, the current kernel) or all BN rows of the
+    tile.  Accesses the range check drops (offset + 16 > num_records) touch
+    nothing."""
+    rows = min(kend - kt0, m["bn"]) if clamp else m["bn"]
+    num_records = rows * krow
+    ch_per_row = m["kch"] + 1
+    res = []
+    for _, _, _, s, row, _ in dma_lanes(m, "k"):
+        ch = s % ch_per_row
+        off = row * krow + 16 * (pad_chunk if ch == m["kch"] else ch)
+        if off + 16 <= num_records:
+            res.append((kt0 * krow + off, kt0 * krow + off + 16))
+    return res
+
+
+@pytest.mark.parametrize("pad_chunk,clamp,inside", [
+    (0, True, True),     # the current kernel: pad slots read chunk 0, descriptor ends at kend
+    ("KCH", True, True),  # pad slots one chunk past the row: range-checked (or inside the allocation)
+    (0, False, False),   # descriptor over all BN rows: reads rows past kend, outside a kend-row buffer
+])
+def test_addressing_variants_on_a_48_key_buffer(pad_chunk, clamp, inside):
+    # The 48-token d128 case that faulted an earlier direct-to-LDS version,
+    # with K read in place from an f16 cache holding exactly 48 rows of one KV
+    # head (krow = 2 D bytes): which addressing variants touch memory outside
+    # the allocation [0, 48 krow)?  The pad-slot offset alone cannot (the
+    # range check drops whatever passes the descriptor); a descriptor that is
+    # not clamped to the existing keys does.
+    d, n_rows = 128, 48
+    m = tile_dma_model(d)
+    krow = 2 * d
+    pc = m["kch"] if pad_chunk == "KCH" else pad_chunk
+    acc = []
+    for kt0 in range(0, n_rows, m["bn"]):
+        acc += _k_tile_accesses(m, krow, n_rows, kt0, pc, clamp)
+    outside = [a for a in acc if a[0] < 0 or a[1] > n_rows * krow]
+    assert (not outside) == inside, outside[:4]
+
+
 def test_stage_arrays_and_lds_pointers():
     # The four stage arrays are separate __shared__ objects of exactly the
     # modelled sizes (so a write inside a stage is inside the workgroup's

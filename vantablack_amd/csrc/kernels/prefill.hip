@@ -467,14 +467,45 @@ __device__ __forceinline__ void prefill_write_out(const PrefillArgs& a, int h, i
   }
 }
 
+// A work item's keys: [kbeg, kend) = [k_lo, k_hi) intersected with the keys
+// some query of block qb may attend (its causal end, its first query's
+// window start).
+template <int BM>
+__device__ __forceinline__ void item_keys(const PrefillArgs& a, int qb, long long k_lo, long long k_hi,
+                                          long long& kbeg, long long& kend) {
+  const int m0 = qb * BM;
+  const int m_last = (m0 + BM < a.n_q ? m0 + BM : a.n_q) - 1;
+  kend = a.pos0 + m_last + 1;
+  if (k_hi < kend) kend = k_hi;
+  kbeg = k_lo;
+  const long long q_lo = a.pos0 + m0;
+  if (a.window > 0 && q_lo >= a.window && q_lo - a.window + 1 > kbeg) kbeg = q_lo - a.window + 1;
+}
+
+// A KV head's f16 key rows and V^T rows, as the tile DMA reads them.
+struct TileSrc {
+  const char* kbase;
+  const char* vbase;
+  long long krow_bytes;
+  int vrow_bytes;
+};
+template <int D>
+__device__ __forceinline__ TileSrc tile_src(const PrefillArgs& a, int kvh) {
+  return TileSrc{(const char*)((const _Float16*)a.k + (long long)kvh * a.k_head_stride),
+                 (const char*)((const _Float16*)a.vt + (long long)kvh * D * a.vt_ld), a.k_row_stride * 2,
+                 a.vt_ld * 2};
+}
+
 // One work item: queries of block qb against keys [k_lo, k_hi) (intersected
 // with each query's causal and window range); piece < 0: the whole block
 // (write the output), else a piece of a split block (prefill_merge_pieces).
+// The entry has issued the DMA of the item's first key tile into stage 0
+// and the load of that tile's exponents (x_first).
 template <int D, int NW, bool XQ, bool XP>
 __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, const int qb, const int kvh,
                                              const f16x8 (&qf)[D / 16], const f16x8 (&ql)[D / 16],
                                              const int eq, PrefillLds<D>& lds, const long long k_lo,
-                                             const long long k_hi, const int piece) {
+                                             const long long k_hi, const int piece, const int2 x_first) {
   constexpr int NT = 64 * NW;                 // threads per workgroup
   constexpr int BM = 32 * NW;                 // queries per workgroup (NW waves x 32)
   constexpr int BN = prefill_block_n(D);      // keys per tile
@@ -516,11 +547,8 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   const int mq = m0 + wave * 32 + lc;  // this lane's query (may be >= n_q: padding)
   const long long qpos = a.pos0 + mq;
   const long long q_lo = a.pos0 + m0;  // first query position of the workgroup
-  const int m_last = (m0 + BM < a.n_q ? m0 + BM : a.n_q) - 1;
-  long long kend = a.pos0 + m_last + 1;  // keys [.., kend) may be attended
-  if (k_hi < kend) kend = k_hi;
-  long long kbeg = k_lo;
-  if (a.window > 0 && q_lo >= a.window && q_lo - a.window + 1 > kbeg) kbeg = q_lo - a.window + 1;
+  long long kbeg, kend;  // keys [kbeg, kend) may be attended
+  item_keys<BM>(a, qb, k_lo, k_hi, kbeg, kend);
   const long long kt_first = kbeg / BN * BN;
 
   // Wave-level query range, for tile skipping.
@@ -528,10 +556,11 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   const long long wq_hi = a.pos0 + (m0 + wave * 32 + 31 < a.n_q ? m0 + wave * 32 + 31 : a.n_q - 1);
   const bool wave_live = m0 + wave * 32 < a.n_q;
 
-  const char* kbase = (const char*)((const _Float16*)a.k + (long long)kvh * a.k_head_stride);
-  const char* vbase = (const char*)((const _Float16*)a.vt + (long long)kvh * D * a.vt_ld);
-  const long long krow_bytes = a.k_row_stride * 2;
-  const int vrow_bytes = a.vt_ld * 2;
+  const TileSrc src = tile_src<D>(a, kvh);
+  const char* const kbase = src.kbase;
+  const char* const vbase = src.vbase;
+  const long long krow_bytes = src.krow_bytes;
+  const int vrow_bytes = src.vrow_bytes;
   const TileDma<D, NW> dma(wave, lane, (int)krow_bytes, vrow_bytes);
   auto fetch = [&](long long kt0, lchar* kl, lchar* vl) {
     dma.issue_k(kbase, krow_bytes, kend, kt0, kl);
@@ -745,8 +774,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   const int ikend = __builtin_amdgcn_readfirstlane((int)kend);
   const int ikt_first = __builtin_amdgcn_readfirstlane((int)kt_first);
   if (ikt_first < ikend) {
-    fetch(kt_first, k_lds0, v_lds0);
-    x0 = texp_of(kt_first);
+    x0 = x_first;
     wait_loads();
     x0.x = __builtin_amdgcn_readfirstlane(x0.x);
     x0.y = __builtin_amdgcn_readfirstlane(x0.y);
@@ -860,6 +888,23 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
     const int piece = it == 0 ? pc0 : -1;
     const long long k_lo = it == 0 ? lo0 : 0, k_hi = it == 0 ? hi0 : (1LL << 62);
     if (it > 0) __syncthreads();  // the previous item's LDS reads are done
+    // The item's keys; the DMA of its first key tile into stage 0 goes out
+    // before the q and statistics loads, so the three latencies overlap
+    // (the body waits for the tile).
+    long long kbeg, kend;
+    item_keys<BM>(a, qb, k_lo, k_hi, kbeg, kend);
+    int2 x_first = {0, 0};  // the first tile's (key, value) exponents
+    {
+      const long long kt_first = kbeg / BN * BN;
+      if (kt_first < kend) {
+        const TileSrc src = tile_src<D>(a, kvh);
+        const TileDma<D, NW> dma(wave, lane, (int)src.krow_bytes, src.vrow_bytes);
+        dma.issue_k(src.kbase, src.krow_bytes, kend, kt_first, lds.k0);
+        dma.issue_v(src.vbase, src.vrow_bytes, kt_first, lds.v0);
+        if (a.texp)
+          x_first = *reinterpret_cast<const int2*>(a.texp + ((long long)kvh * (a.vt_ld >> 6) + (kt_first >> 6)) * 2);
+      }
+    }
     const int mq = qb * 32 * NW + wave * 32 + lc;
     const int mr = mq < a.n_q ? mq : a.n_q - 1;  // padding lanes reuse the last query
     const float* qp = a.q + ((long long)mr * a.n_heads + h) * D + 8 * hi;
@@ -872,13 +917,23 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
     f16x8 qf[KS], ql[KS];
     int eq;
     float n2 = 0.0f;  // |q|^2 of the lane's half row
-    {
-      f32x4 qv[KS][2];
+    f32x4 qv[KS][2];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        qv[ks][0] = *reinterpret_cast<const f32x4*>(qp + 16 * ks);
-        qv[ks][1] = *reinterpret_cast<const f32x4*>(qp + 16 * ks + 4);
-      }
+    for (int ks = 0; ks < KS; ++ks) {
+      qv[ks][0] = *reinterpret_cast<const f32x4*>(qp + 16 * ks);
+      qv[ks][1] = *reinterpret_cast<const f32x4*>(qp + 16 * ks + 4);
+    }
+    // The statistics of the item's key tiles (64-key pre-pass tiles; one
+    // per thread, the rest, beyond 64 * NT keys, in a loop): largest
+    // |k_t|^2, keys, largest |v|, sum of v^2.
+    const float* ts = a.tstat + (long long)kvh * (a.vt_ld >> 6) * 8;
+    const long long t_lo = kbeg >> 6, t_hi = (kend + 63) >> 6;
+    f32x4 r0 = {0.0f, 0.0f, 0.0f, 0.0f}, r1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (t_lo + tid < t_hi) {
+      r0 = *reinterpret_cast<const f32x4*>(ts + (t_lo + tid) * 8);
+      r1 = *reinterpret_cast<const f32x4*>(ts + (t_lo + tid) * 8 + 4);
+    }
+    {
       float mx = 0.0f;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
@@ -903,29 +958,18 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
           }
     }
     // |q|^2 of the lane's row (the lane pair hi = 0, 1 holds it), max over
-    // the workgroup; the item's key tiles (the body's key range, in 64-key
-    // pre-pass tiles): largest |k_t|^2, keys, largest |v|, sum of v^2.
+    // the workgroup, with the tile statistics.
     float n2lo, n2hi;
     lane_halves(n2, n2lo, n2hi);
     const float wn2 = wave_max(n2lo + n2hi);
-    const int m0 = qb * BM;
-    const int m_last = (m0 + BM < a.n_q ? m0 + BM : a.n_q) - 1;
-    long long kend = a.pos0 + m_last + 1;
-    if (k_hi < kend) kend = k_hi;
-    long long kbeg = k_lo;
-    const long long q_lo = a.pos0 + m0;
-    if (a.window > 0 && q_lo >= a.window && q_lo - a.window + 1 > kbeg) kbeg = q_lo - a.window + 1;
-    float kn2 = 0.0f, vmx = 0.0f, vss = 0.0f, cnt = 0.0f;
-    {
-      const float* ts = a.tstat + (long long)kvh * (a.vt_ld >> 6) * 8;
-      for (long long t = (kbeg >> 6) + tid; t < ((kend + 63) >> 6); t += NT) {
-        const f32x4 r0 = *reinterpret_cast<const f32x4*>(ts + t * 8);
-        const f32x4 r1 = *reinterpret_cast<const f32x4*>(ts + t * 8 + 4);
-        kn2 = fmaxf(kn2, r0[2]);
-        cnt += r0[3];
-        vmx = fmaxf(vmx, r1[0]);
-        vss += r1[1];
-      }
+    float kn2 = r0[2], cnt = r0[3], vmx = r1[0], vss = r1[1];
+    for (long long t = t_lo + tid + NT; t < t_hi; t += NT) {
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(ts + t * 8);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(ts + t * 8 + 4);
+      kn2 = fmaxf(kn2, x0[2]);
+      cnt += x0[3];
+      vmx = fmaxf(vmx, x1[0]);
+      vss += x1[1];
     }
     kn2 = wave_max(kn2);
     vmx = wave_max(vmx);
@@ -960,11 +1004,11 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
     // kernel made the register allocator spill VGPRs in the d128 and d256
     // kernels.
     if (xp)
-      prefill_body<D, NW, true, true>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece);
+      prefill_body<D, NW, true, true>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece, x_first);
     else if (xq)
-      prefill_body<D, NW, true, false>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece);
+      prefill_body<D, NW, true, false>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece, x_first);
     else
-      prefill_body<D, NW, false, false>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece);
+      prefill_body<D, NW, false, false>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece, x_first);
   }
 }
 
