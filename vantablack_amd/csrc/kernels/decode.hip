@@ -16,17 +16,18 @@
 //     elements is spread over LPR = D*bytes/16 lanes, one 16-byte load per
 //     lane; scores are reduced across the LPR lanes with DPP adds and
 //     permlane swaps (no LDS);
-//   - MFMA (f16/bf16 caches, GQA groups of 4..16): the G dot products of a
-//     16-key block are v_mfma_f32_16x16x32_{bf16,f16} products of the keys,
-//     loaded straight into operand layout (a lane holds 8 contiguous
-//     elements of one key), with the queries as three pieces of the cache's
+//   - MFMA (f16/bf16 caches, GQA groups of 4..16; 4..8 at head_dim 256):
+//     K and V are staged in LDS by DMA (two 16-key stages per wave); the G
+//     dot products of a 16-key block are v_mfma_f32_16x16x32_{bf16,f16}
+//     products of the keys with the queries as three pieces of the cache's
 //     16-bit type (q*2^-e = p0 + p1 + p2 exactly, one power of two e per
-//     query), so every product is exact and sums are f32.  Softmax and P.V
-//     stay f32 on the VALU, V in the scalar form's row layout; P crosses
-//     from the score layout to the V layout through the wave's LDS.
-//   Loads are double-buffered in registers: the next tile's loads are issued
-//   before this tile's math.  The softmax is online (running max m, sum l,
-//   accumulator acc) per wave, in registers.
+//     query), so every product is exact and sums are f32; P.V is
+//     v_mfma_f32_16x16x16_{bf16,f16} with P as 16-bit pieces and V read from
+//     LDS with the transposing ds_read_b64_tr_b16 (details at the MFMA form
+//     below).
+//   Scalar form: loads are double-buffered in registers (the next tile's
+//   loads are issued before this tile's math).  The softmax is online
+//   (running max m, sum l, accumulator) per wave.
 //   The waves combine into one (m, l, o) partial per workgroup through
 //   per-wave LDS slots summed in a fixed order.  The last-arriving
 //   workgroup of each (query, KV head) merges the partials: it loads every
@@ -36,9 +37,14 @@
 //   the arrival counter to zero, so no memset is needed between launches.
 //   Partials travel through agent-coherent stores/loads and a relaxed
 //   counter; no device-wide fence (L2 writeback/invalidate) is executed.
+//   A single query with more splits than one workgroup merges flat instead
+//   publishes its partials only, and a second launch (vtb_decode_merge)
+//   merges every column in parallel.
 //
 // Numerics: scores and P.V are f32 on exactly-upcast K/V (MFMA form: exact
-// products of the query pieces and the 16-bit keys, f32 sums).  The
+// products of the query pieces and the 16-bit keys, f32 sums; P enters P.V
+// as 16-bit pieces, exact for groups of 4 and 16 (bf16) or 22 (f16)
+// significant bits for groups of 8-16).  The
 // 1/sqrt(D) scale is folded with log2(e) into q once, and exp is evaluated
 // as exp2.
 //
