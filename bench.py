@@ -888,8 +888,8 @@ def pmc_workload():
     """The launches of every measured kernel shape, for rocprofv3 --pmc runs:
     the calibration copy (vtb_copy_f32); the fused append + decode launch of
     C2 (vtb_decodeh_f16_d128_g1), C3 (vtb_decode_bf16_d128_g4) and C5
-    (vtb_decode_bf16_d256_g8), each over PMC_DECODE's layer count of distinct
-    cache layers; and the C4 (8192 tokens) and C5 (4096 tokens) causal
+    (vtb_decode_bf16_d256_g8, with its merge launch vtb_decode_merge), each
+    over PMC_DECODE's layer count of distinct cache layers; and the C4 (8192 tokens) and C5 (4096 tokens) causal
     prefill calls: the pre-pass (vtb_kvt_*: tile statistics and the f16
     operands) and the attention kernels (vtb_prefill_d128,
     vtb_prefill_d256)."""
@@ -1094,13 +1094,17 @@ def mfma_busy_field(e):
                       "GRBM_GUI_ACTIVE / 8 XCDs (at_clock) or duration x 2.4 GHz (at_2p4ghz); C4 8192 tokens"}
 
 
-def decode_counter_field(kname, tr, e):
-    """HBM traffic and VALU figures of one decode kernel from profiles/."""
+def decode_counter_field(kname, tr, e, merge_tr=None):
+    """HBM traffic and VALU figures of one decode kernel from profiles/;
+    merge_tr: the traffic of its merge launch (vtb_decode_merge), when the
+    config takes one, added to the decode launch's."""
     if not tr and not e:
         return None
     out = {"kernel": kname}
     if tr:
-        out["traffic_bytes"] = tr["traffic_bytes"]
+        out["traffic_bytes"] = tr["traffic_bytes"] + (merge_tr["traffic_bytes"] if merge_tr else 0)
+        if merge_tr:
+            out["traffic_bytes_merge_launch"] = merge_tr["traffic_bytes"]
     if e:
         out.update({"valu_busy_at_2p4ghz": e.get("valu_busy_at_peak_clock"),
                     "valu_insts_per_wave": e.get("valu_insts_per_wave"), "waves": e.get("waves"),
@@ -1207,10 +1211,13 @@ def main():
         },
     }
     if dec_more:
-        for cfg, kname in (("C3", decode_kernel_name(32, 8, 128, "bf16")),
-                           ("C5", decode_kernel_name(8, 1, 256, "bf16"))):
+        # C5 (one query, 256 splits) merges in a second launch (vtb_decode_merge), the
+        # only config of the counter workload that takes one.
+        for cfg, kname, merge in (("C3", decode_kernel_name(32, 8, 128, "bf16"), None),
+                                  ("C5", decode_kernel_name(8, 1, 256, "bf16"), "vtb_decode_merge")):
             if cfg in dec_more:
-                dec_more[cfg]["counters"] = decode_counter_field(kname, traffic.get(kname), counters.get(kname))
+                dec_more[cfg]["counters"] = decode_counter_field(kname, traffic.get(kname), counters.get(kname),
+                                                                 traffic.get(merge) if merge else None)
         line["decode_other_configs"] = dec_more
     if gemv:
         line["quant_gemv"] = {

@@ -337,7 +337,9 @@ struct TileDma {
 #pragma unroll
     for (int i = 0; i < KPW; ++i) {
       const int blk = wave + NW * i;
-      if (blk < KBL && (KSL % 64 == 0 || 64 * blk + lane < KSL))
+      // Rounds in which every wave has a block need no wave check (a
+      // compile-time fact the compiler cannot see from wave < NW).
+      if (((i + 1) * NW <= KBL || blk < KBL) && (KSL % 64 == 0 || 64 * blk + lane < KSL))
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, reinterpret_cast<__attribute__((address_space(3))) void*>(kl + 1024 * blk), 16,
                                                  koff[i], 0, 0, 0);
     }
@@ -349,7 +351,7 @@ struct TileDma {
 #pragma unroll
     for (int i = 0; i < VPW; ++i) {
       const int blk = wave + NW * i;
-      if (blk < VBL && (VSL % 64 == 0 || 64 * blk + lane < VSL))
+      if (((i + 1) * NW <= VBL || blk < VBL) && (VSL % 64 == 0 || 64 * blk + lane < VSL))
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, reinterpret_cast<__attribute__((address_space(3))) void*>(vl + 1024 * blk), 16,
                                                  voff[i], 0, 0, 0);
     }
