@@ -102,8 +102,11 @@ struct PrefillArgs {
   unsigned* part_ctr;        // [n_heads][nblk / 2] x 32 arrival counters, zero between launches
 };
 // PrefillArgs::flags.  kPrefillBalance: paired key ranges (prefill_entry;
-// d256, nblk even).
+// d256, nblk even).  kPrefillPairOrder: the grid fits two workgroups per
+// CU at once, so the second half of the dispatch order takes the query
+// blocks complementary to the first half's (prefill_entry).
 constexpr int kPrefillBalance = 1;
+constexpr int kPrefillPairOrder = 2;
 static_assert(sizeof(PrefillArgs) == 128 && offsetof(PrefillArgs, flags) == 100 &&
                   offsetof(PrefillArgs, part_o) == 104 && offsetof(PrefillArgs, part_ctr) == 120,
               "PrefillArgs layout");

@@ -846,14 +846,22 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
     // with GQA these share KV heads, so each XCD's L2 holds fewer K/V tiles
     // -- and every XCD takes its longest (last) query blocks first.
     const int i = blockIdx.y * gridDim.x + blockIdx.x;
+    int rank;  // position of the workgroup's query block in dispatch order
     if (a.n_heads % 8 == 0) {
       const int hpx = a.n_heads / 8, j = i / 8;
       h = (i % 8) * hpx + j % hpx;
-      w = nblk - 1 - j / hpx;
+      rank = j / hpx;
     } else {
       h = blockIdx.x;
-      w = nblk - 1 - (int)blockIdx.y;
+      rank = blockIdx.y;
     }
+    // Longest blocks first.  With kPrefillPairOrder (the whole grid is
+    // resident at once, two workgroups per CU, nblk even) the second half
+    // of the order runs the blocks in increasing length instead: rank r <
+    // nblk/2 takes block nblk-1-r and rank r + nblk/2 block r, so when the
+    // second round of workgroups fills the CUs in the first round's order,
+    // every CU holds two blocks of nblk+1 blocks' keys in total.
+    w = ((a.flags & kPrefillPairOrder) && rank >= nblk / 2) ? rank - nblk / 2 : nblk - 1 - rank;
   }
   // Work items.  Plain launches: block w, all its keys.  Balanced launches
   // (a.balance, nblk even): causal blocks b = p and c = nblk - 1 - p pair up

@@ -580,6 +580,13 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
   a.pos0 = pos0;
   a.window = window;
   a.scale_log2 = inv_sqrt_hd * 1.4426950408889634f;
+  // One round of workgroups, two per CU (d <= 128: 72 KB of LDS each): the
+  // pair order evens each CU's causal load.  VTB_PREFILL_PAIR_ORDER=0 turns
+  // it off.
+  if (!balance && head_dim <= 128 && nblk % 2 == 0 && (long long)(n_heads * nblk) > (long long)ctx->cu_count &&
+      (long long)(n_heads * nblk) <= 2LL * ctx->cu_count && (window <= 0 || window >= pos0 + (long long)n_q) &&
+      env_flag("VTB_PREFILL_PAIR_ORDER", true))
+    a.flags |= vtb::kPrefillPairOrder;
   if (balance) {
     a.flags |= vtb::kPrefillBalance;
     a.part_o = (float*)(base + ps.bal_o);
