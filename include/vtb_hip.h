@@ -71,6 +71,18 @@ void *vtb_hip_stream(VtbHipCtx *ctx);
 const char *vtb_hip_last_error(VtbHipCtx *ctx);
 /* Number of compute units of the bound device (0 on error). */
 int vtb_hip_cu_count(VtbHipCtx *ctx);
+/* No reference counterpart (introspection of a gfx950 launch property).
+ * Number of XCDs the workgroups of a launch are dealt over round-robin, as
+ * vtb_hip_init measured it (0: the dealing did not check out, or
+ * VTB_DECODE_XCD_LOCAL=0).  When nonzero, single-query decode launches whose
+ * units divide evenly over the XCDs run every split of a unit on one XCD
+ * and hand the split partials over through that XCD's L2. */
+int vtb_hip_xcd_map(VtbHipCtx *ctx);
+/* The check vtb_hip_init applies to the XCC ids xcc[0..n) of the workgroups
+ * of one launch: nx when workgroup i runs on the XCD of workgroup i mod nx
+ * and workgroups 0..nx-1 on nx different XCDs (n >= 2 nx), else 0.  Host
+ * logic only; no device access. */
+int vtb_hip_xcd_deal(const int *xcc, int n);
 
 /* ---- buffers: replaces vtb_metal_alloc / vtb_metal_wrap / vtb_metal_release
  * (bridge.h:27-39).  Device memory, no host pointer. */

@@ -36,7 +36,13 @@ struct DecodeArgs {
   const float* rope_inv_freq;  // optional: [D/2] 1/base^(2j/D); RoPE of q and
   long long rope_pos;          //   k_new at absolute position rope_pos is
   int rope_half;               //   fused when set (half form if rope_half)
-  int pad2;
+  // XCD-local split merge (one query, in-kernel merge): the number of XCDs
+  // nx the launch's workgroups are dealt over round-robin, 0 when off.
+  // Workgroup i then serves unit (i % nx) * (units / nx) + (i / nx) /
+  // n_splits, split (i / nx) % n_splits, so every split of a unit runs on
+  // one XCD and its partials travel through that XCD's L2 (sc0 stores and
+  // loads) instead of through to memory (sc1).
+  int xcd_map;
 };
 static_assert(sizeof(DecodeArgs) == 152, "DecodeArgs layout");
 static_assert(offsetof(DecodeArgs, n_heads) == 72 && offsetof(DecodeArgs, pos0) == 88 &&

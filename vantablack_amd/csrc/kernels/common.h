@@ -240,6 +240,33 @@ __device__ inline void buffer_store_f4_coherent(__amdgpu_buffer_rsrc_t r, int of
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kBufSc1);
 }
 
+// Split-merge hand-off, XL = true when writer and reader run on one XCD
+// and so share its L2: stores stay in the L2 (sc0, group scope; the L2
+// acknowledges them) and loads skip only the L1 (sc0).  XL = false: the
+// agent-coherent (sc1) forms above, through to memory.  The arrival counter
+// atomic is the same in both (atomics are performed past the L2s).
+constexpr int kBufSc0 = 1;
+template <bool XL>
+__device__ inline f32x4 part_load_f4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, XL ? kBufSc0 : kBufSc1));
+}
+template <bool XL>
+__device__ inline void part_store_f4(__amdgpu_buffer_rsrc_t r, int off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, XL ? kBufSc0 : kBufSc1);
+}
+template <bool XL>
+__device__ inline void part_load8(__amdgpu_buffer_rsrc_t r, int off, float& x, float& y) {
+  x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, XL ? kBufSc0 : kBufSc1));
+  y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 4, 0, XL ? kBufSc0 : kBufSc1));
+}
+template <bool XL>
+__device__ inline void part_store(float* p, float v) {
+  if constexpr (XL)
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  else
+    store_coherent(p, v);
+}
+
 // Wait for all of this wave's vector-memory loads, including buffer->LDS
 // transfers (their LDS writes have landed when vmcnt reaches zero).
 __device__ inline void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }

@@ -37,6 +37,9 @@
 //   the arrival counter to zero, so no memset is needed between launches.
 //   Partials travel through agent-coherent stores/loads and a relaxed
 //   counter; no device-wide fence (L2 writeback/invalidate) is executed.
+//   With the XCD-local map (DecodeArgs::xcd_map) every split of a unit runs
+//   on one XCD and the partials stay in that XCD's L2 (sc0 stores and
+//   loads).
 //   A single query with more splits than one workgroup merges flat instead
 //   publishes its partials only, and a second launch (vtb_decode_merge)
 //   merges every column in parallel.
@@ -99,6 +102,15 @@ __device__ inline bool decode_unit(const DecodeArgs& a, DecodeUnit& u) {
   u.split = blockIdx.x;
   u.kvh = blockIdx.y;
   u.b = blockIdx.z;
+  if (a.xcd_map > 0) {
+    // XCD-local merge (one query; units a multiple of nx, checked by the
+    // host): workgroups i = nx * k + x of one XCD x serve whole units.
+    const int nx = a.xcd_map;
+    const int i = blockIdx.x + gridDim.x * blockIdx.y;
+    const int x = i % nx, k = i / nx;
+    u.kvh = x * ((int)gridDim.y / nx) + k / (int)gridDim.x;
+    u.split = k % (int)gridDim.x;
+  }
   const long long qpos = a.pos0 + u.b;
   const long long wstart = (a.window <= 0 || qpos < a.window) ? 0 : qpos - a.window + 1;
   const long long L = qpos + 1 - wstart;
@@ -176,7 +188,7 @@ struct MergeShape {
 //   block through LDS, in a fixed order.  Slots past `count` load at an
 //   offset past the buffer's range: zeros, no memory access, no branch.
 //   Every sum has a fixed order, so results are bit-reproducible.
-template <int G, int D, int NT, int MAXS>
+template <int G, int D, int NT, int MAXS, bool XL>
 __device__ __forceinline__ void decode_merge(const DecodeArgs& a, const DecodeUnit& u, const float* src_o,
                                              const float* src_ml, long long first, int count, bool to_out,
                                              float* dst_o, float* dst_ml, float* sh_w, float* sh_ml,
@@ -206,7 +218,7 @@ __device__ __forceinline__ void decode_merge(const DecodeArgs& a, const DecodeUn
 #pragma unroll
     for (int i = 0; i < SPL; ++i) {
       const int s = p + MP * i;
-      ov[c][i] = buffer_load_f4_coherent(ro, s < count ? (s * MC + col) * 16 : (int)bytes_o);
+      ov[c][i] = part_load_f4<XL>(ro, s < count ? (s * MC + col) * 16 : (int)bytes_o);
     }
   }
   // (m, l) of slot s of query g in lane s of half-wave g (loop only when
@@ -215,7 +227,7 @@ __device__ __forceinline__ void decode_merge(const DecodeArgs& a, const DecodeUn
     const int t = t0 + tid;
     const int g = t >> 5, s = t & 31;
     float m, l;
-    buffer_load8_coherent(rm, (s < count ? s * G + g : count * G) * 8, m, l);
+    part_load8<XL>(rm, (s < count ? s * G + g : count * G) * 8, m, l);
     m = s < count ? m : -INFINITY;
     const float M = group_max<32>(m);
     const float Ms = M == -INFINITY ? 0.0f : M;
@@ -274,10 +286,10 @@ __device__ __forceinline__ void decode_merge(const DecodeArgs& a, const DecodeUn
       op[3] = O[c].w / L;
     } else {
       const auto rw = buffer_rsrc(dst_o, G * D * 4);
-      buffer_store_f4_coherent(rw, col * 16, O[c]);
+      part_store_f4<XL>(rw, col * 16, O[c]);
       if (d4 == 0) {
-        store_coherent(&dst_ml[g * 2 + 0], M);
-        store_coherent(&dst_ml[g * 2 + 1], L);
+        part_store<XL>(&dst_ml[g * 2 + 0], M);
+        part_store<XL>(&dst_ml[g * 2 + 1], L);
       }
     }
   }
@@ -310,6 +322,7 @@ __device__ __forceinline__ void decode_finish(const DecodeArgs& a, const DecodeU
   __shared__ f32x4 sh_red[WPB > 1 ? WPB * MC : 1];
   __shared__ int s_last;
   const bool single = (u.n_act == 1);
+  const bool xl = kDecodeXclSlots(G * D) && a.xcd_map > 0;  // XCD-local hand-off (wave-uniform)
   const long long units = gridDim.y;  // (query, KV head or head group) units per query
   const long long ub = (long long)u.b * units + u.kvh;
   const long long part = ub * a.n_splits + u.split;
@@ -344,11 +357,22 @@ __device__ __forceinline__ void decode_finish(const DecodeArgs& a, const DecodeU
     } else {
       // Agent-scope (sc1) stores are coherent across the XCDs' L2s, so the
       // partials need no cache-wide writeback (a __threadfence() here costs
-      // a full L2 writeback + invalidate per workgroup on this chip).
-      buffer_store_f4_coherent(rw, (g * D + d4 * 4) * 4, O);
-      if (d4 == 0) {
-        store_coherent(&ml_unit[((long long)u.split * G + g) * 2 + 0], M);
-        store_coherent(&ml_unit[((long long)u.split * G + g) * 2 + 1], L);
+      // a full L2 writeback + invalidate per workgroup on this chip).  With
+      // the XCD-local map the unit's merger shares this workgroup's L2, and
+      // the partials stay in it (sc0).
+      float* mlp = &ml_unit[((long long)u.split * G + g) * 2];
+      if (xl) {
+        part_store_f4<true>(rw, (g * D + d4 * 4) * 4, O);
+        if (d4 == 0) {
+          part_store<true>(mlp, M);
+          part_store<true>(mlp + 1, L);
+        }
+      } else {
+        part_store_f4<false>(rw, (g * D + d4 * 4) * 4, O);
+        if (d4 == 0) {
+          part_store<false>(mlp, M);
+          part_store<false>(mlp + 1, L);
+        }
       }
     }
   }
@@ -377,21 +401,34 @@ __device__ __forceinline__ void decode_finish(const DecodeArgs& a, const DecodeU
 
   if (!arrive(ctr0 + (long long)grp * decode_counter_stride, members)) return;
   const float* o_unit = a.ws_o + ub * a.n_splits * G * D;
-  if (!two_level) {
-    // Up to 16 splits the merge issues loads for 16 slots only (slots past
-    // the count still pass through the load pipeline).
-    if (FLAT > GS && u.n_act <= GS)
-      decode_merge<G, D, NT, GS>(a, u, o_unit, ml_unit, 0, u.n_act, true, nullptr, nullptr, sh_w, sh_ml, sh_red);
-    else
-      decode_merge<G, D, NT, FLAT>(a, u, o_unit, ml_unit, 0, u.n_act, true, nullptr, nullptr, sh_w, sh_ml, sh_red);
-    return;
+  auto merge_all = [&](auto xl_tag) {
+    constexpr bool XL = decltype(xl_tag)::value != 0;
+    if (!two_level) {
+      // Up to 16 splits the merge issues loads for 16 slots only (slots past
+      // the count still pass through the load pipeline).
+      if (FLAT > GS && u.n_act <= GS)
+        decode_merge<G, D, NT, GS, XL>(a, u, o_unit, ml_unit, 0, u.n_act, true, nullptr, nullptr, sh_w, sh_ml,
+                                       sh_red);
+      else
+        decode_merge<G, D, NT, FLAT, XL>(a, u, o_unit, ml_unit, 0, u.n_act, true, nullptr, nullptr, sh_w, sh_ml,
+                                         sh_red);
+      return;
+    }
+    float* go_unit = a.wg_o + ub * n_groups * G * D;
+    float* gml_unit = a.wg_ml + ub * n_groups * G * 2;
+    decode_merge<G, D, NT, GS, XL>(a, u, o_unit, ml_unit, (long long)grp * GS, members, false,
+                                   go_unit + (long long)grp * G * D, gml_unit + (long long)grp * G * 2, sh_w, sh_ml,
+                                   sh_red);
+    if (!arrive(ctr0 + (long long)n_groups * decode_counter_stride, n_grp)) return;
+    decode_merge<G, D, NT, GS, XL>(a, u, go_unit, gml_unit, 0, n_grp, true, nullptr, nullptr, sh_w, sh_ml, sh_red);
+  };
+  if constexpr (kDecodeXclSlots(G * D)) {
+    if (xl) {
+      merge_all(ic<1>{});
+      return;
+    }
   }
-  float* go_unit = a.wg_o + ub * n_groups * G * D;
-  float* gml_unit = a.wg_ml + ub * n_groups * G * 2;
-  decode_merge<G, D, NT, GS>(a, u, o_unit, ml_unit, (long long)grp * GS, members, false,
-                             go_unit + (long long)grp * G * D, gml_unit + (long long)grp * G * 2, sh_w, sh_ml, sh_red);
-  if (!arrive(ctr0 + (long long)n_groups * decode_counter_stride, n_grp)) return;
-  decode_merge<G, D, NT, GS>(a, u, go_unit, gml_unit, 0, n_grp, true, nullptr, nullptr, sh_w, sh_ml, sh_red);
+  merge_all(ic<0>{});
 }
 
 // ----------------------------------------------------------------- scalar form
@@ -1120,6 +1157,15 @@ __device__ __forceinline__ void decode_merge_launch(const DecodeMergeArgs& a) {
 
 extern "C" __global__ __launch_bounds__(256) void vtb_decode_merge(vtb::DecodeMergeArgs a) {
   vtb::decode_merge_launch(a);
+}
+
+// The XCD (XCC_ID bits 3:0) each workgroup runs on, for the host's check of
+// the round-robin dealing of workgroups over XCDs that the XCD-local split
+// merge relies on.
+extern "C" __global__ __launch_bounds__(64) void vtb_xcc_probe(int* out) {
+  int v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  if (threadIdx.x == 0) out[blockIdx.x] = v & 0xf;
 }
 
 // Split-K workspace of the no-allocation decode entry

@@ -84,6 +84,10 @@ constexpr int decode_counter_stride = 32;
 // last workgroup's reads near 64 KiB.
 constexpr int decode_merge_flat(int partial_floats) { return partial_floats <= 512 ? 32 : 16; }
 constexpr int decode_merge_group = 16;
+// Kernels built with the XCD-local split merge (DecodeArgs::xcd_map): partials
+// of up to 1024 floats.  The d256 kernels with groups of 8 or more (one wave
+// per SIMD) needed stack for the second merge form.
+constexpr bool kDecodeXclSlots(int partial_floats) { return partial_floats <= 1024; }
 // Splits per (query, KV head) are capped so the group partials fit one
 // merge: decode_merge_group groups of decode_merge_group splits.
 constexpr int decode_max_splits = decode_merge_group * decode_merge_group;

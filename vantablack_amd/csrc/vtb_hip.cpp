@@ -83,6 +83,10 @@ struct VtbHipCtx {
   hipFunction_t f_decode[kNumKv][kNumD][kNumG] = {};
   hipFunction_t f_decodeh[kNumKv][kNumD][2] = {};  // vtb_decodeh_<kv>_d<D>_g<1|2>: head-group form
   hipFunction_t f_decode_merge = nullptr;            // vtb_decode_merge: the split merge as its own launch
+  // XCDs the workgroups of a launch are dealt over round-robin (workgroup i
+  // on XCD (i + r) mod xcd_map, r varying per launch), from vtb_xcc_probe at
+  // init; 0 when the dealing did not check out (no XCD-local merge).
+  int xcd_map = 0;
   hipFunction_t f_prefill[kNumD] = {};
   hipFunction_t f_kvt[kNumKv][kNumD] = {};  // pre-pass per cache dtype (f16, bf16)
   hipFunction_t f_append[kNumKv] = {};
@@ -420,6 +424,17 @@ int launch_decode(VtbHipCtx* ctx, float* out, const float* q, const void* k, con
   const bool merge_launch = n_q == 1 && n_splits > vtb::decode_merge_flat(G * HG * (int)head_dim) &&
                             env_flag("VTB_DECODE_MERGE_LAUNCH", true);
   a.merge_mode = merge_launch ? vtb::kDecodeMergeLaunch : vtb::kDecodeMergeInKernel;
+  // XCD-local merge: one query on the MFMA form with an in-kernel (flat)
+  // merge whose units split evenly over the XCDs; each unit's (m, l)
+  // partials then fill whole 128-byte lines ((n_splits * slots) % 16 == 0),
+  // so no line is written by two XCDs.  (C3: 9.9 -> 9.6 us per launch; the
+  // scalar head-group form at the C2 shape measured the same either way,
+  // 25.1 against 25.2 us, and keeps its units spread over the XCDs.)
+  const long long units = (long long)(n_kv / HG);
+  if (ctx->xcd_map > 0 && n_q == 1 && n_splits > 1 && !merge_launch && units % ctx->xcd_map == 0 &&
+      (n_splits * G * HG) % 16 == 0 && vtb::kDecodeXclSlots(G * HG * (int)head_dim) &&
+      vtb::decode_uses_mfma(kKvBytes[dtype], (int)head_dim, G))
+    a.xcd_map = ctx->xcd_map;
   hipFunction_t f = HG > 1 ? ctx->f_decodeh[dtype][di][G - 1] : ctx->f_decode[dtype][di][gi];
   int rc = launch(ctx, f, (unsigned)n_splits, (unsigned)(n_kv / HG), (unsigned)n_q,
                   64 * vtb::decode_waves(kKvBytes[dtype], (int)head_dim, G), &a);
@@ -835,6 +850,67 @@ char* bptr(VtbHipBuf* b, size_t off = 0) { return static_cast<char*>(b->ptr) + o
 
 // ============================================================== lifecycle
 
+// Number of XCDs the workgroups of one launch are dealt over, read from the
+// per-workgroup XCC ids of a launch (xcc[i] of workgroup i): nx when every
+// workgroup i runs on the XCD of workgroup i mod nx and workgroups
+// 0 .. nx-1 run on nx different XCDs, else 0.  The XCD-local split merge
+// (DecodeArgs::xcd_map) relies on exactly this dealing.
+extern "C" int vtb_hip_xcd_deal(const int* xcc, int n) {
+  if (!xcc || n <= 0) return 0;
+  int nx = 0;
+  bool seen[16] = {};
+  for (int i = 0; i < n; ++i) {
+    if (xcc[i] < 0 || xcc[i] >= 16) return 0;
+    if (!seen[xcc[i]]) {
+      seen[xcc[i]] = true;
+      ++nx;
+    }
+  }
+  if (n < 2 * nx) return 0;  // too few workgroups to see the pattern repeat
+  for (int i = nx; i < n; ++i)
+    if (xcc[i] != xcc[i % nx]) return 0;
+  return nx;
+}
+
+// Runs vtb_xcc_probe twice over 4096 workgroups and checks the dealing of
+// both launches (vtb_hip_xcd_deal; the starting XCD may differ between
+// launches).  0 on any failure or when VTB_DECODE_XCD_LOCAL=0.
+int probe_xcd_map(VtbHipCtx* ctx) {
+  if (!env_flag("VTB_DECODE_XCD_LOCAL", true)) return 0;
+  hipFunction_t f = nullptr;
+  if (hipModuleGetFunction(&f, ctx->mod_decode, "vtb_xcc_probe") != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  constexpr int kN = 4096;
+  int* d = nullptr;
+  if (hipMalloc((void**)&d, kN * sizeof(int)) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  std::vector<int> h(kN);
+  int nx = -1;
+  for (int rep = 0; rep < 2; ++rep) {
+    struct {
+      int* out;
+    } pa{d};
+    int r = -1;
+    if (launch(ctx, f, kN, 1, 1, 64, &pa) == VTB_HIP_OK &&
+        hipMemcpyAsync(h.data(), d, kN * sizeof(int), hipMemcpyDeviceToHost, ctx->stream) == hipSuccess &&
+        hipStreamSynchronize(ctx->stream) == hipSuccess)
+      r = vtb_hip_xcd_deal(h.data(), kN);
+    if (r <= 0 || (nx > 0 && r != nx)) {
+      nx = 0;
+      break;
+    }
+    nx = r;
+  }
+  (void)hipFree(d);
+  (void)hipGetLastError();
+  ctx->err.clear();
+  return nx > 0 ? nx : 0;
+}
+
 extern "C" VtbHipCtx* vtb_hip_init(void) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
@@ -924,6 +1000,7 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
     (void)hipGetLastError();
     ctx->err.clear();
   }
+  ctx->xcd_map = probe_xcd_map(ctx);
   return ctx;
 }
 
@@ -950,6 +1027,8 @@ extern "C" void* vtb_hip_stream(VtbHipCtx* ctx) { return ctx ? (void*)ctx->strea
 extern "C" const char* vtb_hip_last_error(VtbHipCtx* ctx) { return ctx ? ctx->err.c_str() : ""; }
 
 extern "C" int vtb_hip_cu_count(VtbHipCtx* ctx) { return ctx ? ctx->cu_count : 0; }
+
+extern "C" int vtb_hip_xcd_map(VtbHipCtx* ctx) { return ctx ? ctx->xcd_map : 0; }
 
 // ============================================================== buffers
 

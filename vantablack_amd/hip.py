@@ -71,6 +71,8 @@ SIGNATURES = {
     "vtb_hip_stream": ([_P], _P),
     "vtb_hip_last_error": ([_P], ctypes.c_char_p),
     "vtb_hip_cu_count": ([_P], _I),
+    "vtb_hip_xcd_map": ([_P], _I),
+    "vtb_hip_xcd_deal": ([_P, _I], _I),
     "vtb_hip_alloc": ([_P, _S], _P),
     "vtb_hip_wrap": ([_P, _P, _S], _P),
     "vtb_hip_release": ([_P], None),
@@ -391,6 +393,12 @@ class Context:
     @property
     def cu_count(self) -> int:
         return int(lib().vtb_hip_cu_count(self.h))
+
+    @property
+    def xcd_map(self) -> int:
+        """XCDs the decode launches' workgroups are dealt over (0: no
+        XCD-local split merge)."""
+        return int(lib().vtb_hip_xcd_map(self.h))
 
     @property
     def last_error(self) -> str:
