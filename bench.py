@@ -31,6 +31,10 @@ written by `bench.py --pmc-summary FETCH_DIR WRITE_DIR`.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ctx 8192]
        python bench.py --pmc-workload              (the counter-run workload)
        python bench.py --pmc-summary FETCH_DIR WRITE_DIR
+       python bench.py --trace-summary TRACE_DIR   (kernel-trace table by bench
+                                                    section; trace taken with
+                                                    VTB_BENCH_ROCTX=1 and
+                                                    --marker-trace)
 """
 from __future__ import annotations
 
@@ -55,6 +59,38 @@ BF16_PEAK_TFLOPS = 2500.0
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+class _Phases:
+    """ROCTx ranges around the bench sections when VTB_BENCH_ROCTX=1, so a
+    `rocprofv3 --kernel-trace --marker-trace` run of this script can be cut
+    by section (`--trace-summary`).  A no-op otherwise."""
+
+    def __init__(self):
+        self.lib = None
+        if os.environ.get("VTB_BENCH_ROCTX") == "1":
+            import ctypes
+            try:
+                self.lib = ctypes.CDLL("librocprofiler-sdk-roctx.so.1")
+                self.lib.roctxRangePushA.argtypes = [ctypes.c_char_p]
+            except OSError:
+                self.lib = None
+
+    def __call__(self, name):
+        phases = self
+
+        class _Range:
+            def __enter__(self):
+                if phases.lib is not None:
+                    phases.lib.roctxRangePushA(name.encode())
+
+            def __exit__(self, *exc):
+                if phases.lib is not None:
+                    phases.lib.roctxRangePop()
+        return _Range()
+
+
+phase = _Phases()
 
 
 def decode_bytes(L, n_heads, n_kv, d, kv_bytes):
@@ -956,6 +992,60 @@ def pmc_read(dirs):
     return {k: {c: sum(v) / len(v) for c, v in cs.items()} for k, cs in vals.items()}
 
 
+def trace_summary(dirs):
+    """Markdown table of the vtb_* dispatches in rocprofv3 kernel-trace csv
+    outputs under dirs, one row per (bench section, kernel, grid, block) in
+    dispatch order.  Sections come from the ROCTx ranges bench.py opens when
+    VTB_BENCH_ROCTX=1 (`--marker-trace` output); a dispatch belongs to the
+    range its start lies in."""
+    import csv
+    import glob
+
+    def files(pat):
+        return [f for d in dirs for f in glob.glob(os.path.join(d, "**", pat), recursive=True)]
+
+    def col(r, *names):
+        for n in names:
+            if n in r and r[n] != "":
+                return r[n]
+        return None
+
+    ranges = []
+    for f in files("*marker_api_trace.csv"):
+        for r in csv.DictReader(open(f)):
+            name = col(r, "Function", "Message", "Name")
+            t0, t1 = col(r, "Start_Timestamp"), col(r, "End_Timestamp")
+            if name and t0 and t1 and int(t1) > int(t0):
+                ranges.append((int(t0), int(t1), name))
+    ranges.sort()
+    rows = {}
+    for f in files("*kernel_trace.csv"):
+        for r in csv.DictReader(open(f)):
+            kname = r["Kernel_Name"].split("(")[0]
+            if not kname.startswith("vtb_"):
+                continue
+            t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+            sec = ""
+            for a, b, n in ranges:  # innermost (latest-starting) range holding t0
+                if a <= t0 < b:
+                    sec = n
+            grid = "x".join(col(r, f"Grid_Size_{c}") or "1" for c in "XYZ")
+            block = col(r, "Workgroup_Size_X", "Workgroup_Size") or "?"
+            key = (sec, kname, grid, block)
+            e = rows.setdefault(key, {"first": t0, "us": [], "vgpr": col(r, "Arch_VGPR_Count", "VGPR_Count"),
+                                      "agpr": col(r, "Accum_VGPR_Count"), "lds": col(r, "LDS_Block_Size", "Lds_Size"),
+                                      "scratch": col(r, "Scratch_Size", "Private_Segment_Size")})
+            e["first"] = min(e["first"], t0)
+            e["us"].append((t1 - t0) / 1e3)
+    print("| section | kernel | launches | avg us | min us | max us | grid (threads) | block | arch VGPR | AGPR | "
+          "LDS B | scratch B |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|---|")
+    for (sec, kname, grid, block), e in sorted(rows.items(), key=lambda kv: kv[1]["first"]):
+        us = e["us"]
+        print(f"| {sec or '-'} | {kname} | {len(us)} | {sum(us) / len(us):.2f} | {min(us):.2f} | {max(us):.2f} | "
+              f"{grid} | {block} | {e['vgpr']} | {e['agpr']} | {e['lds']} | {e['scratch']} |")
+
+
 def pmc_summary(fetch_dir, write_dir):
     """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the vtb_* kernels from
     two rocprofv3 --pmc csv outputs, scaled by the copy calibration, written
@@ -1066,6 +1156,25 @@ def pmc_sq_summary(dirs):
         print(f"| {k} | {e['dispatches']} | {e['dur_us']} | {e.get('clock_ghz', '')} | {e.get('mfma_flops', '')} | "
               f"{e.get('mfma_busy_at_clock', '')} | {e.get('mfma_busy_at_peak_clock', '')} | "
               f"{e.get('valu_busy_at_peak_clock', '')} | {e.get('valu_insts_per_wave', '')} | {e.get('waves', '')} |")
+    # Per wave: quad-cycle counters divided by SQ_WAVES; instruction counts
+    # per wave; LDS bank conflicts as a total.
+    print()
+    print("| kernel | waves | wave life | waiting (SQ_WAIT_ANY) | issuing (SQ_ACTIVE_INST_ANY) | of which VALU | "
+          "VMEM reads | LDS insts | MFMA insts | LDS bank conflicts (total) |")
+    print("|---|---|---|---|---|---|---|---|---|---|")
+    for k, e in kernels.items():
+        c = e["counters"]
+        w = c.get("SQ_WAVES")
+        if not w or "SQ_WAVE_CYCLES" not in c:
+            continue
+        life = c["SQ_WAVE_CYCLES"] / w
+
+        def pw(n):
+            return c.get(n, 0) / w
+        print(f"| {k} | {int(w)} | {life:.0f} | {pw('SQ_WAIT_ANY'):.0f} ({100 * pw('SQ_WAIT_ANY') / life:.0f}%) | "
+              f"{pw('SQ_ACTIVE_INST_ANY'):.0f} ({100 * pw('SQ_ACTIVE_INST_ANY') / life:.0f}%) | "
+              f"{pw('SQ_ACTIVE_INST_VALU'):.0f} | {pw('SQ_INSTS_VMEM_RD'):.0f} | {pw('SQ_INSTS_LDS'):.0f} | "
+              f"{pw('SQ_INSTS_MFMA'):.0f} | {int(c.get('SQ_LDS_BANK_CONFLICT', 0))} |")
 
 
 def load_counters():
@@ -1120,6 +1229,8 @@ def main():
         return pmc_summary(sys.argv[2], sys.argv[3])
     if len(sys.argv) > 1 and sys.argv[1] == "--pmc-sq-summary":
         return pmc_sq_summary(sys.argv[2:])
+    if len(sys.argv) > 1 and sys.argv[1] == "--trace-summary":
+        return trace_summary(sys.argv[2:])
     if len(sys.argv) > 1 and sys.argv[1] == "--pmc-dump":
         return print(json.dumps(pmc_read(sys.argv[2:]), indent=1))
     ap = argparse.ArgumentParser()
@@ -1141,34 +1252,40 @@ def main():
     import torch
     import vantablack_amd as vb
     ctx = vb.Context()
-    dec = bench_decode(ctx, torch, args)
+
+    def run(name, fn, *a, **kw):
+        with phase(name):
+            return fn(*a, **kw)
+
+    dec = run("C2 decode @8K", bench_decode, ctx, torch, args)
     # The other decode configs (3, 5), reported
     # beside the headline.  C3: window 4096 at position 16383 -> 4096 rows.
     dec_more = {} if args.no_more else {
-        "C1": bench_decode_cfg(ctx, torch, "C1", 1, 32, 4, 64, "f32", 512, steps=64),
-        "C3": bench_decode_cfg(ctx, torch, "C3", 32, 32, 8, 128, "bf16", 4096),
-        "C5": bench_decode_cfg(ctx, torch, "C5", 26, 8, 1, 256, "bf16", 32768),
+        "C1": run("C1 decode", bench_decode_cfg, ctx, torch, "C1", 1, 32, 4, 64, "f32", 512, steps=64),
+        "C3": run("C3 decode", bench_decode_cfg, ctx, torch, "C3", 32, 32, 8, 128, "bf16", 4096),
+        "C5": run("C5 decode", bench_decode_cfg, ctx, torch, "C5", 26, 8, 1, 256, "bf16", 32768),
         # C2's shape at 8K with the layer's RoPE of q and k_cur fused into
         # the same launch (the next-row prologue), to price the rotation.
-        "C2_rope_fused": bench_decode_cfg(ctx, torch, "C2+RoPE", 32, 32, 32, 128, "f16", 8192, rope=True),
+        "C2_rope_fused": run("C2 + RoPE decode", bench_decode_cfg, ctx, torch, "C2+RoPE", 32, 32, 32, 128, "f16",
+                             8192, rope=True),
         # C2 as BASELINE.json writes it: 256 steps, L 4097 -> 4352.
-        "C2_256": bench_decode_c2_run(ctx, torch),
+        "C2_256": run("C2 256 steps", bench_decode_c2_run, ctx, torch),
     }
     pre = {} if args.no_prefill else {
-        "C4_L512": bench_prefill(ctx, torch, 32, 8, 128, 512),
-        "C4_L2048": bench_prefill(ctx, torch, 32, 8, 128, 2048),
-        "C4_L8192": bench_prefill(ctx, torch, 32, 8, 128, 8192),
-        "C5_L4096": bench_prefill(ctx, torch, 8, 1, 256, 4096),
+        "C4_L512": run("C4 prefill 512", bench_prefill, ctx, torch, 32, 8, 128, 512),
+        "C4_L2048": run("C4 prefill 2048", bench_prefill, ctx, torch, 32, 8, 128, 2048),
+        "C4_L8192": run("C4 prefill 8192", bench_prefill, ctx, torch, 32, 8, 128, 8192),
+        "C5_L4096": run("C5 prefill 4096", bench_prefill, ctx, torch, 8, 1, 256, 4096),
     }
     # The next row beside attention: segMatmulQuant's GEMVs at Llama-2-7B
     # shapes, HBM-bound (weights streamed once per launch).
-    gemv = None if args.no_gemv else {kind: bench_gemv_layer(ctx, torch, kind)
+    gemv = None if args.no_gemv else {kind: run(f"GEMV {kind}", bench_gemv_layer, ctx, torch, kind)
                                        for kind in ("q4_k", "q5_k", "q6_k", "q8_0")}
     # matmulBatched (the prefill projections) at the C4 prompt length.
-    qgemm = None if args.no_gemv else bench_qgemm_layer(ctx, torch, "q4_k", 8192)
+    qgemm = None if args.no_gemv else run("batched projections", bench_qgemm_layer, ctx, torch, "q4_k", 8192)
     # The whole token: every layer on the GPU (gpuLayerStep x 32 + gpuFinalStep).
-    full = None if args.no_gemv else bench_full_decode(ctx, torch, ctx_rows=args.ctx)
-    fullp = None if (args.no_gemv or args.no_prefill) else bench_full_prefill(ctx, torch)
+    full = None if args.no_gemv else run("full decode", bench_full_decode, ctx, torch, ctx_rows=args.ctx)
+    fullp = None if (args.no_gemv or args.no_prefill) else run("full prefill", bench_full_prefill, ctx, torch)
     cpu = None if args.no_cpu else cpu_baseline()
     cpu_cfg = None if args.no_cpu else cpu_baseline_configs()
     ctx.close()
