@@ -343,7 +343,12 @@ def prefill_flops(L, n_heads, d):
 
 def prefill_kernel_name(torch, n_heads, n_q, d):
     """The attention kernel one attn_prefill call runs (launch_prefill_mfma in
-    vantablack_amd/csrc/vtb_hip.cpp): one per head_dim."""
+    vantablack_amd/csrc/vtb_hip.cpp): one per head_dim, and the key-split
+    form for d <= 128 when 128-query workgroups would fill at most half the
+    CUs."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if d <= 128 and 2 * n_heads * ((n_q + 127) // 128) <= cus:
+        return f"vtb_prefill_ks_d{d}"
     return f"vtb_prefill_d{d}"
 
 

@@ -180,7 +180,15 @@ def test_stage_arrays_and_lds_pointers():
                  "__shared__ __attribute__((aligned(16))) char s_k1[PrefillLds<D>::KBYTES];",
                  "__shared__ __attribute__((aligned(16))) char s_v0[PrefillLds<D>::VBYTES];",
                  "__shared__ __attribute__((aligned(16))) char s_v1[PrefillLds<D>::VBYTES];",
-                 "PrefillLds<D> lds{(lchar*)s_k0, (lchar*)s_k1, (lchar*)s_v0, (lchar*)s_v1};",
+                 # the key-split form's second tile of each step: the same sizes
+                 "__shared__ __attribute__((aligned(16))) char s_k2[KSPLIT ? PrefillLds<D>::KBYTES : 16];",
+                 "__shared__ __attribute__((aligned(16))) char s_k3[KSPLIT ? PrefillLds<D>::KBYTES : 16];",
+                 "__shared__ __attribute__((aligned(16))) char s_v2[KSPLIT ? PrefillLds<D>::VBYTES : 16];",
+                 "__shared__ __attribute__((aligned(16))) char s_v3[KSPLIT ? PrefillLds<D>::VBYTES : 16];",
+                 "PrefillLds<D> lds{(lchar*)s_k0, (lchar*)s_k1, (lchar*)s_v0, (lchar*)s_v1,\n"
+                 "                    (lchar*)s_k2, (lchar*)s_k3, (lchar*)s_v2, (lchar*)s_v3};",
+                 # a second-half tile is fetched only below the item's last key
+                 "if (t + BN < ikend) fetch(t + BN, kb, vb);",
                  "static constexpr int KBYTES = BN * (D / 8 + 1) * 16;",
                  "static constexpr int VBYTES = D * (BN / 8 + 1) * 16;",
                  "typedef __attribute__((address_space(3))) char lchar;"):

@@ -385,3 +385,38 @@ def test_prefill_value_outliers_alone_take_p_pieces(ctx, orc):
     vs = np.ones((n_rows, 2, 1), np.float32)
     vs[[9, 150, 390]] = 300.0
     prefill_case(ctx, orc, 8, 2, 128, "f16", n_rows, seed=87, v_scale=vs, q_scale=0.25)
+
+
+# Key-split small-prompt form (d <= 128; launch_prefill_mfma picks it when
+# 128-query workgroups would fill at most half the CUs): 64 queries per
+# workgroup, two waves per 32 queries taking alternate key tiles, their
+# partials merged through LDS as half 0's terms plus half 1's.  Each case
+# runs forced on (VTB_PREFILL_KS=2) and off (=0) against the oracle: C4 at
+# 512 tokens, a single query, one tile plus one key (the second half has no
+# tile), offsets, a window that starts mid-prompt, MQA d64, an uneven GQA map,
+# both two-piece precision forms (large scores; value outliers), and a long
+# prompt where the key ranges run many steps.
+@pytest.mark.parametrize("ks", ["2", "0"])
+@pytest.mark.parametrize("n_heads,n_kv,d,dtype,B,pos0,window,q_scale,v_outliers", [
+    (32, 8, 128, "bf16", 512, 0, None, 1.0, False),
+    (8, 2, 128, "bf16", 1, 0, None, 1.0, False),
+    (8, 2, 128, "bf16", 65, 0, None, 1.0, False),
+    (8, 2, 128, "f16", 200, 37, None, 1.0, False),
+    (8, 2, 128, "bf16", 300, 100, 96, 1.0, False),
+    (8, 1, 64, "bf16", 333, 0, None, 1.0, False),
+    (6, 4, 128, "bf16", 129, 0, None, 1.0, False),
+    (8, 2, 128, "bf16", 256, 0, None, 8.0, False),
+    (8, 2, 128, "bf16", 320, 0, None, 1.0, True),
+    (4, 1, 128, "bf16", 1500, 20, None, 1.0, False),
+])
+def test_prefill_key_split(ctx, orc, monkeypatch, ks, n_heads, n_kv, d, dtype, B, pos0, window, q_scale,
+                           v_outliers):
+    monkeypatch.setenv("VTB_PREFILL_KS", ks)
+    v_scale = 1.0
+    if v_outliers:  # 1% of value channels x20: crest factor above 8 (P as two pieces)
+        v_scale = np.ones((1, n_kv, d), np.float32)
+        v_scale[:, :, ::97] = 20.0
+    rows = None if B * n_heads <= 4096 else _dense_rows(B, 3, bm=64)
+    err = prefill_case(ctx, orc, n_heads, n_kv, d, dtype, B, pos0=pos0, window=window, seed=1200 + B,
+                       q_scale=q_scale, v_scale=v_scale, rows=rows, pooled=B * n_heads > 4096)
+    print(f"key split={ks} h{n_heads}/{n_kv} d{d} {dtype} B{B} pos0 {pos0} w{window}: rel err {err:.2e}")

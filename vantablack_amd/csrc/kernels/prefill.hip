@@ -289,6 +289,12 @@ struct PrefillLds {
   lchar* k1;
   lchar* v0;
   lchar* v1;
+  // Key-split form only: the second key tile of each step (stage sets
+  // {k0, v0, k2, v2} and {k1, v1, k3, v3}).
+  lchar* k2;
+  lchar* k3;
+  lchar* v2;
+  lchar* v3;
 };
 
 // Tile staging by LDS DMA (buffer_load_dwordx4 ... lds): a stage is filled
@@ -502,14 +508,15 @@ __device__ __forceinline__ TileSrc tile_src(const PrefillArgs& a, int kvh) {
 // with each query's causal and window range); piece < 0: the whole block
 // (write the output), else a piece of a split block (prefill_merge_pieces).
 // The entry has issued the DMA of the item's first key tile into stage 0
-// and the load of that tile's exponents (x_first).
-template <int D, int NW, bool XQ, bool XP>
+// (key-split: its first two tiles, into k0/v0 and k2/v2) and the load of
+// that tile's exponents (x_first; key-split: the wave's own tile's).
+template <int D, int NW, bool XQ, bool XP, bool KSPLIT>
 __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, const int qb, const int kvh,
                                              const f16x8 (&qf)[D / 16], const f16x8 (&ql)[D / 16],
                                              const int eq, PrefillLds<D>& lds, const long long k_lo,
                                              const long long k_hi, const int piece, const int2 x_first) {
   constexpr int NT = 64 * NW;                 // threads per workgroup
-  constexpr int BM = 32 * NW;                 // queries per workgroup (NW waves x 32)
+  constexpr int BM = prefill_item_queries(NW, KSPLIT);  // queries per work item
   constexpr int BN = prefill_block_n(D);      // keys per tile
   constexpr int KCH = D / 8;                  // 16-byte chunks per K row
   constexpr int VCH = BN / 8;                 // 16-byte chunks per V^T row
@@ -544,9 +551,13 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int hi = lane >> 5;   // lane half
   const int lc = lane & 31;   // lane column: the query this lane owns
+  // The wave's 32 queries (sub-block wsb of the item) and, in the key-split
+  // form, its key half kh: of each step's two key tiles it computes tile kh.
+  const int wsb = KSPLIT ? wave >> 1 : wave;
+  const int kh = KSPLIT ? wave & 1 : 0;
 
   const int m0 = qb * BM;
-  const int mq = m0 + wave * 32 + lc;  // this lane's query (may be >= n_q: padding)
+  const int mq = m0 + wsb * 32 + lc;  // this lane's query (may be >= n_q: padding)
   const long long qpos = a.pos0 + mq;
   const long long q_lo = a.pos0 + m0;  // first query position of the workgroup
   long long kbeg, kend;  // keys [kbeg, kend) may be attended
@@ -554,9 +565,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   const long long kt_first = kbeg / BN * BN;
 
   // Wave-level query range, for tile skipping.
-  const long long wq_lo = a.pos0 + m0 + wave * 32;
-  const long long wq_hi = a.pos0 + (m0 + wave * 32 + 31 < a.n_q ? m0 + wave * 32 + 31 : a.n_q - 1);
-  const bool wave_live = m0 + wave * 32 < a.n_q;
+  const long long wq_lo = a.pos0 + m0 + wsb * 32;
+  const long long wq_hi = a.pos0 + (m0 + wsb * 32 + 31 < a.n_q ? m0 + wsb * 32 + 31 : a.n_q - 1);
+  const bool wave_live = m0 + wsb * 32 < a.n_q;
 
   const TileSrc src = tile_src<D>(a, kvh);
   const char* const kbase = src.kbase;
@@ -586,6 +597,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   // wave accumulated (wave-uniform); a tile with another exponent first
   // rescales O by a power of two (exact).
   int E = 0;
+  int acc = 0;  // some tile was accumulated (wave-uniform)
   // The window as a 32-bit bound (positions stay below 2^30; a larger or
   // absent window keeps every causal key).
   const int wcap = (a.window > 0 && a.window < (1 << 30)) ? (int)a.window : (1 << 30);
@@ -604,6 +616,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
     bool live = wave_live && t0 <= iwq_hi;
     if (iwin > 0 && t0 + BN - 1 < iwq_lo - iwin + 1) live = false;
     if (!live) return;
+    acc = 1;
     evt = evt == kEvAny ? E : evt;  // an all-zero tile fits any unit
     int es = eq + ek;
     es = es < -120 ? -120 : (es > 120 ? 120 : es);
@@ -775,36 +788,129 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
   int2 x0 = {0, 0}, x1 = {0, 0};
   const int ikend = __builtin_amdgcn_readfirstlane((int)kend);
   const int ikt_first = __builtin_amdgcn_readfirstlane((int)kt_first);
-  if (ikt_first < ikend) {
-    x0 = x_first;
-    wait_loads();
-    x0.x = __builtin_amdgcn_readfirstlane(x0.x);
-    x0.y = __builtin_amdgcn_readfirstlane(x0.y);
-    E = x0.y == kEvAny ? 0 : x0.y;
-  }
-  for (int kt0 = ikt_first; kt0 < ikend; kt0 += 2 * BN) {
-    __syncthreads();
-    const bool more1 = kt0 + BN < ikend;
-    if (more1) {
-      fetch(kt0 + BN, k_lds1, v_lds1);
-      x1 = texp_of(kt0 + BN);
+  auto uniform2 = [](int2 x) { return int2{__builtin_amdgcn_readfirstlane(x.x), __builtin_amdgcn_readfirstlane(x.y)}; };
+  if constexpr (!KSPLIT) {
+    if (ikt_first < ikend) {
+      x0 = x_first;
+      wait_loads();
+      x0 = uniform2(x0);
+      E = x0.y == kEvAny ? 0 : x0.y;
     }
-    compute(k_lds0, v_lds0, kt0, x0.x, x0.y);
-    if (!more1) break;
-    wait_loads();
-    x1.x = __builtin_amdgcn_readfirstlane(x1.x);
-    x1.y = __builtin_amdgcn_readfirstlane(x1.y);
-    __syncthreads();
-    const bool more2 = kt0 + 2 * BN < ikend;
-    if (more2) {
-      fetch(kt0 + 2 * BN, k_lds0, v_lds0);
-      x0 = texp_of(kt0 + 2 * BN);
+    for (int kt0 = ikt_first; kt0 < ikend; kt0 += 2 * BN) {
+      __syncthreads();
+      const bool more1 = kt0 + BN < ikend;
+      if (more1) {
+        fetch(kt0 + BN, k_lds1, v_lds1);
+        x1 = texp_of(kt0 + BN);
+      }
+      compute(k_lds0, v_lds0, kt0, x0.x, x0.y);
+      if (!more1) break;
+      wait_loads();
+      x1 = uniform2(x1);
+      __syncthreads();
+      const bool more2 = kt0 + 2 * BN < ikend;
+      if (more2) {
+        fetch(kt0 + 2 * BN, k_lds0, v_lds0);
+        x0 = texp_of(kt0 + 2 * BN);
+      }
+      compute(k_lds1, v_lds1, kt0 + BN, x1.x, x1.y);
+      if (!more2) break;
+      wait_loads();
+      x0 = uniform2(x0);
     }
-    compute(k_lds1, v_lds1, kt0 + BN, x1.x, x1.y);
-    if (!more2) break;
-    wait_loads();
-    x0.x = __builtin_amdgcn_readfirstlane(x0.x);
-    x0.y = __builtin_amdgcn_readfirstlane(x0.y);
+  } else {
+    // Key-split form: each step stages two key tiles, t (for the kh = 0
+    // waves) and t + BN (kh = 1), in one stage set while the other set is
+    // computed: sets {k0, v0, k2, v2} and {k1, v1, k3, v3}.  A tile at or
+    // past the item's last key is neither fetched nor read (no wave is live
+    // for it) and its exponents are not loaded.
+    lchar* const k_lds2 = lds.k2;
+    lchar* const k_lds3 = lds.k3;
+    lchar* const v_lds2 = lds.v2;
+    lchar* const v_lds3 = lds.v3;
+    auto fetch2 = [&](int t, lchar* ka, lchar* va, lchar* kb, lchar* vb) {
+      fetch(t, ka, va);
+      if (t + BN < ikend) fetch(t + BN, kb, vb);
+    };
+    auto texp_own = [&](int t) -> int2 { return t + kh * BN < ikend ? texp_of(t + kh * BN) : int2{0, 0}; };
+    if (ikt_first < ikend) {  // the entry issued the first step and this wave's exponent load
+      x0 = x_first;
+      wait_loads();
+      x0 = uniform2(x0);
+      E = x0.y == kEvAny ? 0 : x0.y;
+    }
+    for (int kt0 = ikt_first; kt0 < ikend; kt0 += 4 * BN) {
+      __syncthreads();
+      const bool more1 = kt0 + 2 * BN < ikend;
+      if (more1) {
+        fetch2(kt0 + 2 * BN, k_lds1, v_lds1, k_lds3, v_lds3);
+        x1 = texp_own(kt0 + 2 * BN);
+      }
+      // One call per half (wave-uniform branch): with a select between the
+      // stage pointers the compiler cannot tell the read stage from the one
+      // the DMA above fills and waits for that DMA first.
+      if (kh)
+        compute(k_lds2, v_lds2, kt0 + BN, x0.x, x0.y);
+      else
+        compute(k_lds0, v_lds0, kt0, x0.x, x0.y);
+      if (!more1) break;
+      wait_loads();
+      x1 = uniform2(x1);
+      __syncthreads();
+      const bool more2 = kt0 + 4 * BN < ikend;
+      if (more2) {
+        fetch2(kt0 + 4 * BN, k_lds0, v_lds0, k_lds2, v_lds2);
+        x0 = texp_own(kt0 + 4 * BN);
+      }
+      if (kh)
+        compute(k_lds3, v_lds3, kt0 + 3 * BN, x1.x, x1.y);
+      else
+        compute(k_lds1, v_lds1, kt0 + 2 * BN, x1.x, x1.y);
+      if (!more2) break;
+      wait_loads();
+      x0 = uniform2(x0);
+    }
+    // The two key halves of each 32 queries: the kh = 1 wave hands its
+    // partial (o, m, l per lane; E) to the kh = 0 wave through the free
+    // stage buffers, which merges them as half 0's terms plus half 1's (the
+    // same order every launch).  Both waves hold the same (dim, query) in
+    // the same lane and register.
+    typedef __attribute__((address_space(3))) float lfloat;
+    static_assert(ND * 16 * 64 * 4 <= PrefillLds<D>::KBYTES && 130 * 4 <= PrefillLds<D>::VBYTES, "hand-off space");
+    __syncthreads();  // every wave is done with the stages
+    lfloat* const xo = (lfloat*)(wsb == 0 ? k_lds0 : k_lds1);
+    lfloat* const xm = (lfloat*)(wsb == 0 ? v_lds0 : v_lds1);
+    if (kh) {
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xo[(dt * 16 + r) * 64 + lane] = o[dt][r];
+      xm[lane] = m_ref;
+      xm[64 + lane] = l_run;
+      if (lane == 0) {
+        xm[128] = __builtin_bit_cast(float, E);
+        xm[129] = __builtin_bit_cast(float, acc);
+      }
+    }
+    __syncthreads();
+    if (kh) return;
+    const float m1 = xm[lane], l1 = xm[64 + lane];
+    const int E1 = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, xm[128]));
+    const int acc1 = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, xm[129]));
+    const float M = fmaxf(m_ref, m1);
+    const float f0 = m_ref == -INFINITY ? 0.0f : exp2_fast(m_ref - M);
+    const float f1 = m1 == -INFINITY ? 0.0f : exp2_fast(m1 - M);
+    // The common unit: the larger of the two, or the other half's where one
+    // half accumulated no tile (its E is only its first tile's, or none).
+    const int Em = !acc1 ? E : (!acc ? E1 : (E > E1 ? E : E1));
+    const float g0 = f0 * pow2_diff(E - Em), g1 = f1 * pow2_diff(E1 - Em);
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * g0 + xo[(dt * 16 + r) * 64 + lane] * g1;
+    l_run = l_run * f0 + l1 * f1;
+    m_ref = M;
+    E = Em;
   }
 
   if constexpr (kBalanced<D>) {
@@ -826,10 +932,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const int h, 
 //       |v - out|, so outlier values carry it into the output.
 // Keys of bf16 caches are exact in f16 (per-tile power-of-two scale), f16
 // keys are the cache itself; P's rounding enters the output through V only.
-template <int D, int NW>
+template <int D, int NW, bool KSPLIT = false>
 __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
   constexpr int KS = D / 16;
-  constexpr int BM = 32 * NW;
+  constexpr int BM = prefill_item_queries(NW, KSPLIT);
   constexpr int BN = prefill_block_n(D);
   constexpr int NT = 64 * NW;
   __shared__ float s_red[NW][5];
@@ -837,7 +943,13 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
   __shared__ __attribute__((aligned(16))) char s_k1[PrefillLds<D>::KBYTES];
   __shared__ __attribute__((aligned(16))) char s_v0[PrefillLds<D>::VBYTES];
   __shared__ __attribute__((aligned(16))) char s_v1[PrefillLds<D>::VBYTES];
-  PrefillLds<D> lds{(lchar*)s_k0, (lchar*)s_k1, (lchar*)s_v0, (lchar*)s_v1};
+  // The key-split form's second tile per step (a 16-byte stand-in otherwise).
+  __shared__ __attribute__((aligned(16))) char s_k2[KSPLIT ? PrefillLds<D>::KBYTES : 16];
+  __shared__ __attribute__((aligned(16))) char s_k3[KSPLIT ? PrefillLds<D>::KBYTES : 16];
+  __shared__ __attribute__((aligned(16))) char s_v2[KSPLIT ? PrefillLds<D>::VBYTES : 16];
+  __shared__ __attribute__((aligned(16))) char s_v3[KSPLIT ? PrefillLds<D>::VBYTES : 16];
+  PrefillLds<D> lds{(lchar*)s_k0, (lchar*)s_k1, (lchar*)s_v0, (lchar*)s_v1,
+                    (lchar*)s_k2, (lchar*)s_k3, (lchar*)s_v2, (lchar*)s_v3};
   const int nblk = gridDim.y;
   int h, w;
   {
@@ -911,11 +1023,18 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
         const TileDma<D, NW> dma(wave, lane, (int)src.krow_bytes, src.vrow_bytes);
         dma.issue_k(src.kbase, src.krow_bytes, kend, kt_first, lds.k0);
         dma.issue_v(src.vbase, src.vrow_bytes, kt_first, lds.v0);
-        if (a.texp)
-          x_first = *reinterpret_cast<const int2*>(a.texp + ((long long)kvh * (a.vt_ld >> 6) + (kt_first >> 6)) * 2);
+        // Key-split: the first step's second tile too, and each wave's own
+        // tile's exponents (none past the item's last key).
+        if (KSPLIT && kt_first + BN < kend) {
+          dma.issue_k(src.kbase, src.krow_bytes, kend, kt_first + BN, lds.k2);
+          dma.issue_v(src.vbase, src.vrow_bytes, kt_first + BN, lds.v2);
+        }
+        const long long kx = kt_first + (KSPLIT ? (wave & 1) * BN : 0);
+        if (a.texp && kx < kend)
+          x_first = *reinterpret_cast<const int2*>(a.texp + ((long long)kvh * (a.vt_ld >> 6) + (kx >> 6)) * 2);
       }
     }
-    const int mq = qb * 32 * NW + wave * 32 + lc;
+    const int mq = qb * BM + (KSPLIT ? wave >> 1 : wave) * 32 + lc;
     const int mr = mq < a.n_q ? mq : a.n_q - 1;  // padding lanes reuse the last query
     const float* qp = a.q + ((long long)mr * a.n_heads + h) * D + 8 * hi;
     // Q^T fragments (B operand): lane holds Q[mq][16ks + 8hi .. +8], read as
@@ -1014,11 +1133,11 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
     // kernel made the register allocator spill VGPRs in the d128 and d256
     // kernels.
     if (xp)
-      prefill_body<D, NW, true, true>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece, x_first);
+      prefill_body<D, NW, true, true, KSPLIT>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece, x_first);
     else if (xq)
-      prefill_body<D, NW, true, false>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece, x_first);
+      prefill_body<D, NW, true, false, KSPLIT>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece, x_first);
     else
-      prefill_body<D, NW, false, false>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece, x_first);
+      prefill_body<D, NW, false, false, KSPLIT>(a, h, qb, kvh, qf, ql, eq, lds, k_lo, k_hi, piece, x_first);
   }
 }
 
@@ -1036,9 +1155,19 @@ __device__ __forceinline__ void prefill_entry(const PrefillArgs& a) {
     vtb::kvt_body<vtb::DTT, D>(a);                                                         \
   }
 
+// Key-split small-prompt form (d <= 128): 64 queries per workgroup, two
+// waves per 32 queries each taking every other key tile; one workgroup per
+// CU (eight K / V^T stages, 140 KB of LDS at d128).
+#define VTB_PREFILL_KS(D)                                                                  \
+  extern "C" __global__ __launch_bounds__(256, 1) void vtb_prefill_ks_d##D(vtb::PrefillArgs a) { \
+    vtb::prefill_entry<D, 4, true>(a);                                                     \
+  }
+
 VTB_PREFILL(64)
 VTB_PREFILL(128)
 VTB_PREFILL(256)
+VTB_PREFILL_KS(64)
+VTB_PREFILL_KS(128)
 VTB_KVT(bf16, kv_bf16, 64)
 VTB_KVT(bf16, kv_bf16, 128)
 VTB_KVT(bf16, kv_bf16, 256)

@@ -107,6 +107,9 @@ constexpr int decode_split_quantum(int head_dim, int kv_bytes, int g, int hg = 1
 // Prefill (MFMA): 4 waves x 32 queries per workgroup; keys per LDS tile by
 // head_dim (the K and V^T tiles stay near 36 KiB of LDS).
 constexpr int prefill_block_m(int) { return 128; }
+// Queries per work item: 32 per wave, or in the key-split small-prompt form
+// (two waves per 32 queries, each taking every other key tile) 64.
+constexpr int prefill_item_queries(int nw, bool key_split) { return key_split ? 64 : 32 * nw; }
 constexpr int prefill_block_n(int head_dim) { return head_dim <= 128 ? 64 : 32; }
 // Minimum resident waves per SIMD the prefill kernel is compiled for: two
 // waves let one wave's softmax and LDS waits hide behind the other's MFMAs

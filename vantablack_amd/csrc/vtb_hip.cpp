@@ -88,6 +88,7 @@ struct VtbHipCtx {
   // init; 0 when the dealing did not check out (no XCD-local merge).
   int xcd_map = 0;
   hipFunction_t f_prefill[kNumD] = {};
+  hipFunction_t f_prefill_ks[kNumD] = {};  // key-split small-prompt form (d <= 128)
   hipFunction_t f_kvt[kNumKv][kNumD] = {};  // pre-pass per cache dtype (f16, bf16)
   hipFunction_t f_append[kNumKv] = {};
   hipFunction_t f_copy = nullptr;
@@ -521,7 +522,19 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
     return set_err(ctx, VTB_HIP_EUNSUPPORTED, "prefill kernel not built for this shape");
   if (!aligned16(k) || !aligned16(v) || !aligned16(q))
     return set_err(ctx, VTB_HIP_EINVAL, "q/K/V not 16-byte aligned");
-  const size_t bm = (size_t)vtb::prefill_block_m((int)head_dim);
+  // Key-split small prompts (d <= 128): when the plain grid of 128-query
+  // workgroups would fill at most half the CUs, a workgroup takes 64
+  // queries and two waves share each 32, taking alternate key tiles, so the
+  // longest causal block runs half its tiles per wave and twice as many CUs
+  // work.  C4 (32/8 heads, d128) at 512 tokens: 26.4 -> 23.9 us per call;
+  // at 1024 tokens (a plain grid of one workgroup per CU) it measured 42.8
+  // against 38.9 us, hence the half.  VTB_PREFILL_KS=0 turns it off, =2
+  // forces it.
+  const int ks_mode = env_flag("VTB_PREFILL_KS", true) ? env_int("VTB_PREFILL_KS", 1) : 0;
+  const size_t bm_plain = (size_t)vtb::prefill_block_m((int)head_dim);
+  const bool ks = ctx->f_prefill_ks[di] && ks_mode != 0 &&
+                  (ks_mode == 2 || 2LL * (long long)(n_heads * ((n_q + bm_plain - 1) / bm_plain)) <= ctx->cu_count);
+  const size_t bm = ks ? (size_t)vtb::prefill_item_queries(4, true) : bm_plain;
   const size_t nblk = (n_q + bm - 1) / bm;
   if (nblk > 65535 || n_heads > 0x7fffffff) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "grid too large");
   // Balanced pairs of query blocks (prefill_entry; the d256 kernel, whose
@@ -529,7 +542,7 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
   // an even block count and causal ranges not cut by a window.  C5 (4096
   // tokens, 8/1 heads): 140 against 214 us per call.  VTB_PREFILL_BALANCE=0
   // turns it off.
-  const bool balance = env_flag("VTB_PREFILL_BALANCE", true) && head_dim >= 256 && nblk >= 2 &&
+  const bool balance = !ks && env_flag("VTB_PREFILL_BALANCE", true) && head_dim >= 256 && nblk >= 2 &&
                        nblk % 2 == 0 && (window <= 0 || window >= pos0 + (long long)n_q);
   const size_t nt = 256;
   // Pre-pass over keys [0, pos0 + n_q), padded to whole 64-key tiles, from
@@ -598,7 +611,7 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
   // One round of workgroups, two per CU (d <= 128: 72 KB of LDS each): the
   // pair order evens each CU's causal load.  VTB_PREFILL_PAIR_ORDER=0 turns
   // it off.
-  if (!balance && head_dim <= 128 && nblk % 2 == 0 && (long long)(n_heads * nblk) > (long long)ctx->cu_count &&
+  if (!balance && !ks && head_dim <= 128 && nblk % 2 == 0 && (long long)(n_heads * nblk) > (long long)ctx->cu_count &&
       (long long)(n_heads * nblk) <= 2LL * ctx->cu_count && (window <= 0 || window >= pos0 + (long long)n_q) &&
       env_flag("VTB_PREFILL_PAIR_ORDER", true))
     a.flags |= vtb::kPrefillPairOrder;
@@ -610,7 +623,8 @@ int launch_prefill_mfma(VtbHipCtx* ctx, float* out, const float* q, const void* 
   }
   // x = head (fastest), y = query block: the longest (causal) blocks of every
   // head are dispatched first.
-  return launch(ctx, ctx->f_prefill[di], (unsigned)n_heads, (unsigned)nblk, 1, (unsigned)nt, &a);
+  return launch(ctx, ks ? ctx->f_prefill_ks[di] : ctx->f_prefill[di], (unsigned)n_heads, (unsigned)nblk, 1,
+                (unsigned)nt, &a);
 }
 
 // Quantised GEMV launcher: out[m] = W[m, k] . x.  One workgroup per R rows
@@ -949,6 +963,9 @@ extern "C" VtbHipCtx* vtb_hip_init(void) {
         snprintf(name, sizeof name, "vtb_prefill_d%d", D);
         if (hipModuleGetFunction(&ctx->f_prefill[di], ctx->mod_prefill, name) != hipSuccess)
           ctx->f_prefill[di] = nullptr;
+        snprintf(name, sizeof name, "vtb_prefill_ks_d%d", D);
+        if (D > 128 || hipModuleGetFunction(&ctx->f_prefill_ks[di], ctx->mod_prefill, name) != hipSuccess)
+          ctx->f_prefill_ks[di] = nullptr;
       }
     }
     if (ok) {
