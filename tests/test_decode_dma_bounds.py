@@ -32,8 +32,12 @@ TILES = os.path.join(ROOT, "vantablack_amd", "csrc", "tiles.h")
 HOST = os.path.join(ROOT, "vantablack_amd", "csrc", "vtb_hip.cpp")
 
 
-def mfma_waves(d, g):  # tiles.h decode_mfma_waves (VTB_DECODE_MFMA_WAVES 8, _D256 4)
-    return (4 if d >= 256 else 8) // (2 if g >= 16 else 1)
+def mfma_waves(d, g):  # tiles.h decode_mfma_waves (VTB_DECODE_MFMA_WAVES 8, _D256 8)
+    return 8 // (2 if g >= 16 else 1)
+
+
+def mfma_stages(d):  # tiles.h decode_mfma_stages (VTB_DECODE_MFMA_STAGES_D256 1)
+    return 1 if d >= 256 else 2
 
 
 def kswz(d, r):
@@ -62,7 +66,7 @@ SHAPES = [(d, g) for d in (64, 128, 256) for g in (4, 8, 16) if not (g >= 16 and
 def test_lds_writes_stay_in_the_waves_region_and_cover_it(d, g):
     m = model(d, g)
     assert m["NI"] * 64 == 16 * m["C"] and m["NI"] >= 1
-    for stage in (0, 1):
+    for stage in range(mfma_stages(d)):
         array_bytes = m["NW"] * m["SB"]  # s_stg0 / s_stg1
         seen = [0] * array_bytes
         for wave in range(m["NW"]):
@@ -144,12 +148,14 @@ def test_model_constants_match_the_sources():
     for expr in ("constexpr int C = D / 8;", "constexpr int RB = 2 * D;", "constexpr int VOFF = 16 * RB;",
                  "constexpr int SB = 2 * 16 * RB;", "constexpr int NI = 16 * C / 64;",
                  "__shared__ __attribute__((aligned(16))) char s_stg0[NW * SB];",
-                 "__shared__ __attribute__((aligned(16))) char s_stg1[NW * SB];",
+                 "constexpr int NSTG = decode_mfma_stages(D);",
+                 "__shared__ __attribute__((aligned(16))) char s_stg1[NSTG > 1 ? NW * SB : 16];",
+                 "dchar* const stg1 = (dchar*)s_stg1 + (NSTG > 1 ? wave * SB : 0);",
+                 "if (NSTG > 1 && n_blk > 1) issue(1, stg1);",
                  "const int s = 64 * i + lane, r = s / C, cs = s % C;",
                  "koff[i] = (int)(r * rs) + 16 * (cs ^ kswz<D>(r));",
                  "voff[i] = (int)(r * rs) + 16 * (cs ^ vswz<D>(r));",
                  "dchar* const stg0 = (dchar*)s_stg0 + wave * SB;",
-                 "dchar* const stg1 = (dchar*)s_stg1 + wave * SB;",
                  "const long long nr = w1 - t0 < 16 ? w1 - t0 : 16;",
                  "const auto rk = buffer_rsrc(kbase + t0 * rs, (unsigned)(nr * rs));",
                  "const auto rv = buffer_rsrc(vbase + t0 * rs, (unsigned)(nr * rs));",
@@ -161,7 +167,10 @@ def test_model_constants_match_the_sources():
     tiles = open(TILES).read()
     assert "return (head_dim >= 256 ? VTB_DECODE_MFMA_WAVES_D256 : VTB_DECODE_MFMA_WAVES) / (g >= 16 ? 2 : 1);" \
         in tiles
-    assert "#define VTB_DECODE_MFMA_WAVES 8" in tiles and "#define VTB_DECODE_MFMA_WAVES_D256 4" in tiles
+    assert "#define VTB_DECODE_MFMA_WAVES 8" in tiles and "#define VTB_DECODE_MFMA_WAVES_D256 8" in tiles
+    assert "#define VTB_DECODE_MFMA_STAGES_D256 1" in tiles
+    assert ("constexpr int decode_mfma_stages(int head_dim) { return head_dim >= 256 ? "
+            "VTB_DECODE_MFMA_STAGES_D256 : 2; }") in tiles
     assert "return kv_bytes == 2 && g >= 4 && !(g >= 16 && head_dim >= 256);" in tiles
     host = open(HOST).read()
     assert "(long long)(n_kv * head_dim) * 2 * 16 >= (1LL << 31)" in host

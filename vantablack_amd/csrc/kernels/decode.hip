@@ -769,7 +769,8 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a) {
   static_assert((long long)G * D * 4 <= SB, "a wave's partial must fit its stage");
 
   __shared__ __attribute__((aligned(16))) char s_stg0[NW * SB];
-  __shared__ __attribute__((aligned(16))) char s_stg1[NW * SB];
+  constexpr int NSTG = decode_mfma_stages(D);
+  __shared__ __attribute__((aligned(16))) char s_stg1[NSTG > 1 ? NW * SB : 16];
   __shared__ float s_m[NW][G];
   __shared__ float s_l[NW][G];
   __shared__ __attribute__((aligned(16))) uint16_t s_q[4 * G][QLD];
@@ -806,7 +807,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a) {
     voff[i] = (int)(r * rs) + 16 * (cs ^ vswz<D>(r));
   }
   dchar* const stg0 = (dchar*)s_stg0 + wave * SB;
-  dchar* const stg1 = (dchar*)s_stg1 + wave * SB;
+  dchar* const stg1 = (dchar*)s_stg1 + (NSTG > 1 ? wave * SB : 0);
   // Block j (rows w0 + 16 j ...) of K and V into a stage.
   auto issue = [&](int j, dchar* st) {
     const long long t0 = w0 + 16LL * j;
@@ -853,7 +854,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a) {
   }
   __builtin_amdgcn_sched_barrier(0);
   if (n_blk > 0) issue(0, stg0);
-  if (n_blk > 1) issue(1, stg1);
+  if (NSTG > 1 && n_blk > 1) issue(1, stg1);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < QPW; ++j) {
@@ -1024,23 +1025,35 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
 
-  // Two stages per wave: block j in stage j % 2, block j + 2 issued into
-  // it once block j has been computed.  vmcnt counts this wave's DMA
-  // instructions (2 NI per block), so "block j has landed" is vmcnt <= 2 NI
-  // while block j + 1 is in flight, else 0.
-  for (int j = 0; j < n_blk; j += 2) {
-    if (j + 1 < n_blk) wait_vmcnt<2 * NI>(); else wait_vmcnt<0>();
-    compute(stg0, j);
-    if (j + 2 < n_blk) {
-      wait_lds();
-      issue(j + 2, stg0);
+  // Two stages per wave (NSTG = 2): block j in stage j % 2, block j + 2
+  // issued into it once block j has been computed.  vmcnt counts this wave's
+  // DMA instructions (2 NI per block), so "block j has landed" is vmcnt <=
+  // 2 NI while block j + 1 is in flight, else 0.  One stage (NSTG = 1): block
+  // j + 1 is issued into the stage once block j has been computed.
+  if constexpr (NSTG == 1) {
+    for (int j = 0; j < n_blk; ++j) {
+      wait_vmcnt<0>();
+      compute(stg0, j);
+      if (j + 1 < n_blk) {
+        wait_lds();
+        issue(j + 1, stg0);
+      }
     }
-    if (j + 1 >= n_blk) break;
-    if (j + 2 < n_blk) wait_vmcnt<2 * NI>(); else wait_vmcnt<0>();
-    compute(stg1, j + 1);
-    if (j + 3 < n_blk) {
-      wait_lds();
-      issue(j + 3, stg1);
+  } else {
+    for (int j = 0; j < n_blk; j += 2) {
+      if (j + 1 < n_blk) wait_vmcnt<2 * NI>(); else wait_vmcnt<0>();
+      compute(stg0, j);
+      if (j + 2 < n_blk) {
+        wait_lds();
+        issue(j + 2, stg0);
+      }
+      if (j + 1 >= n_blk) break;
+      if (j + 2 < n_blk) wait_vmcnt<2 * NI>(); else wait_vmcnt<0>();
+      compute(stg1, j + 1);
+      if (j + 3 < n_blk) {
+        wait_lds();
+        issue(j + 3, stg1);
+      }
     }
   }
 

@@ -45,18 +45,28 @@ constexpr bool decode_uses_mfma(int kv_bytes, int head_dim, int g) {
 #ifndef VTB_DECODE_WAVES8
 #define VTB_DECODE_WAVES8 8
 #endif
-// MFMA form: the two K/V stages of every wave (64 * head_dim bytes each)
-// fill about 128 KiB of LDS: 8 waves (two per SIMD) for head_dim <= 128, 4
-// for 256; groups of 16 halve that to leave room for their query pieces.
+// MFMA form: the K/V stages of every wave (64 * head_dim bytes each) fill
+// about 128 KiB of LDS: 8 waves (two per SIMD) of two stages for head_dim
+// <= 128, of one stage for 256 (decode_mfma_stages); groups of 16 halve the
+// waves to leave room for their query pieces.
 #ifndef VTB_DECODE_MFMA_WAVES
 #define VTB_DECODE_MFMA_WAVES 8
 #endif
 #ifndef VTB_DECODE_MFMA_WAVES_D256
-#define VTB_DECODE_MFMA_WAVES_D256 4
+#define VTB_DECODE_MFMA_WAVES_D256 8
 #endif
 constexpr int decode_mfma_waves(int head_dim, int g) {
   return (head_dim >= 256 ? VTB_DECODE_MFMA_WAVES_D256 : VTB_DECODE_MFMA_WAVES) / (g >= 16 ? 2 : 1);
 }
+// LDS stages per wave of the MFMA form (2: block j+1's DMA in flight while
+// block j is computed; 1: one block at a time, the SIMD's other wave
+// overlapping).  head_dim 256: eight waves of one stage (two waves per SIMD,
+// 150 KB of LDS) instead of four of two: C5 18.2-18.4 -> 16.8 us per layer
+// (four waves of one stage: 17.5-17.7).
+#ifndef VTB_DECODE_MFMA_STAGES_D256
+#define VTB_DECODE_MFMA_STAGES_D256 1
+#endif
+constexpr int decode_mfma_stages(int head_dim) { return head_dim >= 256 ? VTB_DECODE_MFMA_STAGES_D256 : 2; }
 constexpr int decode_waves(int kv_bytes, int head_dim, int g) {
   return decode_uses_mfma(kv_bytes, head_dim, g) ? decode_mfma_waves(head_dim, g)
          : g == 1                      ? VTB_DECODE_WAVES1
