@@ -374,18 +374,21 @@ def bench_prefill(ctx, torch, n_heads, n_kv, d, L, reps=20, warm_s=0.05):
     qb, kb, vbuf, ob = ctx.wrap_tensor(q), ctx.wrap_tensor(k), ctx.wrap_tensor(v), ctx.wrap_tensor(out)
     stream = torch.cuda.ExternalStream(ctx.stream)
     inv = 1.0 / np.sqrt(d)
+    # Warm-up in growing chunks, each timed with events, until warm_s of
+    # calls have run (at most 4000 calls).
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with ctx.segment() as seg:
-        e0.record(stream)
-        seg.attn_prefill(ob, qb, kb, vbuf, 0, L, 0, vb.NO_WINDOW, n_heads, n_kv, d, inv, vb.BF16)
-        e1.record(stream)
-    ctx.wait_idle()
-    torch.cuda.synchronize()
-    warmup = min(4000, max(2, int(warm_s / max(e0.elapsed_time(e1) * 1e-3, 1e-6))))
-    with ctx.segment() as seg:
-        for _ in range(warmup):
-            seg.attn_prefill(ob, qb, kb, vbuf, 0, L, 0, vb.NO_WINDOW, n_heads, n_kv, d, inv, vb.BF16)
-    ctx.wait_idle()
+    warmup, spent, chunk = 0, 0.0, 1
+    while spent < warm_s and warmup < 4000:
+        with ctx.segment() as seg:
+            e0.record(stream)
+            for _ in range(chunk):
+                seg.attn_prefill(ob, qb, kb, vbuf, 0, L, 0, vb.NO_WINDOW, n_heads, n_kv, d, inv, vb.BF16)
+            e1.record(stream)
+        ctx.wait_idle()
+        torch.cuda.synchronize()
+        spent += e0.elapsed_time(e1) * 1e-3
+        warmup += chunk
+        chunk = min(2 * chunk, 256)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
     with ctx.segment() as seg:
         for e0, e1 in ev:
