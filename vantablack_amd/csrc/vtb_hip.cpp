@@ -293,6 +293,18 @@ int plan_decode(VtbHipCtx* ctx, size_t n_q, size_t units, size_t head_dim, long 
   const long long want = decode_target_splits(ctx, n_q, units);
   long long rps = (Lmax + want - 1) / want;
   rps = std::max(quantum, (rps + quantum - 1) / quantum * quantum);
+  // Short ranges: a single query whose plan has more splits than the
+  // kernel's flat merge takes (decode_merge_flat; more would need the merge
+  // launch) gets that many splits instead, when each then holds at most
+  // kDecodeShortSplitRows rows: the second launch costs more than the
+  // longer splits.  C1 (512 rows, 4 KV heads, f32 d64): 64 splits of 8 rows
+  // and the merge launch 9.2 us, 32 splits of 16 rows 7.95 us.
+  constexpr long long kDecodeShortSplitRows = 32;
+  const long long flat = vtb::decode_merge_flat(G * HG * (int)head_dim);
+  if (n_q == 1 && (Lmax + rps - 1) / rps > flat) {
+    const long long r = ((Lmax + flat - 1) / flat + quantum - 1) / quantum * quantum;
+    if (r <= kDecodeShortSplitRows) rps = r;
+  }
   const long long n_splits = (Lmax + rps - 1) / rps;
   if (n_splits > 65535) return set_err(ctx, VTB_HIP_EUNSUPPORTED, "too many splits");
   p->rps = rps;
