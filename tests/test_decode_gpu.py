@@ -260,3 +260,30 @@ def test_merge_launch_matches_in_kernel_merge(ctx, orc, monkeypatch, n_heads, n_
         check(orc, outs[0], ref, n_heads, dtype, what=f"merge launch={mode} h{n_heads}/{n_kv} d{d} L{pos + 1}")
         got[mode] = outs[0]
     assert rel_err(got["1"], got["0"], n_heads) <= 2e-6
+
+
+@pytest.mark.parametrize("pos", [1023, 1024])
+def test_short_range_plan_boundary(ctx, orc, monkeypatch, pos):
+    """C1's head shape (32/4 heads, f32, d64) at 256 workgroups: 1024 rows
+    plan 32 splits of 32 rows with the flat in-kernel merge (the short-range
+    rule), 1025 rows 52 splits of 20 rows and the merge launch.  Both against
+    the oracle, each bit-identical when repeated."""
+    import vantablack_amd as vb
+    n_heads, n_kv, d = 32, 4, 64
+    monkeypatch.setenv("VTB_DECODE_TARGET_WGS", "256")
+    ks, kx, vs, vx = make_kv(orc, pos + 1, n_kv, d, "f32", seed=pos % 97)
+    q = orc.normal(pos % 89 + 3, n_heads * d)
+    kb, vbuf, qb = ctx.to_device(ks), ctx.to_device(vs), ctx.to_device(q)
+    oc = orc.OracleKvCache(1, n_kv, d, pos + 1)
+    oc.layer_rows("k", 0)[:] = kx
+    oc.layer_rows("v", 0)[:] = vx
+    oc.pos = pos
+    ref = orc.cpu_attention(q, oc, orc.config(n_heads, n_kv, d, pos + 1), 0)
+    outs = []
+    for _ in range(2):
+        ob = ctx.alloc(n_heads * d * 4)
+        with ctx.segment() as seg:
+            seg.attn_decode(ob, qb, kb, 0, vbuf, 0, n_heads, n_kv, d, pos + 1, 1.0 / np.sqrt(d), vb.F32)
+        outs.append(ctx.download(ob, np.float32, n_heads * d))
+    assert np.array_equal(outs[0], outs[1])
+    check(orc, outs[0], ref, n_heads, "f32", what=f"short-range plan L{pos + 1}")
